@@ -1,0 +1,76 @@
+"""ctypes binding of libhx_exl3.so (the C ABI declared in include/hx/exl3.h).
+
+The library is the product path: nothing here falls back to another implementation.  When the
+shared object is missing the import of this module raises, naming the build command.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("HX_EXL3_LIB", _PKG / "libhx_exl3.so"))
+
+HX_ERR_INVALID = -1
+HX_ERR_WORKSPACE = -2
+HX_ERR_HIP = -3
+HX_ERR_UNSUPPORTED = -4
+HX_GEMM_PATH_MFMA = 1
+HX_GEMM_PATH_GEMV = 90
+
+
+class GroupWordsC(C.Structure):
+    _fields_ = [("trellis", C.c_void_p), ("suh", C.c_void_p), ("svh", C.c_void_p), ("mul1", C.c_int)]
+
+
+class ExpertTablesC(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "gate_trellis", "gate_suh", "gate_svh", "up_trellis", "up_suh", "up_svh",
+        "down_trellis", "down_suh", "down_svh", "gate_bits", "up_bits", "down_bits")]
+
+
+# name -> (restype, argtypes); the exported symbol set is exactly the declarations of exl3.h
+SIGNATURES: dict[str, tuple] = {
+    "hx_version": (C.c_char_p, []),
+    "hx_last_error": (C.c_char_p, []),
+    "hx_workspace_init": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p]),
+    "hx_exl3_gemm_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
+    "hx_exl3_gemm": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(GroupWordsC), C.c_int, C.c_int, C.c_int, C.c_int,
+                               C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_size_t]),
+    "hx_exl3_reconstruct_slice": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                            C.c_int, C.c_int64, C.c_void_p]),
+    "hx_had_r_128": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_float,
+                               C.c_void_p]),
+    "hx_routing_ds3_nogroup": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                         C.c_float, C.c_int, C.c_int, C.c_void_p]),
+    "hx_moe_permute": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                 C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "hx_moe_reduce_sorted": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "hx_swiglu_clamp": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_float, C.c_void_p]),
+}
+
+
+def _load() -> C.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is not built; run `python -m helios_glm53flash_amd.build` (hipcc, gfx950)")
+    lib = C.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+class HxError(RuntimeError):
+    pass
+
+
+def check(code: int, what: str) -> int:
+    if code < 0:
+        raise HxError(f"{what} failed ({code}): {lib.hx_last_error().decode()}")
+    return code

@@ -1,0 +1,152 @@
+// hx_device.hpp -- gfx950 device primitives for the EXL3 trellis path.
+//
+// Trellis format (reference src/cuda/quant/exl3_gemm.cuh:17-29, pack.cu:6-54):
+//   a K x N weight is (K/16) x (N/16) tiles of 16x16; tile (tk, tn) is 8*bits little-endian
+//   uint32 words at word offset (tk * (N/16) + tn) * 8 * bits.  Stream bit b of a tile is bit
+//   31 - (b % 32) of word b / 32.  Position p (0..255) decodes the 16-bit window made of stream
+//   bits [(p+1)*bits - 16, (p+1)*bits) (cyclic), read MSB first (exl3_dq.cuh:17-32).
+//   Position p holds weight (k, n) of the tile with l = p/8, j = p%8:
+//     k = 2*(l%4) + (j&1) + 8*((j>>1)&1),  n = 8*(j>>2) + l/4        (reconstruct.cu:36-81)
+//   so positions p (even) and p+1 are the k-adjacent pair (k, k+1) of one column n.
+//
+// Everything here is written for 64-lane wavefronts.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 hx_h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 hx_h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 hx_h8 __attribute__((ext_vector_type(8)));
+typedef float hx_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t hx_u4 __attribute__((ext_vector_type(4)));
+typedef float hx_f16v __attribute__((ext_vector_type(16)));
+
+#define HX_INLINE __device__ __forceinline__
+
+static constexpr float HX_RSQRT128 = 0.088388347648f;
+
+HX_INLINE hx_h2 u32_as_h2(uint32_t u) { return __builtin_bit_cast(hx_h2, u); }
+HX_INLINE uint32_t h2_as_u32(hx_h2 h) { return __builtin_bit_cast(uint32_t, h); }
+HX_INLINE _Float16 u16_as_h(uint16_t u) { return __builtin_bit_cast(_Float16, u); }
+HX_INLINE uint16_t h_as_u16(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
+
+// ------------------------------------------------------------------ window extraction
+
+// Window of position P from the tile's words held in registers.  P is a compile-time constant in
+// every caller (fully unrolled loops), so each window folds to one v_alignbit_b32 or v_bfe_u32.
+template <int BITS, int P>
+HX_INLINE uint32_t hx_window(const uint32_t* w)
+{
+    constexpr int total = 256 * BITS;
+    constexpr int nw = 8 * BITS;
+    constexpr int s = (((P + 1) * BITS - 16) % total + total) % total;  // first stream bit
+    constexpr int wi = s >> 5;
+    constexpr int off = s & 31;
+    if constexpr (off <= 16) {
+        return (w[wi] >> (16 - off)) & 0xffffu;
+    } else {
+        // bits from the low (32-off) bits of w[wi] followed by the top bits of w[wi+1]
+        return __builtin_amdgcn_alignbit(w[wi], w[(wi + 1) % nw], 48 - off) & 0xffffu;
+    }
+}
+
+// ------------------------------------------------------------------ codebooks
+
+// Two decoded weights (windows w0 -> low half, w1 -> high half) as fp16x2.
+// codebook.cuh:57-124.  cb2: x = w * 0x83DCD12D; h = fp16(0x6400 + bytesum(x)) = 1024 + s exactly;
+// v = fma(h, 0x1eee, 0xc931) in fp16 (v_pk_fma_f16 is one rounding of the exact value, as hfma).
+// cb0/cb1: x = w*a (+b); x = (x & 0x8fff8fff) ^ 0x3b603b60; v = lo16 + hi16 in fp16.
+template <int CB>
+HX_INLINE hx_h2 hx_decode2(uint32_t w0, uint32_t w1)
+{
+    if constexpr (CB == 2) {
+        uint32_t x0 = w0 * 0x83DCD12Du;
+        uint32_t x1 = w1 * 0x83DCD12Du;
+        uint32_t s0 = __builtin_amdgcn_udot4(x0, 0x01010101u, 0x6400u, false);
+        uint32_t s1 = __builtin_amdgcn_udot4(x1, 0x01010101u, 0x6400u, false);
+        hx_h2 h = u32_as_h2((s1 << 16) | s0);
+        const hx_h2 c1 = u32_as_h2(0x1eee1eeeu);
+        const hx_h2 c0 = u32_as_h2(0xc931c931u);
+        return __builtin_elementwise_fma(h, c1, c0);
+    } else {
+        uint32_t x0, x1;
+        if constexpr (CB == 1) {
+            x0 = w0 * 0xCBAC1FEDu;
+            x1 = w1 * 0xCBAC1FEDu;
+        } else {
+            x0 = w0 * 89226354u + 64248484u;
+            x1 = w1 * 89226354u + 64248484u;
+        }
+        x0 = (x0 & 0x8fff8fffu) ^ 0x3b603b60u;
+        x1 = (x1 & 0x8fff8fffu) ^ 0x3b603b60u;
+        uint32_t lo = __builtin_amdgcn_perm(x1, x0, 0x05040100u);  // (x0.lo, x1.lo)
+        uint32_t hi = __builtin_amdgcn_perm(x1, x0, 0x07060302u);  // (x0.hi, x1.hi)
+        return u32_as_h2(lo) + u32_as_h2(hi);
+    }
+}
+
+template <int CB>
+HX_INLINE _Float16 hx_decode1(uint32_t w)
+{
+    hx_h2 v = hx_decode2<CB>(w, w);
+    return v.x;
+}
+
+// Position pair (P, P+1), P even -> column n and k-pair index kp (the pair covers k = 2*kp, 2*kp+1).
+template <int P> struct hx_pos {
+    static constexpr int l = P >> 3, j = P & 7;
+    static constexpr int k = 2 * (l & 3) + (j & 1) + 8 * ((j >> 1) & 1);
+    static constexpr int n = 8 * (j >> 2) + (l >> 2);
+    static constexpr int kp = k >> 1;
+};
+
+// Inverse map (k, n) -> position.
+HX_INLINE int hx_kn_to_pos(int k, int n)
+{
+    int l = 4 * (n & 7) + ((k >> 1) & 3);
+    int j = (k & 1) + 2 * (k >> 3) + 4 * (n >> 3);
+    return 8 * l + j;
+}
+
+// ------------------------------------------------------------------ wave-level Hadamard-128
+
+// 128-point Sylvester transform of one vector held as 2 values per lane (elements 2*lane,
+// 2*lane+1) across a 64-lane wave; scaled by 1/sqrt(128).
+HX_INLINE void hx_had128_wave(float& v0, float& v1)
+{
+    const int lane = threadIdx.x & 63;
+    float a = v0 + v1, b = v0 - v1;
+    v0 = a;
+    v1 = b;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        float p0 = __shfl_xor(v0, m, 64);
+        float p1 = __shfl_xor(v1, m, 64);
+        bool upper = (lane & m) != 0;
+        v0 = upper ? p0 - v0 : v0 + p0;
+        v1 = upper ? p1 - v1 : v1 + p1;
+    }
+    v0 *= HX_RSQRT128;
+    v1 *= HX_RSQRT128;
+}
+
+// ------------------------------------------------------------------ cross-agent handoff
+
+HX_INLINE int hx_atomic_add_acqrel(int* p, int v)
+{
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+HX_INLINE void hx_atomic_store_relaxed(int* p, int v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// fp32 SiLU in the fp16 chain order of hadamard_inner.cuh:331-340 (exp, 1+e, rcp, mul), each
+// step rounded to fp16 as the reference's half2 ops are.
+HX_INLINE _Float16 hx_silu_h(_Float16 g)
+{
+    _Float16 e = (_Float16)__expf(-(float)g);
+    _Float16 s = (_Float16)(1.0f + (float)e);
+    _Float16 r = (_Float16)(1.0f / (float)s);
+    return (_Float16)((float)g * (float)r);
+}

@@ -1,0 +1,34 @@
+// hx_kernels.hpp -- host-side launchers shared by the kernel translation units and the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace hx {
+
+// small-M linear (hx_linear.hip)
+void gemv_plan(int M, int K, int N, int* splits, int* kc);
+size_t gemv_workspace_bytes(int M, int K, int N);
+hipError_t launch_linear_gemv(const _Float16* x, const uint16_t* trellis, const _Float16* suh, const _Float16* svh,
+                              void* y, int M, int K, int N, int bits, int cb, bool y_fp32, void* ws, hipStream_t st);
+
+// large-M linear on MFMA (hx_gemm.hip)
+hipError_t launch_input_had(const _Float16* x, const _Float16* suh, _Float16* a, long rows, int K, hipStream_t st);
+hipError_t launch_linear_mfma(const _Float16* a_had, const uint16_t* trellis, const _Float16* svh, void* y,
+                              int M, int K, int N, int bits, int cb, bool y_fp32, hipStream_t st);
+
+// utilities (hx_misc.hip)
+hipError_t launch_reconstruct(_Float16* out, const uint16_t* packed, int packed_rows, int packed_cols,
+                              int unpacked_cols, int bits, int cb, long n_offset, hipStream_t st);
+hipError_t launch_had_r_128(const _Float16* in, _Float16* out, const _Float16* pre, const _Float16* post,
+                            long rows, int cols, float r_scale, hipStream_t st);
+hipError_t launch_routing(const _Float16* scores, const _Float16* bias, int64_t* idx, _Float16* w, int bsz, int E,
+                          int K, float scale, hipStream_t st);
+hipError_t launch_permute(const int64_t* ids, const _Float16* w, int M, int topk, int E, int64_t* expert_count,
+                          int64_t* token_sorted, _Float16* weight_sorted, int64_t* route_to_sorted,
+                          int64_t* workspace, hipStream_t st);
+hipError_t launch_reduce_sorted(float* y, const float* contrib, const int64_t* route_to_sorted, int M, int topk,
+                                int hidden, hipStream_t st);
+hipError_t launch_swiglu_clamp(const float* g, const float* u, _Float16* out, size_t n, float limit, hipStream_t st);
+
+}  // namespace hx

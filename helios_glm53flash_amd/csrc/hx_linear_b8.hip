@@ -1,0 +1,6 @@
+// Instantiation of the small-M linear kernels for 8-bit trellis.
+#include "hx_linear_impl.hpp"
+
+namespace hx {
+template hipError_t launch_gemv_cb<8>(int, const GemvArgs&, const _Float16*, void*, bool, hipStream_t);
+}  // namespace hx

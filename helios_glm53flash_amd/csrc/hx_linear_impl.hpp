@@ -1,0 +1,82 @@
+#pragma once
+// hx_linear_impl.hpp -- EXL3 quantized linear y = svh . H_N(H_K(x . suh) . W_hat) on gfx950,
+// small-M path (M <= 8): fused trellis decode + GEMV + split-K + output Hadamard epilogue in one
+// launch.  Reference semantics: src/cuda/quant/exl3_gemv_kernel.cuh:138-402 and
+// exl3_gemm_kernel.cuh:8-80 (input transform, GEMM, output transform + svh).
+#include "hx_gemv.hpp"
+#include "hx_kernels.hpp"
+
+namespace hx {
+
+// Output epilogue for one 128-column group: y[m][cg*128 + c] = svh . H128(colsum[m][:])
+//   fp32 out: had_ff_r_128_inner<false,true> (transform in fp32, times float(svh))
+//   fp16 out: had_fh_r_128_inner<false,true> (transform, round to fp16, fp16 multiply by svh)
+template <int MT>
+__device__ void linear_epilogue(const float* colsum, const _Float16* svh, void* y, int M, int N,
+                                int cg, bool y_fp32)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = cg * 128 + 2 * lane;
+    hx_h2 sv = *reinterpret_cast<const hx_h2*>(svh + c);
+    for (int m = wave; m < M && m < MT; m += GEMV_WAVES) {
+        float v0 = colsum[m * 128 + 2 * lane], v1 = colsum[m * 128 + 2 * lane + 1];
+        hx_had128_wave(v0, v1);
+        if (y_fp32) {
+            float2 o = make_float2(v0 * (float)sv.x, v1 * (float)sv.y);
+            *reinterpret_cast<float2*>(static_cast<float*>(y) + (size_t)m * N + c) = o;
+        } else {
+            hx_h2 h = {(_Float16)v0, (_Float16)v1};
+            h = h * sv;
+            *reinterpret_cast<hx_h2*>(static_cast<_Float16*>(y) + (size_t)m * N + c) = h;
+        }
+    }
+}
+
+template <int BITS, int CB, int MT>
+__global__ __launch_bounds__(GEMV_THREADS) void linear_gemv_kernel(GemvArgs g, const _Float16* svh, void* y,
+                                                                  bool y_fp32)
+{
+    extern __shared__ uint32_t a_lds[];
+    __shared__ float red[GEMV_WAVES * MT * 128];
+    __shared__ float colsum[MT * 128];
+    const int groups = g.N >> 7;
+    const int cg = blockIdx.x % groups;
+    const int s = blockIdx.x / groups;
+    gemv_split_sum<BITS, CB, MT>(g, cg, s, a_lds, red, colsum);
+    if (g.splits > 1) {
+        publish_partial<MT>(g.partial, g.M, g.N, cg, s, colsum);
+        if (!arrive_last(&g.counter[cg], g.splits)) return;
+        gather_partials<MT>(g.partial, g.M, g.N, g.splits, cg, colsum);
+    }
+    linear_epilogue<MT>(colsum, svh, y, g.M, g.N, cg, y_fp32);
+}
+
+template <int BITS, int CB, int MT>
+hipError_t launch_gemv_t(const GemvArgs& g, const _Float16* svh, void* y, bool y_fp32, hipStream_t st)
+{
+    const int groups = g.N >> 7;
+    size_t lds = (size_t)MT * g.kc * sizeof(_Float16);
+    hipLaunchKernelGGL((linear_gemv_kernel<BITS, CB, MT>), dim3(groups * g.splits), dim3(GEMV_THREADS), lds, st,
+                       g, svh, y, y_fp32);
+    return hipGetLastError();
+}
+
+template <int BITS, int CB>
+hipError_t launch_gemv_b(const GemvArgs& g, const _Float16* svh, void* y, bool y_fp32, hipStream_t st)
+{
+    if (g.M <= 1) return launch_gemv_t<BITS, CB, 1>(g, svh, y, y_fp32, st);
+    if (g.M <= 4) return launch_gemv_t<BITS, CB, 4>(g, svh, y, y_fp32, st);
+    return launch_gemv_t<BITS, CB, 8>(g, svh, y, y_fp32, st);
+}
+
+template <int BITS>
+hipError_t launch_gemv_cb(int cb, const GemvArgs& g, const _Float16* svh, void* y, bool y_fp32, hipStream_t st)
+{
+    switch (cb) {
+        case 0: return launch_gemv_b<BITS, 0>(g, svh, y, y_fp32, st);
+        case 1: return launch_gemv_b<BITS, 1>(g, svh, y, y_fp32, st);
+        default: return launch_gemv_b<BITS, 2>(g, svh, y, y_fp32, st);
+    }
+}
+
+}  // namespace hx

@@ -1,0 +1,308 @@
+// hx_misc.hip -- trellis reconstruct, standalone Hadamard-128, sigmoid top-k router, deterministic
+// MoE permutation, ordered reduction and swiglu for gfx950.
+#include "hx_device.hpp"
+#include "hx_kernels.hpp"
+
+namespace hx {
+
+// ------------------------------------------------------------------ reconstruct
+
+HX_INLINE uint32_t window_rt(const uint32_t* w, int bits, int p)
+{
+    const int total = 256 * bits, nw = 8 * bits;
+    int s = (p + 1) * bits - 16;
+    if (s < 0) s += total;
+    const int wi = s >> 5, off = s & 31;
+    if (off <= 16) return (w[wi] >> (16 - off)) & 0xffffu;
+    int wj = wi + 1;
+    if (wj == nw) wj = 0;
+    return __builtin_amdgcn_alignbit(w[wi], w[wj], 48 - off) & 0xffffu;
+}
+
+// One workgroup per (tile row tk, 8 consecutive tile columns): thread t writes 8 consecutive
+// fp16 of row 16*tk + t/16.  Reference: reconstruct.cu:8-81 (same W_hat [K][N] row-major output).
+template <int CB>
+__global__ __launch_bounds__(256) void reconstruct_kernel(_Float16* out, const uint16_t* packed, int packed_cols,
+                                                          int packed_n_offset, int out_cols, int bits)
+{
+    __shared__ uint32_t words[8][64];
+    const int t = threadIdx.x;
+    const int tk = blockIdx.y;
+    const int tn0 = blockIdx.x * 8;  // first output tile column of this group
+    const int nw = 8 * bits;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(packed) +
+                          ((size_t)tk * packed_cols + packed_n_offset + tn0) * nw;
+    for (int i = t; i < 8 * nw; i += 256) words[i / nw][i % nw] = src[i];
+    __syncthreads();
+    const int k = t >> 4, c0 = (t & 15) * 8;
+    const int tile = c0 >> 4, n0 = c0 & 15;
+    hx_h8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = hx_decode1<CB>(window_rt(words[tile], bits, hx_kn_to_pos(k, n0 + i)));
+    *reinterpret_cast<hx_h8*>(out + (size_t)(16 * tk + k) * out_cols + tn0 * 16 + c0) = v;
+}
+
+hipError_t launch_reconstruct(_Float16* out, const uint16_t* packed, int packed_rows, int packed_cols,
+                              int unpacked_cols, int bits, int cb, long n_offset, hipStream_t st)
+{
+    if (bits < 1 || bits > 8 || unpacked_cols % 128 || n_offset % 128 || n_offset < 0 ||
+        n_offset + unpacked_cols > (long)packed_cols * 16)
+        return hipErrorInvalidValue;
+    if (unpacked_cols == 0 || packed_rows == 0) return hipSuccess;
+    dim3 grid(unpacked_cols / 128, packed_rows);
+    const int off = (int)(n_offset / 16);
+    switch (cb) {
+        case 0: hipLaunchKernelGGL(reconstruct_kernel<0>, grid, dim3(256), 0, st, out, packed, packed_cols, off, unpacked_cols, bits); break;
+        case 1: hipLaunchKernelGGL(reconstruct_kernel<1>, grid, dim3(256), 0, st, out, packed, packed_cols, off, unpacked_cols, bits); break;
+        default: hipLaunchKernelGGL(reconstruct_kernel<2>, grid, dim3(256), 0, st, out, packed, packed_cols, off, unpacked_cols, bits); break;
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ had_r_128
+
+// Row-wise Hadamard-128 with optional fp16 pre/post scales (reference hadamard.cu had_r_128:
+// pre-scale by fp16 multiply, transform in fp32, times r_scale, round to fp16, post-scale by
+// fp16 multiply).  One wave per 128-element block.
+__global__ __launch_bounds__(256) void had_r_128_kernel(const _Float16* in, _Float16* out, const _Float16* pre,
+                                                        const _Float16* post, long blocks, int cols, float r_scale)
+{
+    const int lane = threadIdx.x & 63;
+    const long b = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= blocks) return;
+    const long row = b / (cols / 128);
+    const int c = (int)(b % (cols / 128)) * 128 + 2 * lane;
+    hx_h2 v = *reinterpret_cast<const hx_h2*>(in + row * cols + c);
+    if (pre) v = v * *reinterpret_cast<const hx_h2*>(pre + c);
+    float v0 = (float)v.x, v1 = (float)v.y;
+    hx_had128_wave(v0, v1);
+    const float rs = r_scale / HX_RSQRT128;  // hx_had128_wave already applied 1/sqrt(128)
+    hx_h2 o = {(_Float16)(v0 * rs), (_Float16)(v1 * rs)};
+    if (post) o = o * *reinterpret_cast<const hx_h2*>(post + c);
+    *reinterpret_cast<hx_h2*>(out + row * cols + c) = o;
+}
+
+hipError_t launch_had_r_128(const _Float16* in, _Float16* out, const _Float16* pre, const _Float16* post,
+                            long rows, int cols, float r_scale, hipStream_t st)
+{
+    if (cols % 128) return hipErrorInvalidValue;
+    long blocks = rows * (cols / 128);
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(had_r_128_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, st, in, out, pre, post,
+                       blocks, cols, r_scale);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ router
+
+// Sigmoid top-k (reference routing.cu:211-329, ROUTING_ACT_SIGMOID).  One wave per token.
+// Selection key without bias is the fp16 logit, with bias sigmoid(logit) + bias.  Order: larger
+// key first using the monotone unsigned encoding of the fp32 key (so +0 ranks above -0), ties to
+// the lower expert index.  Weights: sigmoid(logit) (no bias) or the selected payload, normalised
+// as o * scale / (sum o + 1e-20), rounded to fp16.
+HX_INLINE float sigmoid_stable(float x)
+{
+    float ez = __expf(-fabsf(x));
+    float base = ez / (1.0f + ez);
+    return x >= 0.0f ? 1.0f - base : base;
+}
+
+__global__ __launch_bounds__(64) void routing_topk_kernel(const _Float16* scores, const _Float16* bias, int64_t* idx,
+                                                          _Float16* w, int E, int K, float scale)
+{
+    const int lane = threadIdx.x;
+    const int row = blockIdx.x;
+    scores += (size_t)row * E;
+    constexpr int PER = 8;  // E <= 512
+    uint64_t cand[PER];
+    float payload[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = lane + 64 * i;
+        cand[i] = 0;
+        payload[i] = 0.0f;
+        if (e < E) {
+            float logit = (float)scores[e];
+            float key = logit;
+            payload[i] = logit;
+            if (bias) {
+                payload[i] = sigmoid_stable(logit);
+                key = payload[i] + (float)bias[e];
+            }
+            uint32_t u = __float_as_uint(key);
+            u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+            // larger is better: key high, lower index wins ties; +1 keeps valid candidates nonzero
+            cand[i] = ((uint64_t)u << 32) | (uint64_t)(0xfffffu - (uint32_t)e + 1u);
+        }
+    }
+    float o_sel = 0.0f;
+    int e_sel = 0;
+    float sum = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        uint64_t best = 0;
+        float best_p = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (cand[i] > best) { best = cand[i]; best_p = payload[i]; }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            uint64_t ob = __shfl_xor(best, m, 64);
+            float op = __shfl_xor(best_p, m, 64);
+            if (ob > best) { best = ob; best_p = op; }
+        }
+        const int e = (int)(0xfffffu + 1u - (uint32_t)(best & 0xffffffffu));
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (cand[i] == best) cand[i] = 0;
+        const float o = bias ? best_p : sigmoid_stable(best_p);
+        sum += o;
+        if (lane == k) { o_sel = o; e_sel = e; }
+    }
+    sum += 1e-20f;
+    if (lane < K) {
+        idx[(size_t)row * K + lane] = e_sel;
+        w[(size_t)row * K + lane] = (_Float16)(o_sel * scale / sum);
+    }
+}
+
+hipError_t launch_routing(const _Float16* scores, const _Float16* bias, int64_t* idx, _Float16* w, int bsz, int E,
+                          int K, float scale, hipStream_t st)
+{
+    if (E > 512 || K > 64 || K > E || K < 1) return hipErrorInvalidValue;
+    if (bsz == 0) return hipSuccess;
+    hipLaunchKernelGGL(routing_topk_kernel, dim3(bsz), dim3(64), 0, st, scores, bias, idx, w, E, K, scale);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ permutation
+
+// Deterministic counting sort of routing slots by expert (reference glue2.cu:244-293 computes the
+// same expert_count / token_sorted / weight_sorted / route_to_sorted, but places slots within an
+// expert with an atomic cursor).  Here slot i of expert e lands at offset[e] + (number of slots
+// i' < i with ids[i'] == e): ascending flat index within each expert.  One 1024-lane workgroup;
+// chunks of 1024 slots are ranked wave by wave in order.
+constexpr int PERM_THREADS = 1024;
+constexpr int PERM_EMAX = 512;
+
+__global__ __launch_bounds__(PERM_THREADS) void permute_kernel(const int64_t* ids, const _Float16* w, int total,
+                                                               int topk, int E, int64_t* expert_count,
+                                                               int64_t* token_sorted, _Float16* weight_sorted,
+                                                               int64_t* route_to_sorted)
+{
+    __shared__ int cnt[PERM_EMAX];
+    __shared__ int cursor[PERM_EMAX];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    for (int e = t; e < PERM_EMAX; e += PERM_THREADS) cnt[e] = 0;
+    __syncthreads();
+    for (int i = t; i < total; i += PERM_THREADS) {
+        const int64_t e = ids[i];
+        if (e >= 0 && e < E) atomicAdd(&cnt[(int)e], 1);
+    }
+    __syncthreads();
+    if (t == 0) {
+        int acc = 0;
+        for (int e = 0; e < E; ++e) {
+            cursor[e] = acc;
+            acc += cnt[e];
+        }
+    }
+    __syncthreads();
+    for (int e = t; e <= E; e += PERM_THREADS) expert_count[e] = e < E ? cnt[e] : 0;
+
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int base = 0; base < total; base += PERM_THREADS) {
+        const int i = base + t;
+        const int64_t e64 = i < total ? ids[i] : -1;
+        const bool valid = e64 >= 0 && e64 < E;
+        const int e = valid ? (int)e64 : -1;
+        int rank = 0, group = 0;
+        bool leader = false;
+        uint64_t remaining = __ballot(valid);
+        while (remaining) {
+            const int ld = __ffsll((unsigned long long)remaining) - 1;
+            const int le = __shfl(e, ld, 64);
+            const uint64_t m = __ballot(valid && e == le);
+            if (valid && e == le) {
+                rank = __popcll(m & lt_mask);
+                group = __popcll(m);
+                leader = (lane == ld);
+            }
+            remaining &= ~m;
+        }
+        for (int wv = 0; wv < PERM_THREADS / 64; ++wv) {
+            if (wave == wv && valid) {
+                const int pos = cursor[e] + rank;
+                __builtin_amdgcn_wave_barrier();
+                if (leader) cursor[e] += group;
+                token_sorted[pos] = i / topk;
+                weight_sorted[pos] = w[i];
+                if (route_to_sorted) route_to_sorted[i] = pos;
+            }
+            __syncthreads();
+        }
+    }
+}
+
+hipError_t launch_permute(const int64_t* ids, const _Float16* w, int M, int topk, int E, int64_t* expert_count,
+                          int64_t* token_sorted, _Float16* weight_sorted, int64_t* route_to_sorted,
+                          int64_t* workspace, hipStream_t st)
+{
+    (void)workspace;
+    if (E > PERM_EMAX || E < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(PERM_THREADS), 0, st, ids, w, M * topk, topk, E, expert_count,
+                       token_sorted, weight_sorted, route_to_sorted);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ ordered reduction / swiglu
+
+// y[t][c] = sum_j contrib[route_to_sorted[t*topk + j]][c], ascending j, from +0 (glue2.cu:297-306).
+__global__ __launch_bounds__(256) void reduce_sorted_kernel(float* y, const float* contrib, const int64_t* r2s, int M,
+                                                            int topk, int hidden)
+{
+    const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t total4 = (size_t)M * hidden / 4;
+    if (i4 >= total4) return;
+    const int t = (int)(i4 * 4 / hidden);
+    const int c = (int)(i4 * 4 % hidden);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < topk; ++j) {
+        const float4 v = *reinterpret_cast<const float4*>(contrib + (size_t)r2s[(size_t)t * topk + j] * hidden + c);
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+    }
+    *reinterpret_cast<float4*>(y + i4 * 4) = acc;
+}
+
+hipError_t launch_reduce_sorted(float* y, const float* contrib, const int64_t* route_to_sorted, int M, int topk,
+                                int hidden, hipStream_t st)
+{
+    if (hidden % 4) return hipErrorInvalidValue;
+    size_t total4 = (size_t)M * hidden / 4;
+    if (total4 == 0) return hipSuccess;
+    hipLaunchKernelGGL(reduce_sorted_kernel, dim3((unsigned)((total4 + 255) / 256)), dim3(256), 0, st, y, contrib,
+                       route_to_sorted, M, topk, hidden);
+    return hipGetLastError();
+}
+
+// out = fp16(silu(min(g, L)) * clamp(u, -L, L))  (glue2.cu:406-414)
+__global__ __launch_bounds__(256) void swiglu_clamp_kernel(const float* g, const float* u, _Float16* out, size_t n,
+                                                           float limit)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float gv = fminf(g[i], limit);
+    const float uv = fminf(fmaxf(u[i], -limit), limit);
+    out[i] = (_Float16)(gv / (1.0f + __expf(-gv)) * uv);
+}
+
+hipError_t launch_swiglu_clamp(const float* g, const float* u, _Float16* out, size_t n, float limit, hipStream_t st)
+{
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(swiglu_clamp_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, out, n, limit);
+    return hipGetLastError();
+}
+
+}  // namespace hx

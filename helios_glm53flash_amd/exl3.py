@@ -1,0 +1,186 @@
+"""Python mirror of the reference's EXL3 / router / MoE-glue entry points over libhx_exl3.so.
+
+Same names, argument meaning and order as the reference C++ interfaces
+(src/cuda/quant/exl3_gemm.cuh:51-83, reconstruct.cuh:15-63, hadamard.cuh:14-43,
+src/cuda/aux/routing.cuh:36-49, src/engine/glue2.cuh:44-64, src/cuda/quant/exl3_moe.cuh:74-105).
+Buffers are torch tensors on the current HIP device (torch only provides device memory and the
+stream; all compute runs in the HIP kernels).  Where the reference aborts, these raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from ._lib import GroupWordsC, HX_GEMM_PATH_GEMV, HX_GEMM_PATH_MFMA, HxError, check, lib
+
+MUL1 = 0x83DCD12D
+MUL1_I32 = MUL1 - (1 << 32)  # the int32 value stored in checkpoints
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _need(t: torch.Tensor, name: str, dtypes: tuple) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a device tensor (got {t.device})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.dtype not in dtypes:
+        raise ValueError(f"{name} has dtype {t.dtype}, expected one of {dtypes}")
+
+
+_workspaces: dict[int, torch.Tensor] = {}
+
+
+def workspace(nbytes: int, device: Optional[torch.device] = None) -> torch.Tensor:
+    """Per-device zero-initialised workspace, grown on demand (counters inside stay zero between
+    calls because every kernel resets what it uses)."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _workspaces.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _workspaces[idx] = ws
+    return ws
+
+
+@dataclass
+class GroupWords:
+    """One EXL3 linear (reference GroupWords, exl3_gemm.cuh:30-36): trellis (K/16, N/16, 16*bits)
+    int16/uint16, suh fp16 [K], svh fp16 [N], mul1 (nonzero selects codebook 2)."""
+    trellis: torch.Tensor
+    suh: torch.Tensor
+    svh: torch.Tensor
+    mul1: int = 0
+
+    @property
+    def bits(self) -> int:
+        return self.trellis.shape[-1] // 16
+
+    @property
+    def in_features(self) -> int:
+        return self.suh.numel()
+
+    @property
+    def out_features(self) -> int:
+        return self.svh.numel()
+
+    def c(self) -> GroupWordsC:
+        m = self.mul1
+        if m and m > 0x7FFFFFFF:
+            m -= 1 << 32
+        return GroupWordsC(self.trellis.data_ptr(), self.suh.data_ptr(), self.svh.data_ptr(), m)
+
+
+def gemm(y: torch.Tensor, x: torch.Tensor, w: GroupWords, M: int, N: int, K: int, bits: int, y_fp32: bool = False,
+         stream=None, a_had: Optional[torch.Tensor] = None, mcg: bool = False) -> int:
+    """y = svh . H_N(H_K(x . suh) . W_hat).  Returns 90 when the small-M GEMV ran, 1 for MFMA."""
+    _need(x, "x", (torch.float16,))
+    _need(y, "y", (torch.float32,) if y_fp32 else (torch.float16,))
+    for t, n in ((w.trellis, "trellis"), (w.suh, "suh"), (w.svh, "svh")):
+        _need(t, n, (torch.int16, torch.uint16, torch.float16))
+    if x.numel() < M * K or y.numel() < M * N:
+        raise ValueError("x / y smaller than M*K / M*N")
+    if w.trellis.numel() != (K // 16) * (N // 16) * 16 * bits or w.suh.numel() < K or w.svh.numel() < N:
+        raise ValueError("GroupWords shapes do not match K, N, bits")
+    if a_had is not None:
+        _need(a_had, "a_had", (torch.float16,))
+    nbytes = lib.hx_exl3_gemm_workspace_size(M, N, K)
+    ws = workspace(nbytes, x.device) if (M <= 8 or a_had is None) else None
+    gw = w.c()
+    return check(lib.hx_exl3_gemm(y.data_ptr(), x.data_ptr(), C.byref(gw), M, N, K, bits, int(y_fp32),
+                                  _stream(stream), _ptr(a_had), int(mcg), _ptr(ws), ws.numel() if ws is not None else 0),
+                 "hx_exl3_gemm")
+
+
+def gemv(y, x, w: GroupWords, M, N, K, bits, y_fp32=False, stream=None, a_had=None, mcg=False) -> None:
+    """Forced small-M path (reference gemv, exl3_gemm.cuh:70-83); M must be <= 8."""
+    if M > 8:
+        raise ValueError("gemv requires M <= 8")
+    gemm(y, x, w, M, N, K, bits, y_fp32, stream, a_had, mcg)
+
+
+def reconstruct_slice(unpacked: torch.Tensor, packed: torch.Tensor, packed_rows: int, packed_cols: int,
+                      unpacked_cols: int, K: int, mcg: bool, mul1: bool, n_offset: int, stream=None) -> None:
+    """Bit-exact trellis -> W_hat fp16 (reference reconstruct_slice, reconstruct.cuh:15-35)."""
+    _need(unpacked, "unpacked", (torch.float16, torch.int16, torch.uint16))
+    _need(packed, "packed", (torch.int16, torch.uint16))
+    check(lib.hx_exl3_reconstruct_slice(unpacked.data_ptr(), packed.data_ptr(), packed_rows, packed_cols,
+                                        unpacked_cols, K, int(mcg), int(bool(mul1)), n_offset, _stream(stream)),
+          "hx_exl3_reconstruct_slice")
+
+
+def reconstruct(unpacked, packed, packed_rows, packed_cols, unpacked_cols, K, mcg, mul1, stream=None) -> None:
+    """Full-width reconstruct (reference reconstruct.cuh:38-48)."""
+    reconstruct_slice(unpacked, packed, packed_rows, packed_cols, unpacked_cols, K, mcg, mul1, 0, stream)
+
+
+def had_r_128(input: torch.Tensor, output: torch.Tensor, pre_scale: Optional[torch.Tensor],
+              post_scale: Optional[torch.Tensor], rows: int, cols: int, r_scale: float = 0.088388347648,
+              stream=None) -> None:
+    _need(input, "input", (torch.float16,))
+    _need(output, "output", (torch.float16,))
+    check(lib.hx_had_r_128(input.data_ptr(), output.data_ptr(), _ptr(pre_scale), _ptr(post_scale), rows, cols,
+                           r_scale, _stream(stream)), "hx_had_r_128")
+
+
+def routing_ds3_nogroup(scores: torch.Tensor, bias: Optional[torch.Tensor], topk_indices: torch.Tensor,
+                        topk_weights: torch.Tensor, bsz: int, num_experts: int, K: int, scaling_factor: float,
+                        use_topk: bool = True, act_fn: int = 0, stream=None) -> None:
+    _need(scores, "scores", (torch.float16,))
+    _need(topk_indices, "topk_indices", (torch.int64,))
+    _need(topk_weights, "topk_weights", (torch.float16,))
+    check(lib.hx_routing_ds3_nogroup(scores.data_ptr(), _ptr(bias), topk_indices.data_ptr(), topk_weights.data_ptr(),
+                                     bsz, num_experts, K, scaling_factor, int(use_topk), act_fn, _stream(stream)),
+          "hx_routing_ds3_nogroup")
+
+
+def moe_permute(ids: torch.Tensor, weights: torch.Tensor, M: int, topk: int, E: int, expert_count: torch.Tensor,
+                token_sorted: torch.Tensor, weight_sorted: torch.Tensor, workspace: Optional[torch.Tensor] = None,
+                stream=None, route_to_sorted: Optional[torch.Tensor] = None) -> None:
+    _need(ids, "ids", (torch.int64,))
+    _need(weights, "weights", (torch.float16,))
+    _need(expert_count, "expert_count", (torch.int64,))
+    _need(token_sorted, "token_sorted", (torch.int64,))
+    _need(weight_sorted, "weight_sorted", (torch.float16,))
+    if expert_count.numel() < E + 1 or token_sorted.numel() < M * topk or weight_sorted.numel() < M * topk:
+        raise ValueError("moe_permute output buffers too small")
+    check(lib.hx_moe_permute(ids.data_ptr(), weights.data_ptr(), M, topk, E, expert_count.data_ptr(),
+                             token_sorted.data_ptr(), weight_sorted.data_ptr(), _ptr(workspace), _stream(stream),
+                             _ptr(route_to_sorted)), "hx_moe_permute")
+
+
+def moe_reduce_sorted(y: torch.Tensor, contributions: torch.Tensor, route_to_sorted: torch.Tensor, M: int, topk: int,
+                      hidden: int, stream=None) -> None:
+    _need(y, "y", (torch.float32,))
+    _need(contributions, "contributions", (torch.float32,))
+    _need(route_to_sorted, "route_to_sorted", (torch.int64,))
+    check(lib.hx_moe_reduce_sorted(y.data_ptr(), contributions.data_ptr(), route_to_sorted.data_ptr(), M, topk, hidden,
+                                   _stream(stream)), "hx_moe_reduce_sorted")
+
+
+def swiglu_clamp(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor, n: int, limit: float, stream=None) -> None:
+    _need(gate, "gate", (torch.float32,))
+    _need(up, "up", (torch.float32,))
+    _need(out, "out", (torch.float16,))
+    check(lib.hx_swiglu_clamp(gate.data_ptr(), up.data_ptr(), out.data_ptr(), n, limit, _stream(stream)),
+          "hx_swiglu_clamp")
+
+
+__all__ = ["GroupWords", "gemm", "gemv", "reconstruct", "reconstruct_slice", "had_r_128", "routing_ds3_nogroup",
+           "moe_permute", "moe_reduce_sorted", "swiglu_clamp", "workspace", "MUL1", "HxError",
+           "HX_GEMM_PATH_GEMV", "HX_GEMM_PATH_MFMA"]

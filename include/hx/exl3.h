@@ -1,0 +1,126 @@
+/*
+ * hx/exl3.h -- C ABI of the MI355X (gfx950) EXL3 quantized expert-GEMM path (libhx_exl3.so).
+ *
+ * Every entry point replaces one reference interface (file:line in the reference repository,
+ * neron82/helios-glm53flash) with the same argument meaning; the differences are C linkage,
+ * POD descriptors, caller-owned workspaces with size queries, and int status codes instead of
+ * abort():
+ *   >= 0  success (hx_exl3_gemm returns which path ran, see below)
+ *   HX_ERR_INVALID     argument outside the supported domain (nothing was launched)
+ *   HX_ERR_WORKSPACE   workspace missing or smaller than the size query
+ *   HX_ERR_HIP         a HIP launch failed (hx_last_error() names it)
+ *   HX_ERR_UNSUPPORTED an option the reference has that this build does not implement
+ *
+ * Conventions: all data pointers are device pointers on the current HIP device; fp16 data is
+ * IEEE binary16; `stream` may be 0 (null stream).  Calls are asynchronous on `stream`.
+ * Workspaces: caller-owned device memory, zero-filled once before first use (hx_workspace_init
+ * or any zero fill); the kernels leave their counters at zero, so a workspace is reused without
+ * clearing.  Two calls in flight at once must not share a workspace.
+ */
+#ifndef HX_EXL3_H
+#define HX_EXL3_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hx_stream_t; /* == hipStream_t */
+
+#define HX_ERR_INVALID (-1)
+#define HX_ERR_WORKSPACE (-2)
+#define HX_ERR_HIP (-3)
+#define HX_ERR_UNSUPPORTED (-4)
+
+#define HX_GEMM_PATH_MFMA 1
+#define HX_GEMM_PATH_GEMV 90 /* same value the reference returns when its GEMV ran */
+
+/* One EXL3 linear W[out=N][in=K]: trellis uint16 (K/16, N/16, 16*bits), suh fp16 [K],
+ * svh fp16 [N], mul1 != 0 selects codebook 2 (mul1 must then be 0x83DCD12D).
+ * Replaces helios::exl3::GroupWords (src/cuda/quant/exl3_gemm.cuh:30-36). */
+typedef struct hx_group_words {
+    const void* trellis;
+    const void* suh;
+    const void* svh;
+    int mul1;
+} hx_group_words;
+
+/* Per-expert device pointer tables, each a device array of num_experts pointers, plus optional
+ * per-expert bit widths (device int32 arrays, or NULL to use the call's uniform widths).
+ * Replaces helios::exl3::ExpertTables (src/cuda/quant/exl3_moe.cuh:20-31); the bits arrays are
+ * an extension for layers that mix bit widths across experts. */
+typedef struct hx_expert_tables {
+    const void* const* gate_trellis;
+    const void* const* gate_suh;
+    const void* const* gate_svh;
+    const void* const* up_trellis;
+    const void* const* up_suh;
+    const void* const* up_svh;
+    const void* const* down_trellis;
+    const void* const* down_suh;
+    const void* const* down_svh;
+    const int32_t* gate_bits;
+    const int32_t* up_bits;
+    const int32_t* down_bits;
+} hx_expert_tables;
+
+/* ---- library ---------------------------------------------------------------------------- */
+const char* hx_version(void);
+const char* hx_last_error(void);
+int hx_workspace_init(void* workspace, size_t bytes, hx_stream_t stream);
+
+/* ---- quantized linear ------------------------------------------------------------------- */
+
+/* y[M][N] = svh . H_N( H_K(x . suh) . W_hat ), x fp16 [M][K], y fp32 (y_fp32) or fp16.
+ * Replaces helios::exl3::gemm (src/cuda/quant/exl3_gemm.cuh:51-66, exl3_gemm.cu:81-243).
+ * M <= 8 runs the fused decode-GEMV (returns HX_GEMM_PATH_GEMV), else the MFMA path (returns
+ * HX_GEMM_PATH_MFMA), which needs a_had (M*K fp16 scratch, as in the reference) or, when
+ * a_had is NULL, takes it from the workspace.  K % 128 == 0, N % 128 == 0, bits 1..8. */
+size_t hx_exl3_gemm_workspace_size(int M, int N, int K);
+int hx_exl3_gemm(void* y, const void* x, const hx_group_words* w, int M, int N, int K, int bits, int y_fp32,
+                 hx_stream_t stream, void* a_had, int mcg, void* workspace, size_t workspace_bytes);
+
+/* Bit-exact decode of a trellis slice to W_hat fp16 [packed_rows*16][unpacked_cols] (no
+ * Hadamard).  Replaces helios::exl3::reconstruct_slice (src/cuda/quant/reconstruct.cuh:15-35,
+ * reconstruct.cu:97-142); bits is the reference's K argument. */
+int hx_exl3_reconstruct_slice(void* unpacked, const void* packed, int packed_rows, int packed_cols,
+                              int unpacked_cols, int bits, int mcg, int mul1, int64_t n_offset, hx_stream_t stream);
+
+/* Row-wise Hadamard-128 with optional fp16 pre/post scales, fp16 in/out.
+ * Replaces helios::exl3::had_r_128 (src/cuda/quant/hadamard.cuh:14-43) for DType::Half. */
+int hx_had_r_128(const void* input, void* output, const void* pre_scale, const void* post_scale, int64_t rows,
+                 int cols, float r_scale, hx_stream_t stream);
+
+/* ---- router / permutation / reduction ----------------------------------------------------- */
+
+/* Sigmoid top-k: topk_indices int64 [bsz][K], topk_weights fp16 [bsz][K].
+ * Replaces helios::aux::routing_ds3_nogroup (src/cuda/aux/routing.cuh:36-49, routing.cu:528-540).
+ * use_topk must be 1 and act_fn 0 (sigmoid); E <= 512, K <= 64. */
+int hx_routing_ds3_nogroup(const void* scores, const void* bias, int64_t* topk_indices, void* topk_weights,
+                           int bsz, int num_experts, int K, float scaling_factor, int use_topk, int act_fn,
+                           hx_stream_t stream);
+
+/* Token-by-expert permutation: expert_count int64 [E+1], token_sorted int64 [M*topk],
+ * weight_sorted fp16 [M*topk], route_to_sorted int64 [M*topk] (optional).  Within an expert the
+ * order is ascending flat routing index (deterministic; the reference uses an atomic cursor).
+ * Replaces helios::glue::moe_permute (src/engine/glue2.cuh:44-46, glue2.cu:280-293); workspace
+ * is accepted for signature parity and unused. */
+int hx_moe_permute(const int64_t* ids, const void* weights, int M, int topk, int E, int64_t* expert_count,
+                   int64_t* token_sorted, void* weight_sorted, int64_t* workspace, hx_stream_t stream,
+                   int64_t* route_to_sorted);
+
+/* y[t][c] = sum_j contributions[route_to_sorted[t*topk+j]][c] in ascending j from +0, fp32.
+ * Replaces helios::glue::moe_reduce_sorted (src/engine/glue2.cuh:48-49, glue2.cu:297-311). */
+int hx_moe_reduce_sorted(float* y, const float* contributions, const int64_t* route_to_sorted, int M, int topk,
+                         int hidden, hx_stream_t stream);
+
+/* out = fp16(silu(min(g, L)) * clamp(u, -L, L)).
+ * Replaces helios::glue::swiglu_clamp (src/engine/glue2.cuh:64, glue2.cu:406-414). */
+int hx_swiglu_clamp(const float* gate, const float* up, void* out, size_t n, float limit, hx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,121 @@
+"""Router top-k, permutation, ordered reduction, Hadamard and swiglu through the C ABI vs the oracle."""
+import itertools
+
+import numpy as np
+import pytest
+
+from helpers import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hx():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from helios_glm53flash_amd import exl3
+    return exl3
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("bsz,E,K", [(1, 288, 8), (4096, 288, 8), (7, 64, 6), (3, 512, 16)])
+def test_routing_bit_exact_indices(hx, bsz, E, K):
+    import torch
+    from oracle import oracle as O
+    r = np.random.default_rng(bsz + E)
+    s = r.standard_normal((bsz, E)).astype(np.float16)
+    s[0, 1] = s[0, 2] = s[0, 3] = np.float16(5.0)  # ties -> lower index first
+    if bsz > 1:
+        s[1, :] = np.float16(0.0)
+        s[1, 5] = np.float16(-0.0)
+    idx = torch.empty((bsz, K), dtype=torch.int64, device="cuda")
+    w = torch.empty((bsz, K), dtype=torch.float16, device="cuda")
+    hx.routing_ds3_nogroup(_dev(s), None, idx, w, bsz, E, K, 2.5)
+    torch.cuda.synchronize()
+    ri, rw = O.routing(s, K, 2.5)
+    assert np.array_equal(idx.cpu().numpy(), ri)
+    gw = w.cpu().float().numpy().astype(np.float64)
+    rw = rw.view(np.float16).astype(np.float64)
+    assert np.abs(gw - rw).max() <= 2 ** -9 * 2.5   # sigmoid via exp: within one fp16 ulp
+
+
+@pytest.mark.parametrize("M,E", [(1, 288), (4096, 288), (37, 17)])
+def test_permute_bit_exact(hx, M, E):
+    import torch
+    from oracle import oracle as O
+    r = np.random.default_rng(M)
+    topk = 8 if E >= 8 else E
+    ids = np.stack([r.permutation(E)[:topk] for _ in range(M)]).astype(np.int64)
+    wt = r.random((M, topk)).astype(np.float16)
+    cnt = torch.empty(E + 1, dtype=torch.int64, device="cuda")
+    ts = torch.empty(M * topk, dtype=torch.int64, device="cuda")
+    ws = torch.empty(M * topk, dtype=torch.float16, device="cuda")
+    r2s = torch.empty(M * topk, dtype=torch.int64, device="cuda")
+    hx.moe_permute(_dev(ids), _dev(wt), M, topk, E, cnt, ts, ws, None, route_to_sorted=r2s)
+    torch.cuda.synchronize()
+    c0, t0, w0, r0 = O.permute(ids, wt, E)
+    assert np.array_equal(cnt.cpu().numpy(), c0)
+    assert np.array_equal(ts.cpu().numpy(), t0)
+    assert np.array_equal(ws.cpu().numpy().view(np.uint16), w0)
+    assert np.array_equal(r2s.cpu().numpy(), r0)
+
+
+def test_reduce_sorted_reference_fixture(hx):
+    """test_deterministic_reductions.cu:49-66: {1e20, -1e20, 1, 1} -> 2.0 for every storage order."""
+    import torch
+    terms = np.array([1e20, -1e20, 1.0, 1.0], np.float32)
+    for perm in itertools.permutations(range(4)):
+        contrib = np.zeros((4, 128), np.float32)
+        for j in range(4):
+            contrib[perm[j]] = terms[j]
+        y = torch.empty((1, 128), dtype=torch.float32, device="cuda")
+        hx.moe_reduce_sorted(y, _dev(contrib), _dev(np.array(perm, np.int64)), 1, 4, 128)
+        torch.cuda.synchronize()
+        assert np.all(y.cpu().numpy() == 2.0)
+
+
+def test_reduce_sorted_random(hx):
+    import torch
+    from oracle import oracle as O
+    r = np.random.default_rng(2)
+    M, topk, hidden = 33, 8, 4096
+    contrib = r.standard_normal((M * topk, hidden)).astype(np.float32)
+    r2s = r.permutation(M * topk).astype(np.int64)
+    y = torch.empty((M, hidden), dtype=torch.float32, device="cuda")
+    hx.moe_reduce_sorted(y, _dev(contrib), _dev(r2s), M, topk, hidden)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), O.reduce_sorted(contrib, r2s, M, topk))
+
+
+def test_had_r_128(hx):
+    import torch
+    from oracle import oracle as O
+    r = np.random.default_rng(3)
+    x = (r.integers(-1000, 1001, (64, 256)) / 250.0).astype(np.float16)
+    pre = r.choice([-1.0, 1.0], 256).astype(np.float16)
+    post = r.uniform(0.5, 1.5, 256).astype(np.float16)
+    out = torch.empty((64, 256), dtype=torch.float16, device="cuda")
+    hx.had_r_128(_dev(x), out, _dev(pre), _dev(post), 64, 256)
+    torch.cuda.synchronize()
+    ref = O.had_r_128_f16(x, pre, post).view(np.float16).astype(np.float64)
+    got = out.cpu().float().numpy().astype(np.float64)
+    # fp32 butterfly order vs exact: at most one fp16 ulp apart
+    assert np.all(np.abs(got - ref) <= np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) * 1.01)
+
+
+def test_swiglu_clamp(hx):
+    import torch
+    from oracle import oracle as O
+    r = np.random.default_rng(4)
+    g = (r.standard_normal(10000) * 6).astype(np.float32)
+    u = (r.standard_normal(10000) * 6).astype(np.float32)
+    out = torch.empty(10000, dtype=torch.float16, device="cuda")
+    hx.swiglu_clamp(_dev(g), _dev(u), out, 10000, 10.0)
+    torch.cuda.synchronize()
+    ref = O.swiglu_clamp(g, u, 10.0).view(np.float16).astype(np.float64)
+    assert_close(out.cpu().float().numpy(), ref, what="swiglu")

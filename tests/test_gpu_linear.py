@@ -1,0 +1,106 @@
+"""Parity of the HIP EXL3 path (through the C ABI) against the CPU oracle."""
+import numpy as np
+import pytest
+
+from helpers import assert_close, make_linear, make_x
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hx():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from helios_glm53flash_amd import exl3
+    return exl3
+
+
+def _dev(a, dtype=None):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.view(dtype)
+    return t.cuda()
+
+
+@pytest.mark.parametrize("bits", range(1, 9))
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_reconstruct_bit_exact_golden(hx, bits, cb):
+    import torch
+    from pathlib import Path
+    f = np.load(Path(__file__).parent / "golden" / "reconstruct_small.npz")
+    tr = f[f"trellis_b{bits}_cb{cb}"]
+    want = f[f"w_b{bits}_cb{cb}"]
+    K, N = tr.shape[0] * 16, tr.shape[1] * 16
+    out = torch.empty((K, N), dtype=torch.float16, device="cuda")
+    hx.reconstruct(out, _dev(tr, torch.int16), K // 16, N // 16, N, bits, cb == 1, cb == 2)
+    torch.cuda.synchronize()
+    got = out.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_reconstruct_slice_offset(hx):
+    import torch
+    from oracle import oracle as O
+    K, N, bits = 64, 512, 3
+    tr, _, _ = make_linear(3, K, N, bits)
+    want = O.reconstruct(tr, K, N, bits, 2)[:, 256:384]
+    out = torch.empty((K, 128), dtype=torch.float16, device="cuda")
+    hx.reconstruct_slice(out, _dev(tr, torch.int16), K // 16, N // 16, 128, bits, False, True, 256)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().view(torch.int16).numpy().view(np.uint16), want)
+
+
+def _run_linear(hx, M, K, N, bits, cb, y_fp32, seed=0):
+    import torch
+    from oracle import oracle as O
+    tr, suh, svh = make_linear(seed + 1, K, N, bits)
+    x = make_x(seed + 2, M, K)
+    w = hx.GroupWords(_dev(tr, torch.int16), _dev(suh), _dev(svh), hx.MUL1 if cb == 2 else 0)
+    y = torch.empty((M, N), dtype=torch.float32 if y_fp32 else torch.float16, device="cuda")
+    path = hx.gemm(y, _dev(x), w, M, N, K, bits, y_fp32, mcg=(cb == 1))
+    torch.cuda.synchronize()
+    ref = O.linear(x, tr, suh, svh, K, N, bits, cb, out_f16=not y_fp32)
+    return path, y.float().cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+@pytest.mark.parametrize("bits,cb", [(2, 2), (3, 2), (4, 2), (4, 0), (5, 1), (6, 2), (8, 2), (1, 0)])
+def test_gemv_parity(hx, M, bits, cb):
+    path, got, ref = _run_linear(hx, M, 1024, 512, bits, cb, True, seed=M * 10 + bits)
+    assert path == hx.HX_GEMM_PATH_GEMV
+    assert_close(got, ref, what=f"gemv M={M} bits={bits} cb={cb}")
+
+
+def test_gemv_fp16_out_and_repeat(hx):
+    # second call reuses the workspace counters (must have been reset by the first)
+    for _ in range(3):
+        _, got, ref = _run_linear(hx, 2, 2048, 1024, 2, 2, False, seed=5)
+        assert_close(got, ref, what="gemv fp16 out")
+
+
+def test_gemv_attention_projection_shape(hx):
+    """K=4096 -> N=12288, 4-bit, M in {1, 4, 8}."""
+    for M in (1, 8):
+        _, got, ref = _run_linear(hx, M, 4096, 12288, 4, 2, True, seed=40 + M)
+        assert_close(got, ref, what=f"attn proj M={M}")
+
+
+@pytest.mark.parametrize("M", [9, 16, 100, 256])
+@pytest.mark.parametrize("bits,cb", [(2, 2), (3, 2), (4, 0), (5, 2)])
+def test_mfma_parity(hx, M, bits, cb):
+    path, got, ref = _run_linear(hx, M, 512, 384, bits, cb, True, seed=M + bits)
+    assert path == hx.HX_GEMM_PATH_MFMA
+    assert_close(got, ref, what=f"mfma M={M} bits={bits} cb={cb}")
+
+
+def test_mfma_fp16_out(hx):
+    _, got, ref = _run_linear(hx, 64, 1024, 256, 2, 2, False, seed=77)
+    assert_close(got, ref, what="mfma fp16")
+
+
+def test_config1_single_linear(hx):
+    """K=4096, N=2048, 2-bit, M=1 vs fp64 decode+matmul."""
+    _, got, ref = _run_linear(hx, 1, 4096, 2048, 2, 2, True, seed=1)
+    assert_close(got, ref, what="config 1")

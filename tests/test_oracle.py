@@ -1,0 +1,309 @@
+"""Pins the CPU oracle (oracle/exl3_oracle.c) independently of its own formulas.
+
+Each check below comes from something other than the oracle's code: numpy/scipy arithmetic,
+the reference's own layout model and test fixtures, or invariants of the mathematics.
+"""
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import scipy.linalg
+
+from oracle import oracle as O
+from helpers import make_linear, make_x
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+# ---------------------------------------------------------------- fp16
+
+def test_fp16_roundtrip_exhaustive():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = h.view(np.float16).astype(np.float64)
+    for i in range(0, 65536, 1):
+        v = f[i]
+        if np.isnan(v):
+            continue
+        assert O.d2h(float(v)) == h[i]
+        assert O.h2d(int(h[i])) == v
+
+
+def test_fp16_rounding_matches_numpy():
+    r = np.random.default_rng(1)
+    vals = np.concatenate([r.standard_normal(20000) * 10.0 ** r.integers(-8, 5, 20000),
+                           [65504.0, 65519.99, 65520.0, 6.0e-8, 2.98e-8, 2.9802322387695312e-08]])
+    for v in vals:
+        assert O.d2h(float(v)) == np.array(v, np.float64).astype(np.float16).view(np.uint16), v
+
+
+# ---------------------------------------------------------------- bitstream
+
+def _stream_bits(tile_u16: np.ndarray) -> np.ndarray:
+    """Stream bits straight from the reference packer's definition (pack.cu:27-53): uint16 words
+    MSB-first, then each uint32 pair half-swapped.  So the stream is the big-endian bit order of
+    the little-endian uint32 words."""
+    w32 = tile_u16.view(np.uint32)
+    return np.unpackbits(w32.astype(">u4").view(np.uint8))
+
+
+@pytest.mark.parametrize("bits", range(1, 9))
+def test_window_matches_bitstream_definition(bits):
+    r = np.random.default_rng(bits)
+    tile = r.integers(0, 65536, 16 * bits, dtype=np.uint16)
+    sb = _stream_bits(tile)
+    total = 256 * bits
+    for p in range(256):
+        end = (p + 1) * bits
+        idx = [(end - 16 + i) % total for i in range(16)]
+        want = int("".join(str(b) for b in sb[idx]), 2)
+        assert O.window(tile, bits, p) == want
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 8])
+def test_window_impulse(bits):
+    """A single set stream bit b appears in exactly the windows whose 16-bit span covers b, at
+    bit position (end - 1 - b) of each (MSB-first)."""
+    total = 256 * bits
+    for b in [0, 1, 15, 16, 31, 32, total - 1, total // 2 + 3]:
+        words = np.zeros(8 * bits, np.uint32)
+        words[b // 32] = np.uint32(1) << np.uint32(31 - b % 32)
+        tile = words.view(np.uint16)
+        for p in range(256):
+            end = (p + 1) * bits
+            d = (end - 1 - b) % total
+            want = (1 << d) if d < 16 else 0
+            assert O.window(tile, bits, p) == want, (bits, b, p)
+
+
+@pytest.mark.parametrize("bits", range(1, 9))
+def test_pack_roundtrip_symbols(bits):
+    r = np.random.default_rng(100 + bits)
+    sym = r.integers(0, 1 << bits, 256)
+    tile = O.pack_tile(sym, bits)
+    win = O.unpack_tile(tile, bits)
+    assert np.array_equal(win & ((1 << bits) - 1), sym)
+    # window p = previous symbols concatenated (16 bits of history, tail-biting)
+    for p in range(256):
+        w = 0
+        nsym = (16 + bits - 1) // bits
+        for q in range(p - nsym + 1, p + 1):
+            w = (w << bits) | int(sym[q % 256])
+        assert int(win[p]) == w & 0xFFFF
+
+
+def test_pack_worked_example():
+    """2-bit symbols 3,0,1,2,... -> stream 11 00 01 10 ...; first uint16 of the MSB-first stream
+    lands in the high half of the first uint32 (SWAP16)."""
+    sym = np.zeros(256, np.int64)
+    sym[:8] = [3, 0, 1, 2, 3, 3, 0, 0]
+    tile = O.pack_tile(sym, 2)
+    w0 = int(tile.view(np.uint32)[0])
+    assert w0 >> 16 == 0b1100011011110000
+
+
+# ---------------------------------------------------------------- codebooks
+
+def _cb_numpy(cb: int) -> np.ndarray:
+    """Codebook re-derived with numpy (codebook.cuh:57-90): uint32 wraparound arithmetic, fp16 via
+    numpy's correctly rounded conversions."""
+    w = np.arange(65536, dtype=np.uint64)
+    if cb == 2:
+        x = (w * 0x83DCD12D) & 0xFFFFFFFF
+        s = (x & 0xFF) + ((x >> 8) & 0xFF) + ((x >> 16) & 0xFF) + (x >> 24)
+        h = (0x6400 + s).astype(np.uint16).view(np.float16).astype(np.float64)
+        c1 = np.array([0x1EEE], np.uint16).view(np.float16).astype(np.float64)[0]
+        c0 = np.array([0xC931], np.uint16).view(np.float16).astype(np.float64)[0]
+        return (h * c1 + c0).astype(np.float16).view(np.uint16)
+    if cb == 1:
+        x = (w * 0xCBAC1FED) & 0xFFFFFFFF
+    else:
+        x = (w * 89226354 + 64248484) & 0xFFFFFFFF
+    x = (x & 0x8FFF8FFF) ^ 0x3B603B60
+    lo = (x & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float64)
+    hi = (x >> 16).astype(np.uint16).view(np.float16).astype(np.float64)
+    return (lo + hi).astype(np.float16).view(np.uint16)
+
+
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_codebook_exhaustive(cb):
+    t = O.codebook_table(cb)
+    assert np.array_equal(t, _cb_numpy(cb))
+    sha = json.loads((GOLD / "codebook_sha256.json").read_text())
+    assert hashlib.sha256(t.tobytes()).hexdigest() == sha[str(cb)]
+
+
+def test_codebook2_properties():
+    v = O.codebook_table(2).view(np.float16).astype(np.float64)
+    c1, c0 = 0.00676727294921875, -10.3828125                    # fp16 0x1eee, 0xc931
+    assert v.min() >= 1024 * c1 + c0 and v.max() <= 2044 * c1 + c0 # byte sum s in [0, 1020]
+    assert v.min() == 1024 * c1 + c0                              # s = 0 (w = 0) is the minimum
+    assert abs(v.mean()) < 0.01 and abs(v.std() - 1.0) < 0.01   # unit-variance Gaussian-like codebook
+
+
+def test_lop3_0x6a_truth_table():
+    """lop3 immediate 0x6a evaluated on the canonical operands (0xF0, 0xCC, 0xAA) is (a & b) ^ c."""
+    a, b, c = 0xF0, 0xCC, 0xAA
+    assert ((a & b) ^ c) == 0x6A
+    assert ((a & b) | (~a & c)) & 0xFF != 0x6A
+
+
+# ---------------------------------------------------------------- tile layout / reconstruct
+
+def _tile_slot_to_index(row: int, col: int):
+    """The reference's own layout model, test_reconstruct.cpp:199-211: slot (row, half2 column col)
+    of a 16x16 tile holds positions (il, il + 32)."""
+    b, g = col // 4, col % 4
+    rb, rr = row // 8, row % 8
+    r, ph = rr // 2, rr % 2
+    q = ph + 2 * rb
+    lane = g * 8 + r
+    il = lane * 8 + q + b * 4
+    return il, il + 32
+
+
+@pytest.mark.parametrize("bits,cb", [(2, 2), (3, 0), (4, 1), (5, 2), (8, 0), (1, 2)])
+def test_reconstruct_layout(bits, cb):
+    K, N = 32, 48
+    trellis, _, _ = make_linear(7 + bits, K, N, bits)
+    W = O.reconstruct(trellis, K, N, bits, cb)
+    table = O.codebook_table(cb)
+    for tk in range(K // 16):
+        for tn in range(N // 16):
+            tile = trellis[tk, tn]
+            win = O.unpack_tile(tile, bits)
+            for k in range(16):
+                for c in range(8):
+                    il, ih = _tile_slot_to_index(k, c)
+                    assert W[16 * tk + k, 16 * tn + 2 * c] == table[win[il]]
+                    assert W[16 * tk + k, 16 * tn + 2 * c + 1] == table[win[ih]]
+
+
+def test_reconstruct_golden():
+    f = np.load(GOLD / "reconstruct_small.npz")
+    for key in [k for k in f.files if k.startswith("trellis_")]:
+        _, bits, cb = key.split("_")
+        bits, cb = int(bits[1:]), int(cb[2:])
+        tr = f[key]
+        K, N = tr.shape[0] * 16, tr.shape[1] * 16
+        assert np.array_equal(O.reconstruct(tr, K, N, bits, cb), f[f"w_b{bits}_cb{cb}"])
+
+
+# ---------------------------------------------------------------- Hadamard
+
+def test_had128_sylvester():
+    H = scipy.linalg.hadamard(128).astype(np.float64) / np.sqrt(128.0)
+    r = np.random.default_rng(3)
+    v = r.standard_normal(256)
+    got = O.had128(v)
+    assert np.allclose(got[:128], H @ v[:128], rtol=0, atol=1e-12)
+    assert np.allclose(got[128:], H @ v[128:], rtol=0, atol=1e-12)
+    assert np.allclose(O.had128(got), v, atol=1e-12)   # H . H = I
+
+
+# ---------------------------------------------------------------- linear
+
+@pytest.mark.parametrize("bits,cb,M", [(2, 2, 1), (4, 0, 3), (3, 1, 2)])
+def test_linear_matches_dense_numpy(bits, cb, M):
+    """Independent dense pipeline: W_hat from reconstruct, H from scipy, fp64 matmul, with the
+    reference's rounding points (x.suh fp16, a_had fp16)."""
+    K, N = 256, 384
+    trellis, suh, svh = make_linear(11, K, N, bits)
+    x = make_x(12, M, K)
+    W = O.reconstruct(trellis, K, N, bits, cb).view(np.float16).astype(np.float64)
+    H = scipy.linalg.hadamard(128).astype(np.float64) / np.sqrt(128.0)
+    xs = (x.astype(np.float64) * suh.astype(np.float64)).astype(np.float16).astype(np.float64)
+    a = (xs.reshape(M, -1, 128) @ H.T).reshape(M, K).astype(np.float16).astype(np.float64)
+    acc = a @ W
+    y = (acc.reshape(M, -1, 128) @ H.T).reshape(M, N) * svh.astype(np.float64)
+    got = O.linear(x, trellis, suh, svh, K, N, bits, cb)
+    assert np.allclose(got, y, rtol=1e-12, atol=1e-9)
+
+
+def test_linear_is_linear_in_transformed_input():
+    K, N = 128, 128
+    trellis, suh, svh = make_linear(5, K, N, 2)
+    x1 = np.ones((1, K), np.float16)
+    y1 = O.linear(x1, trellis, suh, svh, K, N, 2, 2)
+    y2 = O.linear((2 * x1).astype(np.float16), trellis, suh, svh, K, N, 2, 2)
+    assert np.allclose(y2, 2 * y1, rtol=1e-12)
+
+
+def test_cpu_baseline_matches_oracle():
+    K, N, bits = 512, 256, 2
+    trellis, suh, svh = make_linear(21, K, N, bits)
+    x = make_x(22, 2, K)
+    ref = O.linear(x, trellis, suh, svh, K, N, bits, 2)
+    got, secs = O.cpu_linear_f32(x, trellis, suh, svh, K, N, bits, 2, threads=2)
+    assert secs > 0
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-4
+
+
+# ---------------------------------------------------------------- router
+
+def _route_brute(s16: np.ndarray, K: int, scale: float):
+    f = s16.astype(np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    enc = np.where(u & 0x80000000, (~u) & 0xFFFFFFFF, u | 0x80000000)
+    order = sorted(range(len(f)), key=lambda e: (-int(enc[e]), e))[:K]
+    o = np.array([1.0 / (1.0 + np.exp(-float(f[e]))) for e in order])
+    w = (o * scale / (o.sum() + 1e-20)).astype(np.float16)
+    return np.array(order), w
+
+
+def test_routing_brute_force():
+    r = np.random.default_rng(9)
+    s = r.standard_normal((16, 288)).astype(np.float16)
+    s[3, 10] = s[3, 20] = s[3, 30] = np.float16(4.0)    # ties -> lower index first
+    s[4, :] = np.float16(0.0)
+    s[4, 7] = np.float16(-0.0)                          # +0 ranks above -0
+    idx, w = O.routing(s, 8, 2.5)
+    for b in range(16):
+        bi, bw = _route_brute(s[b], 8, 2.5)
+        assert np.array_equal(idx[b], bi)
+        assert np.array_equal(w[b], bw.view(np.uint16))
+    assert list(idx[3, :3]) == [10, 20, 30]
+    assert 7 not in idx[4]
+    assert np.allclose(w.view(np.float16).astype(np.float64).sum(1), 2.5, rtol=5e-3)
+
+
+# ---------------------------------------------------------------- permutation / reduction
+
+def test_permute_definition():
+    r = np.random.default_rng(4)
+    M, topk, E = 50, 8, 40
+    ids = np.stack([r.permutation(E)[:topk] for _ in range(M)]).astype(np.int64)
+    w = r.random((M, topk)).astype(np.float16)
+    cnt, ts, ws, r2s = O.permute(ids, w, E)
+    flat = ids.reshape(-1)
+    assert np.array_equal(cnt[:E], np.bincount(flat, minlength=E)) and cnt[E] == 0
+    order = np.argsort(flat, kind="stable")
+    assert np.array_equal(ts, order // topk)
+    assert np.array_equal(ws, w.reshape(-1).view(np.uint16)[order])
+    assert np.array_equal(flat[order[r2s]], flat)   # route_to_sorted inverts the sort
+    assert np.array_equal(r2s[order], np.arange(M * topk))
+
+
+def test_reduce_sorted_reference_fixture():
+    """test_deterministic_reductions.cu:49-66: terms {1e20, -1e20, 1, 1} in rank order sum to 2.0
+    from +0 for every storage permutation of the contributions."""
+    terms = np.array([1e20, -1e20, 1.0, 1.0], np.float32)
+    import itertools
+    for perm in itertools.permutations(range(4)):
+        contrib = np.zeros((4, 4), np.float32)
+        r2s = np.array(perm, np.int64)
+        for j in range(4):
+            contrib[perm[j], :] = terms[j]
+        y = O.reduce_sorted(contrib, r2s, 1, 4)
+        assert np.all(y == 2.0)
+
+
+def test_swiglu_clamp():
+    g = np.array([-20.0, -1.0, 0.0, 1.0, 12.0], np.float32)
+    u = np.array([1.0, 2.0, 3.0, -15.0, 0.5], np.float32)
+    out = O.swiglu_clamp(g, u, 10.0).view(np.float16).astype(np.float64)
+    gv = np.minimum(g.astype(np.float64), 10.0)
+    uv = np.clip(u.astype(np.float64), -10.0, 10.0)
+    want = (gv / (1 + np.exp(-gv)) * uv).astype(np.float16)
+    assert np.array_equal(out.astype(np.float16), want)
