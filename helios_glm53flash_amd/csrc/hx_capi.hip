@@ -42,7 +42,7 @@ size_t hx_exl3_gemm_workspace_size(int M, int N, int K)
 {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     if (M <= 8) return hx::gemv_workspace_bytes(M, K, N);
-    return align256((size_t)M * K * sizeof(_Float16));
+    return hx::HX_COUNTER_BYTES + align256((size_t)M * K * sizeof(_Float16));
 }
 
 int hx_exl3_gemm(void* y, const void* x, const hx_group_words* w, int M, int N, int K, int bits, int y_fp32,
@@ -68,9 +68,9 @@ int hx_exl3_gemm(void* y, const void* x, const hx_group_words* w, int M, int N, 
     }
     _Float16* ah = static_cast<_Float16*>(a_had);
     if (!ah) {
-        if (!workspace || workspace_bytes < (size_t)M * K * sizeof(_Float16))
+        if (!workspace || workspace_bytes < hx::HX_COUNTER_BYTES + (size_t)M * K * sizeof(_Float16))
             return fail(HX_ERR_WORKSPACE, "hx_exl3_gemm: a_had is null and the workspace cannot hold M*K fp16");
-        ah = static_cast<_Float16*>(workspace);
+        ah = reinterpret_cast<_Float16*>(static_cast<char*>(workspace) + hx::HX_COUNTER_BYTES);
     }
     int r = hip_status(hx::launch_input_had(xh, suh, ah, M, K, st), "hx_exl3_gemm(input transform)");
     if (r) return r;

@@ -6,6 +6,11 @@
 
 namespace hx {
 
+// Every workspace starts with a fixed counter area (arrival counters of the split-K / last-arriver
+// epilogues).  It is zero-filled once by the caller, every kernel leaves the counters it used at
+// zero, and no call ever stores data into it, so calls of different shapes can share a workspace.
+constexpr size_t HX_COUNTER_BYTES = 64 * 1024;
+
 // small-M linear (hx_linear.hip)
 void gemv_plan(int M, int K, int N, int* splits, int* kc);
 size_t gemv_workspace_bytes(int M, int K, int N);

@@ -28,8 +28,7 @@ size_t gemv_workspace_bytes(int M, int K, int N)
 {
     int s, kc;
     gemv_plan(M, K, N, &s, &kc);
-    size_t counters = ((size_t)(N / 128) * sizeof(int) + 255) & ~(size_t)255;
-    return counters + (size_t)s * M * N * sizeof(float);
+    return HX_COUNTER_BYTES + (size_t)s * M * N * sizeof(float);
 }
 
 hipError_t launch_linear_gemv(const _Float16* x, const uint16_t* trellis, const _Float16* suh, const _Float16* svh,
@@ -43,9 +42,9 @@ hipError_t launch_linear_gemv(const _Float16* x, const uint16_t* trellis, const 
     g.K = K;
     g.N = N;
     gemv_plan(M, K, N, &g.splits, &g.kc);
-    size_t counters = ((size_t)(N / 128) * sizeof(int) + 255) & ~(size_t)255;
+    if ((size_t)(N / 128) * sizeof(int) > HX_COUNTER_BYTES) return hipErrorInvalidValue;
     g.counter = static_cast<int*>(ws);
-    g.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + counters);
+    g.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + HX_COUNTER_BYTES);
     g.pre_transformed = false;
     switch (bits) {
         case 1: return launch_gemv_cb<1>(cb, g, svh, y, y_fp32, st);

@@ -14,8 +14,9 @@
  * Conventions: all data pointers are device pointers on the current HIP device; fp16 data is
  * IEEE binary16; `stream` may be 0 (null stream).  Calls are asynchronous on `stream`.
  * Workspaces: caller-owned device memory, zero-filled once before first use (hx_workspace_init
- * or any zero fill); the kernels leave their counters at zero, so a workspace is reused without
- * clearing.  Two calls in flight at once must not share a workspace.
+ * or any zero fill).  The first 64 KiB hold arrival counters that every kernel leaves at zero and
+ * no call writes data into, so one workspace serves calls of any shape without clearing.  Two
+ * calls in flight at once must not share a workspace.
  */
 #ifndef HX_EXL3_H
 #define HX_EXL3_H
