@@ -27,7 +27,7 @@ class GroupWordsC(C.Structure):
 class ExpertTablesC(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in (
         "gate_trellis", "gate_suh", "gate_svh", "up_trellis", "up_suh", "up_svh",
-        "down_trellis", "down_suh", "down_svh", "gate_bits", "up_bits", "down_bits")]
+        "down_trellis", "down_suh", "down_svh", "gate_bits", "up_bits", "down_bits")] + [("bits_mask", C.c_uint32)]
 
 
 # name -> (restype, argtypes); the exported symbol set is exactly the declarations of exl3.h
@@ -48,6 +48,13 @@ SIGNATURES: dict[str, tuple] = {
                                  C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "hx_moe_reduce_sorted": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "hx_swiglu_clamp": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_float, C.c_void_p]),
+    "hx_moe_workspace_size": (C.c_size_t, [C.c_int] * 5),
+    "hx_moe_grouped": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                 C.c_void_p, C.c_void_p, C.POINTER(ExpertTablesC)] + [C.c_int] * 12 +
+                       [C.c_float, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
+    "hx_moe_layer": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(ExpertTablesC),
+                               C.POINTER(GroupWordsC), C.POINTER(C.c_int)] + [C.c_int] * 8 +
+                     [C.c_float, C.c_float, C.c_int, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p]),
 }
 
 

@@ -5,6 +5,8 @@
 
 #include "../../include/hx/exl3.h"
 #include "hx_kernels.hpp"
+#include "hx_moe.hpp"
+#include "hx_moe_decode.hpp"
 
 namespace {
 thread_local char g_err[256] = "";
@@ -142,6 +144,236 @@ int hx_swiglu_clamp(const float* gate, const float* up, void* out, size_t n, flo
     if (!gate || !up || !out) return fail(HX_ERR_INVALID, "hx_swiglu_clamp: null pointer");
     return hip_status(hx::launch_swiglu_clamp(gate, up, static_cast<_Float16*>(out), n, limit, (hipStream_t)stream),
                       "hx_swiglu_clamp");
+}
+
+
+// ------------------------------------------------------------------ MoE
+
+size_t hx_moe_workspace_size(int tokens, int hidden_dim, int intermediate_dim, int num_experts, int topk)
+{
+    if (tokens < 0 || hidden_dim <= 0 || intermediate_dim <= 0 || num_experts <= 0 || topk <= 0) return 0;
+    hx::MoeWs L;
+    L.plan(tokens, hidden_dim, intermediate_dim, num_experts, topk, true);
+    return L.total;
+}
+
+namespace {
+
+int moe_check(const hx_expert_tables* t, int tokens, int hidden, int inter, int E, int topk, int Kg, int Ku, int Kd,
+              int mcg, int mul1, const char* who)
+{
+    if (!t || !t->gate_trellis || !t->gate_suh || !t->gate_svh || !t->up_trellis || !t->up_suh || !t->up_svh ||
+        !t->down_trellis || !t->down_suh || !t->down_svh)
+        return fail(HX_ERR_INVALID, who);
+    if (tokens < 0 || hidden <= 0 || inter <= 0 || hidden % 128 || inter % 128 || E < 1 || E > 512 || topk < 1 ||
+        topk > E || topk > 64)
+        return fail(HX_ERR_INVALID, who);
+    if (!!mcg == !!mul1) return fail(HX_ERR_INVALID, who);  // exactly one of mcg / mul1 (reference contract)
+    const bool tab = t->gate_bits || t->up_bits || t->down_bits;
+    if (tab && !(t->gate_bits && t->up_bits && t->down_bits && t->bits_mask)) return fail(HX_ERR_INVALID, who);
+    if (!tab && (Kg < 1 || Kg > 8 || Ku < 1 || Ku > 8 || Kd < 1 || Kd > 8)) return fail(HX_ERR_INVALID, who);
+    return 0;
+}
+
+void fill_tables(const hx_expert_tables* t, const void* const* (&tr)[3], const void* const* (&suh)[3],
+                 const void* const* (&svh)[3], const int32_t* (&bits)[3], int (&uni)[3], int Kg, int Ku, int Kd)
+{
+    tr[0] = t->gate_trellis; tr[1] = t->up_trellis; tr[2] = t->down_trellis;
+    suh[0] = t->gate_suh; suh[1] = t->up_suh; suh[2] = t->down_suh;
+    svh[0] = t->gate_svh; svh[1] = t->up_svh; svh[2] = t->down_svh;
+    bits[0] = t->gate_bits; bits[1] = t->up_bits; bits[2] = t->down_bits;
+    uni[0] = Kg; uni[1] = Ku; uni[2] = Kd;
+}
+
+uint32_t phase_mask(const hx_expert_tables* t, int Ka, int Kb)
+{
+    if (t->gate_bits) return t->bits_mask;
+    uint32_t m = 1u << Ka;
+    if (Kb > 0) m |= 1u << Kb;
+    return m;
+}
+
+}  // namespace
+
+int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const int64_t* token_sorted,
+                   const void* weight_sorted, void* temp_state_g, void* temp_state_u, void* temp_intermediate_g,
+                   void* temp_intermediate_u, const hx_expert_tables* tables, int tokens, int hidden_dim,
+                   int intermediate_dim, int num_experts, int topk, int max_tokens_per_expert, int concurrency,
+                   int K_gate, int K_up, int K_down, int mcg, int mul1, float act_limit, int act_function,
+                   int num_active, hx_stream_t stream, float* sorted_contributions, const int64_t* route_to_sorted,
+                   void* workspace, size_t workspace_bytes)
+{
+    (void)temp_state_g; (void)temp_state_u; (void)temp_intermediate_g; (void)temp_intermediate_u;
+    (void)max_tokens_per_expert; (void)concurrency; (void)num_active;
+    if (int r = moe_check(tables, tokens, hidden_dim, intermediate_dim, num_experts, topk, K_gate, K_up, K_down, mcg,
+                          mul1, "hx_moe_grouped: bad arguments"))
+        return r;
+    if (act_function != 0) return fail(HX_ERR_UNSUPPORTED, "hx_moe_grouped: only act_function 0 (SiLU)");
+    if (!x || !expert_count || !token_sorted || !weight_sorted) return fail(HX_ERR_INVALID, "hx_moe_grouped: null input");
+    if (!sorted_contributions && (!y || !route_to_sorted))
+        return fail(HX_ERR_INVALID, "hx_moe_grouped: y and route_to_sorted are needed without sorted_contributions");
+    if (tokens == 0) return 0;
+    hx::MoeWs L;
+    L.plan(tokens, hidden_dim, intermediate_dim, num_experts, topk, false);
+    if (!workspace || workspace_bytes < L.total) return fail(HX_ERR_WORKSPACE, "hx_moe_grouped: workspace too small");
+    char* base = static_cast<char*>(workspace);
+    hipStream_t st = (hipStream_t)stream;
+    const int cb = mcg ? 1 : 2;
+    const _Float16* xh = static_cast<const _Float16*>(x);
+    const _Float16* ws_sorted = static_cast<const _Float16*>(weight_sorted);
+    if (tokens <= 8) {
+        hx::MoeDecodeArgs a = L.decode_args(base);
+        a.x = xh;
+        a.expert_count = expert_count;
+        a.token_sorted = token_sorted;
+        a.weight_sorted = ws_sorted;
+        fill_tables(tables, a.tr, a.suh, a.svh, a.bits_tab, a.bits_uniform, K_gate, K_up, K_down);
+        a.act_limit = act_limit;
+        float* contrib = sorted_contributions ? sorted_contributions : reinterpret_cast<float*>(base + L.off_contrib);
+        a.contrib = contrib;
+        int r = hip_status(hx::run_moe_decode(a, cb, phase_mask(tables, K_gate, K_up), phase_mask(tables, K_down, 0), st),
+                           "hx_moe_grouped(decode)");
+        if (r) return r;
+        if (!sorted_contributions)
+            r = hip_status(hx::launch_moe_combine(contrib, route_to_sorted, tokens, topk, hidden_dim, false, nullptr, y,
+                                                  true, st),
+                           "hx_moe_grouped(reduce)");
+        return r;
+    }
+    hx::PrefillArgs p{};
+    p.x = xh;
+    p.T = tokens;
+    p.hidden = hidden_dim;
+    p.inter = intermediate_dim;
+    p.E = num_experts;
+    p.topk = topk;
+    p.R = tokens * topk;
+    p.expert_count = expert_count;
+    p.token_sorted = token_sorted;
+    p.weight_sorted = ws_sorted;
+    p.r2s = route_to_sorted;
+    fill_tables(tables, p.tr, p.suh, p.svh, p.bits_tab, p.bits_uniform, K_gate, K_up, K_down);
+    p.act_limit = act_limit;
+    p.cb = cb;
+    p.ws = base;
+    p.lay = &L;
+    if (sorted_contributions) {
+        // contributions only: combine writes them; no y
+        return hip_status(hx::run_moe_prefill(p, sorted_contributions, nullptr, nullptr, nullptr, false, st),
+                          "hx_moe_grouped(prefill)");
+    }
+    return hip_status(hx::run_moe_prefill(p, nullptr, nullptr, nullptr, y, true, st), "hx_moe_grouped(prefill)");
+}
+
+int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, const void* bias,
+                 const hx_expert_tables* tables, const hx_group_words* shared, const int* shared_bits, int tokens,
+                 int hidden_dim, int intermediate_dim, int num_experts, int topk, int K_gate, int K_up, int K_down,
+                 float routed_scale, float act_limit, int mcg, int mul1, void* workspace, size_t workspace_bytes,
+                 hx_stream_t stream)
+{
+    if (int r = moe_check(tables, tokens, hidden_dim, intermediate_dim, num_experts, topk, K_gate, K_up, K_down, mcg,
+                          mul1, "hx_moe_layer: bad arguments"))
+        return r;
+    if (!x || !scores || (!y && !y_routed)) return fail(HX_ERR_INVALID, "hx_moe_layer: null input/output");
+    if (shared) {
+        if (!shared_bits) return fail(HX_ERR_INVALID, "hx_moe_layer: shared_bits required with a shared expert");
+        for (int i = 0; i < 3; ++i)
+            if (!shared[i].trellis || !shared[i].suh || !shared[i].svh || shared_bits[i] < 1 || shared_bits[i] > 8)
+                return fail(HX_ERR_INVALID, "hx_moe_layer: bad shared expert");
+        if (act_limit <= 0.0f) return fail(HX_ERR_INVALID, "hx_moe_layer: the shared-expert swiglu needs act_limit > 0");
+    }
+    if (tokens == 0) return 0;
+    hx::MoeWs L;
+    L.plan(tokens, hidden_dim, intermediate_dim, num_experts, topk, shared != nullptr);
+    if (!workspace || workspace_bytes < L.total) return fail(HX_ERR_WORKSPACE, "hx_moe_layer: workspace too small");
+    char* base = static_cast<char*>(workspace);
+    hipStream_t st = (hipStream_t)stream;
+    const int cb = mcg ? 1 : 2;
+    const _Float16* xh = static_cast<const _Float16*>(x);
+    int64_t* idx = reinterpret_cast<int64_t*>(base + L.off_idx);
+    _Float16* wt = reinterpret_cast<_Float16*>(base + L.off_w);
+    int64_t* cnt = reinterpret_cast<int64_t*>(base + L.off_count);
+    int64_t* ts = reinterpret_cast<int64_t*>(base + L.off_tsorted);
+    _Float16* wsorted = reinterpret_cast<_Float16*>(base + L.off_wsorted);
+    int64_t* r2s = reinterpret_cast<int64_t*>(base + L.off_r2s);
+
+    int r = hip_status(hx::launch_routing(static_cast<const _Float16*>(scores), static_cast<const _Float16*>(bias), idx,
+                                          wt, tokens, num_experts, topk, routed_scale, st),
+                       "hx_moe_layer(routing)");
+    if (r) return r;
+    r = hip_status(hx::launch_permute(idx, wt, tokens, topk, num_experts, cnt, ts, wsorted, r2s, nullptr, st),
+                   "hx_moe_layer(permute)");
+    if (r) return r;
+
+    if (tokens <= 8) {
+        hx::MoeDecodeArgs a = L.decode_args(base);
+        a.x = xh;
+        a.expert_count = cnt;
+        a.token_sorted = ts;
+        a.weight_sorted = wsorted;
+        fill_tables(tables, a.tr, a.suh, a.svh, a.bits_tab, a.bits_uniform, K_gate, K_up, K_down);
+        uint32_t mgu = phase_mask(tables, K_gate, K_up), md = phase_mask(tables, K_down, 0);
+        if (shared) {
+            for (int i = 0; i < 3; ++i) {
+                a.sh_tr[i] = shared[i].trellis;
+                a.sh_suh[i] = shared[i].suh;
+                a.sh_svh[i] = shared[i].svh;
+                a.sh_bits[i] = shared_bits[i];
+            }
+            mgu |= (1u << shared_bits[0]) | (1u << shared_bits[1]);
+            md |= 1u << shared_bits[2];
+        }
+        a.act_limit = act_limit;
+        float* contrib = reinterpret_cast<float*>(base + L.off_contrib);
+        a.contrib = contrib;
+        r = hip_status(hx::run_moe_decode(a, cb, mgu, md, st), "hx_moe_layer(experts)");
+        if (r) return r;
+        return hip_status(hx::launch_moe_combine(contrib, r2s, tokens, topk, hidden_dim, shared != nullptr,
+                                                 static_cast<_Float16*>(y), y_routed, false, st),
+                          "hx_moe_layer(combine)");
+    }
+
+    const float* shared_rows = nullptr;
+    if (shared) {
+        _Float16* sh_a = reinterpret_cast<_Float16*>(base + L.off_sh_a);
+        float* sh_g = reinterpret_cast<float*>(base + L.off_sh_g);
+        float* sh_u = reinterpret_cast<float*>(base + L.off_sh_u);
+        _Float16* sh_act = reinterpret_cast<_Float16*>(base + L.off_sh_act);
+        float* sh_d = reinterpret_cast<float*>(base + L.off_sh_d);
+        auto H = [](const void* p) { return static_cast<const _Float16*>(p); };
+        auto U16 = [](const void* p) { return static_cast<const uint16_t*>(p); };
+        hipError_t e = hx::launch_input_had(xh, H(shared[0].suh), sh_a, tokens, hidden_dim, st);
+        if (!e) e = hx::launch_linear_mfma(sh_a, U16(shared[0].trellis), H(shared[0].svh), sh_g, tokens, hidden_dim,
+                                           intermediate_dim, shared_bits[0], cb, true, st);
+        if (!e) e = hx::launch_input_had(xh, H(shared[1].suh), sh_a, tokens, hidden_dim, st);
+        if (!e) e = hx::launch_linear_mfma(sh_a, U16(shared[1].trellis), H(shared[1].svh), sh_u, tokens, hidden_dim,
+                                           intermediate_dim, shared_bits[1], cb, true, st);
+        if (!e) e = hx::launch_swiglu_clamp(sh_g, sh_u, sh_act, (size_t)tokens * intermediate_dim, act_limit, st);
+        if (!e) e = hx::launch_input_had(sh_act, H(shared[2].suh), sh_a, tokens, intermediate_dim, st);
+        if (!e) e = hx::launch_linear_mfma(sh_a, U16(shared[2].trellis), H(shared[2].svh), sh_d, tokens,
+                                           intermediate_dim, hidden_dim, shared_bits[2], cb, true, st);
+        if ((r = hip_status(e, "hx_moe_layer(shared expert)"))) return r;
+        shared_rows = sh_d;
+    }
+    hx::PrefillArgs p{};
+    p.x = xh;
+    p.T = tokens;
+    p.hidden = hidden_dim;
+    p.inter = intermediate_dim;
+    p.E = num_experts;
+    p.topk = topk;
+    p.R = tokens * topk;
+    p.expert_count = cnt;
+    p.token_sorted = ts;
+    p.weight_sorted = wsorted;
+    p.r2s = r2s;
+    fill_tables(tables, p.tr, p.suh, p.svh, p.bits_tab, p.bits_uniform, K_gate, K_up, K_down);
+    p.act_limit = act_limit;
+    p.cb = cb;
+    p.ws = base;
+    p.lay = &L;
+    return hip_status(hx::run_moe_prefill(p, nullptr, shared_rows, static_cast<_Float16*>(y), y_routed, false, st),
+                      "hx_moe_layer(prefill)");
 }
 
 }  // extern "C"

@@ -51,15 +51,16 @@ HX_INLINE void tile_mac(const uint32_t* w, const uint32_t (*xa)[8], float (*acc)
 // Input transform of rows [0, M) over k in [k0, k0 + kc) into LDS as fp16:
 //   a = fp16(H128(fp16(x . suh)))   (reference had_hf_r_128_inner<true,false>)
 // When pre_transformed, x already holds a (copied as is).
-HX_INLINE void input_to_lds(uint32_t* a_lds, const _Float16* x, const _Float16* suh, int M, int K,
-                            int k0, int kc, bool pre_transformed)
+HX_INLINE void input_to_lds(uint32_t* a_lds, const _Float16* x, const int64_t* rows, const _Float16* suh, int M,
+                            int K, int k0, int kc, bool pre_transformed)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int blocks = kc >> 7;
     for (int job = wave; job < M * blocks; job += GEMV_WAVES) {
         const int m = job / blocks, b = job % blocks;
         const int k = k0 + b * 128 + 2 * lane;
-        uint32_t xv = *reinterpret_cast<const uint32_t*>(x + (size_t)m * K + k);
+        const size_t row = rows ? (size_t)rows[m] : (size_t)m;
+        uint32_t xv = *reinterpret_cast<const uint32_t*>(x + row * K + k);
         uint32_t out;
         if (pre_transformed) {
             out = xv;
@@ -77,6 +78,7 @@ HX_INLINE void input_to_lds(uint32_t* a_lds, const _Float16* x, const _Float16* 
 
 struct GemvArgs {
     const _Float16* x;       // M x K fp16 (or pre-transformed a)
+    const int64_t* rows;     // optional row gather: row m of the input is x[rows[m]]
     const uint16_t* trellis; // (K/16, N/16, 16*bits)
     const _Float16* suh;     // K
     int M, K, N;
@@ -100,7 +102,7 @@ __device__ void gemv_split_sum(const GemvArgs& g, int cg, int s, uint32_t* a_lds
     const int kc = min(g.kc, g.K - k0);
     const int tiles_n = g.N >> 4;
 
-    input_to_lds(a_lds, g.x, g.suh, g.M, g.K, k0, kc, g.pre_transformed);
+    input_to_lds(a_lds, g.x, g.rows, g.suh, g.M, g.K, k0, kc, g.pre_transformed);
     __syncthreads();
 
     float acc[MT][16];

@@ -36,6 +36,7 @@ hipError_t launch_linear_gemv(const _Float16* x, const uint16_t* trellis, const 
 {
     GemvArgs g;
     g.x = x;
+    g.rows = nullptr;
     g.trellis = trellis;
     g.suh = suh;
     g.M = M;

@@ -1,0 +1,312 @@
+// hx_moe_prefill.hip -- routed experts for many tokens on gfx950 (grouped MFMA GEMMs over the
+// token-by-expert permutation).
+//
+// Flow (all stream-ordered, no host synchronisation):
+//   plan       expert_count -> per-row expert id and 128-row tile jobs per expert
+//   gather     xg[r] = fp16(H(x[token_sorted[r]] . suh_g[e])), xu[r] likewise  (one wave per 128 block)
+//   gemm g/u   G = xg . W_g[e], U = xu . W_u[e]   (decode-to-LDS + MFMA, fp16 outputs, one launch)
+//   guad       act[r] = fp16(H((silu(g) * u) . suh_d)), g = fp16(H(G)) . svh_g ...  (fp16 chain)
+//   gemm d     D = act . W_d[e]                    (fp16 output)
+//   combine    y[t] = fp16(sum_j H(D[r_j]) * w_j / sqrt(128) . svh_d[e_j]  + shared[t])
+// Reference semantics: src/cuda/quant/exl3_moe_kernel.cuh:57-262, hadamard_inner.cuh:284-481,
+// src/engine/glue2.cu:297-306, runner.cpp:957-958.
+#include "hx_mfma.hpp"
+#include "hx_kernels.hpp"
+#include "hx_moe.hpp"
+
+namespace hx {
+
+static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct Job {
+    int expert, row0, rows, pad;
+};
+
+void MoeWs::prefill_layout(size_t o)
+{
+    max_jobs = (R + MF_BM - 1) / MF_BM + E;
+    const int kmax = hidden > inter ? hidden : inter;
+    off_jobs = o;       o = al(o + sizeof(Job) * max_jobs);
+    off_njobs = o;      o = al(o + sizeof(int));
+    off_row_expert = o; o = al(o + sizeof(int) * R);
+    off_xg = o;         o = al(o + sizeof(_Float16) * (size_t)R * hidden);
+    off_xu = o;         o = al(o + sizeof(_Float16) * (size_t)R * hidden);
+    off_G = o;          o = al(o + sizeof(_Float16) * (size_t)R * inter);
+    off_U = o;          o = al(o + sizeof(_Float16) * (size_t)R * inter);
+    off_A = o;          o = al(o + sizeof(_Float16) * (size_t)R * inter);
+    off_D = off_xg;     // D reuses xg (xg is consumed by the gate GEMM before the down GEMM runs)
+    off_sh_a = o;       o = al(o + sizeof(_Float16) * (size_t)T * kmax);
+    off_sh_g = o;       o = al(o + sizeof(float) * (size_t)T * inter);
+    off_sh_u = o;       o = al(o + sizeof(float) * (size_t)T * inter);
+    off_sh_act = o;     o = al(o + sizeof(_Float16) * (size_t)T * inter);
+    off_sh_d = o;       o = al(o + sizeof(float) * (size_t)T * hidden);
+    prefill_end = o;
+}
+
+// ------------------------------------------------------------------ plan
+
+__global__ __launch_bounds__(256) void prefill_plan_kernel(const int64_t* expert_count, int E, int R, Job* jobs,
+                                                          int* njobs, int* row_expert)
+{
+    __shared__ int off[513];
+    const int t = threadIdx.x;
+    if (t == 0) {
+        int acc = 0, n = 0;
+        for (int e = 0; e < E; ++e) {
+            off[e] = acc;
+            const int c = (int)expert_count[e];
+            for (int m0 = 0; m0 < c; m0 += MF_BM) jobs[n++] = Job{e, acc + m0, min(MF_BM, c - m0), 0};
+            acc += c;
+        }
+        off[E] = acc;
+        *njobs = n;
+    }
+    __syncthreads();
+    for (int r = t; r < R; r += 256) {
+        int lo = 0, hi = E;  // largest e with off[e] <= r
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (off[mid] <= r) lo = mid;
+            else hi = mid;
+        }
+        row_expert[r] = lo;
+    }
+}
+
+// ------------------------------------------------------------------ gather + input transform
+
+__global__ __launch_bounds__(256) void prefill_gather_kernel(const _Float16* x, const int64_t* token_sorted,
+                                                            const int* row_expert, const void* const* suh_g,
+                                                            const void* const* suh_u, _Float16* xg, _Float16* xu,
+                                                            long blocks, int hidden)
+{
+    const int lane = threadIdx.x & 63;
+    const long b = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= blocks) return;
+    const int per = hidden / 128;
+    const long r = b / per;
+    const int c = (int)(b % per) * 128 + 2 * lane;
+    const int e = row_expert[r];
+    const hx_h2 xv = *reinterpret_cast<const hx_h2*>(x + (size_t)token_sorted[r] * hidden + c);
+    {
+        hx_h2 v = xv * *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(suh_g[e]) + c);
+        float v0 = (float)v.x, v1 = (float)v.y;
+        hx_had128_wave(v0, v1);
+        *reinterpret_cast<hx_h2*>(xg + r * hidden + c) = hx_h2{(_Float16)v0, (_Float16)v1};
+    }
+    {
+        hx_h2 v = xv * *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(suh_u[e]) + c);
+        float v0 = (float)v.x, v1 = (float)v.y;
+        hx_had128_wave(v0, v1);
+        *reinterpret_cast<hx_h2*>(xu + r * hidden + c) = hx_h2{(_Float16)v0, (_Float16)v1};
+    }
+}
+
+// ------------------------------------------------------------------ grouped GEMM
+
+struct GroupedGemmArgs {
+    const Job* jobs;
+    const int* njobs;
+    const _Float16* A[2];
+    _Float16* out[2];
+    const void* const* tr[2];
+    const int32_t* bits_tab[2];
+    int bits_uniform[2];
+    int K, N, nproj;
+};
+
+template <int CB>
+__global__ __launch_bounds__(MF_THREADS) void grouped_gemm_kernel(GroupedGemmArgs g)
+{
+    __shared__ MfmaSmem sm;
+    const int job_i = blockIdx.y;
+    if (job_i >= *g.njobs) return;
+    const Job job = g.jobs[job_i];
+    const int ntiles = g.N / 128;
+    const int proj = blockIdx.x / ntiles;
+    const int cg = blockIdx.x % ntiles;
+    const int bits = g.bits_tab[proj] ? g.bits_tab[proj][job.expert] : g.bits_uniform[proj];
+    const _Float16* A = g.A[proj] + (size_t)job.row0 * g.K;
+    const uint32_t* tr = static_cast<const uint32_t*>(g.tr[proj][job.expert]);
+    hx_f4 acc[4][4];
+    switch (bits) {
+        case 1: mfma_tile<1, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
+        case 2: mfma_tile<2, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
+        case 3: mfma_tile<3, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
+        case 4: mfma_tile<4, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
+        case 5: mfma_tile<5, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
+        case 6: mfma_tile<6, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
+        case 7: mfma_tile<7, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
+        default: mfma_tile<8, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
+    }
+    _Float16* out = g.out[proj] + (size_t)job.row0 * g.N + cg * 128;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int half = 0; half < 2; ++half) {
+        stage_c_half(acc, half, sm);
+        __syncthreads();
+        for (int r = wave; r < 64; r += 4) {
+            const int row = 64 * half + r;
+            if (row >= job.rows) break;
+            hx_h2 h = {(_Float16)sm.c[r * MF_LDC + 2 * lane], (_Float16)sm.c[r * MF_LDC + 2 * lane + 1]};
+            *reinterpret_cast<hx_h2*>(out + (size_t)row * g.N + 2 * lane) = h;
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------ guad
+
+__global__ __launch_bounds__(256) void prefill_guad_kernel(const _Float16* G, const _Float16* U, const int* row_expert,
+                                                          const void* const* svh_g, const void* const* svh_u,
+                                                          const void* const* suh_d, _Float16* act, long blocks,
+                                                          int inter, float L)
+{
+    const int lane = threadIdx.x & 63;
+    const long b = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= blocks) return;
+    const int per = inter / 128;
+    const long r = b / per;
+    const int c = (int)(b % per) * 128 + 2 * lane;
+    const int e = row_expert[r];
+    const hx_h2 sg = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(svh_g[e]) + c);
+    const hx_h2 su = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(svh_u[e]) + c);
+    const hx_h2 sd = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(suh_d[e]) + c);
+    const hx_h2 Gv = *reinterpret_cast<const hx_h2*>(G + r * inter + c);
+    const hx_h2 Uv = *reinterpret_cast<const hx_h2*>(U + r * inter + c);
+    float g0 = (float)Gv.x, g1 = (float)Gv.y, u0 = (float)Uv.x, u1 = (float)Uv.y;
+    hx_had128_wave(g0, g1);
+    hx_had128_wave(u0, u1);
+    hx_h2 g = hx_h2{(_Float16)g0, (_Float16)g1} * sg;
+    hx_h2 u = hx_h2{(_Float16)u0, (_Float16)u1} * su;
+    g.x = hx_silu_h(g.x);
+    g.y = hx_silu_h(g.y);
+    if (L != 0.0f) {
+        const _Float16 Lh = (_Float16)L, nLh = (_Float16)(-L);
+        u.x = u.x < nLh ? nLh : (u.x > Lh ? Lh : u.x);
+        u.y = u.y < nLh ? nLh : (u.y > Lh ? Lh : u.y);
+        g.x = g.x > Lh ? Lh : g.x;
+        g.y = g.y > Lh ? Lh : g.y;
+    }
+    hx_h2 p = (g * u) * sd;
+    float p0 = (float)p.x, p1 = (float)p.y;
+    hx_had128_wave(p0, p1);
+    *reinterpret_cast<hx_h2*>(act + r * inter + c) = hx_h2{(_Float16)p0, (_Float16)p1};
+}
+
+// ------------------------------------------------------------------ combine
+
+// One wave per (token, 128-column block): contributions H(D[r]) * w / sqrt(128) . svh_d[e] in
+// ascending routing rank from +0, then + shared, then fp16.
+__global__ __launch_bounds__(256) void prefill_combine_kernel(const _Float16* D, const int64_t* r2s,
+                                                             const int* row_expert, const _Float16* w_sorted,
+                                                             const void* const* svh_d, int T, int topk, int hidden,
+                                                             float* contrib, const float* shared_rows, _Float16* y,
+                                                             float* y_routed, bool accumulate)
+{
+    const int lane = threadIdx.x & 63;
+    const long b = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int per = hidden / 128;
+    if (b >= (long)T * per) return;
+    const int t = (int)(b / per);
+    const int c = (int)(b % per) * 128 + 2 * lane;
+    float a0 = 0.0f, a1 = 0.0f;
+    for (int j = 0; j < topk; ++j) {
+        const int64_t r = r2s[(size_t)t * topk + j];
+        const int e = row_expert[r];
+        const hx_h2 dv = *reinterpret_cast<const hx_h2*>(D + (size_t)r * hidden + c);
+        float d0 = (float)dv.x, d1 = (float)dv.y;
+        hx_had128_wave(d0, d1);
+        const float w = (float)w_sorted[r];
+        const hx_h2 sd = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(svh_d[e]) + c);
+        d0 = d0 * w * (float)sd.x;
+        d1 = d1 * w * (float)sd.y;
+        if (contrib) *reinterpret_cast<float2*>(contrib + (size_t)r * hidden + c) = make_float2(d0, d1);
+        a0 += d0;
+        a1 += d1;
+    }
+    const size_t o = (size_t)t * hidden + c;
+    if (y_routed) {
+        float2* yr = reinterpret_cast<float2*>(y_routed + o);
+        float2 prev = accumulate ? *yr : make_float2(0.0f, 0.0f);
+        *yr = make_float2(prev.x + a0, prev.y + a1);
+    }
+    if (y) {
+        if (shared_rows) {
+            a0 += shared_rows[o];
+            a1 += shared_rows[o + 1];
+        }
+        *reinterpret_cast<hx_h2*>(y + o) = hx_h2{(_Float16)a0, (_Float16)a1};
+    }
+}
+
+// ------------------------------------------------------------------ driver
+
+hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* shared_rows, _Float16* y,
+                           float* y_routed, bool accumulate, hipStream_t st)
+{
+    const MoeWs& L = *p.lay;
+    char* ws = p.ws;
+    Job* jobs = reinterpret_cast<Job*>(ws + L.off_jobs);
+    int* njobs = reinterpret_cast<int*>(ws + L.off_njobs);
+    int* row_expert = reinterpret_cast<int*>(ws + L.off_row_expert);
+    _Float16* xg = reinterpret_cast<_Float16*>(ws + L.off_xg);
+    _Float16* xu = reinterpret_cast<_Float16*>(ws + L.off_xu);
+    _Float16* G = reinterpret_cast<_Float16*>(ws + L.off_G);
+    _Float16* U = reinterpret_cast<_Float16*>(ws + L.off_U);
+    _Float16* A = reinterpret_cast<_Float16*>(ws + L.off_A);
+    _Float16* D = reinterpret_cast<_Float16*>(ws + L.off_D);
+    if (p.E > 512) return hipErrorInvalidValue;
+
+    hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(256), 0, st, p.expert_count, p.E, p.R, jobs, njobs,
+                       row_expert);
+    const long gblocks = (long)p.R * (p.hidden / 128);
+    hipLaunchKernelGGL(prefill_gather_kernel, dim3((unsigned)((gblocks + 3) / 4)), dim3(256), 0, st, p.x,
+                       p.token_sorted, row_expert, p.suh[0], p.suh[1], xg, xu, gblocks, p.hidden);
+
+    GroupedGemmArgs g{};
+    g.jobs = jobs;
+    g.njobs = njobs;
+    g.A[0] = xg;
+    g.A[1] = xu;
+    g.out[0] = G;
+    g.out[1] = U;
+    g.tr[0] = p.tr[0];
+    g.tr[1] = p.tr[1];
+    g.bits_tab[0] = p.bits_tab[0];
+    g.bits_tab[1] = p.bits_tab[1];
+    g.bits_uniform[0] = p.bits_uniform[0];
+    g.bits_uniform[1] = p.bits_uniform[1];
+    g.K = p.hidden;
+    g.N = p.inter;
+    g.nproj = 2;
+    dim3 grid_gu(2 * (p.inter / 128), L.max_jobs);
+    if (p.cb == 1) hipLaunchKernelGGL(grouped_gemm_kernel<1>, grid_gu, dim3(MF_THREADS), 0, st, g);
+    else hipLaunchKernelGGL(grouped_gemm_kernel<2>, grid_gu, dim3(MF_THREADS), 0, st, g);
+
+    const long ublocks = (long)p.R * (p.inter / 128);
+    hipLaunchKernelGGL(prefill_guad_kernel, dim3((unsigned)((ublocks + 3) / 4)), dim3(256), 0, st, G, U, row_expert,
+                       p.svh[0], p.svh[1], p.suh[2], A, ublocks, p.inter, p.act_limit);
+
+    GroupedGemmArgs d{};
+    d.jobs = jobs;
+    d.njobs = njobs;
+    d.A[0] = A;
+    d.out[0] = D;
+    d.tr[0] = p.tr[2];
+    d.bits_tab[0] = p.bits_tab[2];
+    d.bits_uniform[0] = p.bits_uniform[2];
+    d.K = p.inter;
+    d.N = p.hidden;
+    d.nproj = 1;
+    dim3 grid_d(p.hidden / 128, L.max_jobs);
+    if (p.cb == 1) hipLaunchKernelGGL(grouped_gemm_kernel<1>, grid_d, dim3(MF_THREADS), 0, st, d);
+    else hipLaunchKernelGGL(grouped_gemm_kernel<2>, grid_d, dim3(MF_THREADS), 0, st, d);
+
+    const long cblocks = (long)p.T * (p.hidden / 128);
+    hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)((cblocks + 3) / 4)), dim3(256), 0, st, D, p.r2s,
+                       row_expert, p.weight_sorted, p.svh[2], p.T, p.topk, p.hidden, contrib, shared_rows, y,
+                       y_routed, accumulate);
+    return hipGetLastError();
+}
+
+}  // namespace hx

@@ -49,9 +49,10 @@ typedef struct hx_group_words {
 } hx_group_words;
 
 /* Per-expert device pointer tables, each a device array of num_experts pointers, plus optional
- * per-expert bit widths (device int32 arrays, or NULL to use the call's uniform widths).
- * Replaces helios::exl3::ExpertTables (src/cuda/quant/exl3_moe.cuh:20-31); the bits arrays are
- * an extension for layers that mix bit widths across experts. */
+ * per-expert bit widths (device int32 arrays, or NULL to use the call's uniform widths) and
+ * bits_mask, the host-side union of the widths those arrays hold (bit b set when some expert
+ * uses b bits).  Replaces helios::exl3::ExpertTables (src/cuda/quant/exl3_moe.cuh:20-31); the
+ * bits arrays and mask are an extension for layers that mix bit widths across experts. */
 typedef struct hx_expert_tables {
     const void* const* gate_trellis;
     const void* const* gate_suh;
@@ -65,6 +66,7 @@ typedef struct hx_expert_tables {
     const int32_t* gate_bits;
     const int32_t* up_bits;
     const int32_t* down_bits;
+    uint32_t bits_mask;
 } hx_expert_tables;
 
 /* ---- library ---------------------------------------------------------------------------- */
@@ -120,6 +122,43 @@ int hx_moe_reduce_sorted(float* y, const float* contributions, const int64_t* ro
 /* out = fp16(silu(min(g, L)) * clamp(u, -L, L)).
  * Replaces helios::glue::swiglu_clamp (src/engine/glue2.cuh:64, glue2.cu:406-414). */
 int hx_swiglu_clamp(const float* gate, const float* up, void* out, size_t n, float limit, hx_stream_t stream);
+
+/* ---- MoE layer ---------------------------------------------------------------------------- */
+
+/* Workspace bytes for hx_moe_grouped / hx_moe_layer with these extents. */
+size_t hx_moe_workspace_size(int tokens, int hidden_dim, int intermediate_dim, int num_experts, int topk);
+
+/* Routed experts of one MoE layer: per expert, gather its rows, input Hadamard with suh_g/suh_u,
+ * gate/up GEMMs, SiLU-gate with act_limit clamp, down GEMM, times the routing weight and svh_d.
+ * With sorted_contributions (fp32 [tokens*topk][hidden_dim], token_sorted order) each weighted row
+ * is written once for a fixed-order reduction (hx_moe_reduce_sorted); without it y (fp32
+ * [tokens][hidden_dim]) receives y += the routed sum in ascending routing rank (deterministic;
+ * route_to_sorted is then required).  tokens <= 8 runs the fused decode-GEMV kernels, larger
+ * batches the grouped MFMA path.  Replaces helios::exl3::moe_grouped
+ * (src/cuda/quant/exl3_moe.cuh:74-105, exl3_moe.cu:58-265).  temp_* buffers, max_tokens_per_expert,
+ * concurrency and num_active are accepted for signature parity and unused (all scratch comes from
+ * the workspace; there is no token cap per expert).  Codebooks: mcg or mul1 (as the reference);
+ * act_function must be 0 (SiLU). */
+int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const int64_t* token_sorted,
+                   const void* weight_sorted, void* temp_state_g, void* temp_state_u, void* temp_intermediate_g,
+                   void* temp_intermediate_u, const hx_expert_tables* tables, int tokens, int hidden_dim,
+                   int intermediate_dim, int num_experts, int topk, int max_tokens_per_expert, int concurrency,
+                   int K_gate, int K_up, int K_down, int mcg, int mul1, float act_limit, int act_function,
+                   int num_active, hx_stream_t stream, float* sorted_contributions, const int64_t* route_to_sorted,
+                   void* workspace, size_t workspace_bytes);
+
+/* A whole MoE FFN layer without host synchronisation: sigmoid top-k over scores (fp16
+ * [tokens][E], optional bias), deterministic permutation, routed experts, shared expert (three
+ * hx_group_words gate/up/down with bit widths shared_bits[3], or NULL), ordered reduction and
+ * y = fp16(routed + shared) [tokens][hidden_dim]; y_routed (fp32, optional) receives the routed
+ * sum.  Replaces the single-GPU part of helios Runner::moe_ffn (src/engine/runner.cpp:711-959:
+ * shared expert :723-738, router :759-762, permute :764, moe_grouped + reduce :918-922,
+ * combine :957-958). */
+int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, const void* bias,
+                 const hx_expert_tables* tables, const hx_group_words* shared, const int* shared_bits, int tokens,
+                 int hidden_dim, int intermediate_dim, int num_experts, int topk, int K_gate, int K_up, int K_down,
+                 float routed_scale, float act_limit, int mcg, int mul1, void* workspace, size_t workspace_bytes,
+                 hx_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,123 @@
+"""MoE layer parity (router -> permute -> experts -> SiLU-gate -> down -> ordered reduce -> shared
+combine) through the C ABI against the CPU oracle."""
+import numpy as np
+import pytest
+
+from helpers import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hx():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from helios_glm53flash_amd import exl3, moe
+    return exl3, moe
+
+
+def _host(t):
+    import torch
+    return t.cpu().view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.int16 else t.cpu().numpy()
+
+
+def _oracle_experts(ex, used):
+    dummy = np.zeros(16, np.uint16)
+    out = {"trellis": [], "suh": [], "svh": [], "bits": []}
+    for p in range(3):
+        out["trellis"].append([_host(ex.trellis[p][e]) if e in used else dummy for e in range(ex.num_experts)])
+        out["suh"].append([_host(ex.suh[p][e]).view(np.uint16) if e in used else dummy for e in range(ex.num_experts)])
+        out["svh"].append([_host(ex.svh[p][e]).view(np.uint16) if e in used else dummy for e in range(ex.num_experts)])
+        out["bits"].append(np.array(ex.bits[p], np.int32))
+    return out
+
+
+def _oracle_shared(sh):
+    return {"trellis": [_host(w.trellis) for w in sh], "suh": [_host(w.suh).view(np.uint16) for w in sh],
+            "svh": [_host(w.svh).view(np.uint16) for w in sh], "bits": [w.bits for w in sh]}
+
+
+def _run_layer(hx, E, hidden, inter, topk, T, bits, shared_bits, seed, rows=None):
+    import torch
+    from oracle import oracle as O
+    exl3, moe = hx
+    ex = moe.ExpertSet.synthetic(E, hidden, inter, bits, seed=seed)
+    sh = moe.synthetic_dense_mlp(hidden, inter, shared_bits, seed=seed + 1) if shared_bits else None
+    layer = moe.MoeLayer(ex, sh, topk=topk)
+    r = np.random.default_rng(seed + 2)
+    x = r.standard_normal((T, hidden)).astype(np.float16)
+    scores = r.standard_normal((T, E)).astype(np.float32).astype(np.float16)
+    y_routed = torch.empty((T, hidden), dtype=torch.float32, device="cuda")
+    y = layer(torch.from_numpy(x).cuda(), torch.from_numpy(scores).cuda(), y_routed=y_routed)
+    torch.cuda.synchronize()
+    idx, w = O.routing(scores, topk, 2.5)
+    rows = np.arange(T) if rows is None else np.asarray(rows)
+    used = set(int(e) for e in idx[rows].reshape(-1))
+    yr_ref, yo_ref = O.moe_rows(x, hidden, inter, idx, w, rows, _oracle_experts(ex, used),
+                                _oracle_shared(sh) if sh else None, 10.0)
+    got_r = y_routed.cpu().numpy()[rows]
+    assert_close(got_r, yr_ref, what=f"routed E={E} T={T}")
+    if sh:
+        assert_close(y.float().cpu().numpy()[rows], yo_ref.view(np.float16).astype(np.float64), what=f"y E={E} T={T}")
+    return ex, y
+
+
+@pytest.mark.parametrize("T", [1, 3, 8])
+def test_moe_decode_small(hx, T):
+    _run_layer(hx, E=16, hidden=512, inter=256, topk=4, T=T, bits=2, shared_bits=2, seed=10 + T)
+
+
+def test_moe_decode_mixed_bits(hx):
+    bits = [(2, 3, 4) if e % 2 else (3, 2, 2) for e in range(12)]
+    _run_layer(hx, E=12, hidden=256, inter=384, topk=3, T=2, bits=bits, shared_bits=(4, 4, 3), seed=3)
+
+
+@pytest.mark.parametrize("T", [9, 40])
+def test_moe_prefill_small(hx, T):
+    _run_layer(hx, E=16, hidden=512, inter=256, topk=4, T=T, bits=2, shared_bits=3, seed=20 + T)
+
+
+def test_moe_prefill_mixed_bits_no_shared(hx):
+    bits = [2 if e < 8 else 3 for e in range(16)]
+    _run_layer(hx, E=16, hidden=256, inter=256, topk=8, T=33, bits=bits, shared_bits=None, seed=5)
+
+
+def test_moe_decode_config3(hx):
+    """288 experts + shared, 4096 -> 2048 -> 4096, 2 bits, top-8, 1 token."""
+    _run_layer(hx, E=288, hidden=4096, inter=2048, topk=8, T=1, bits=2, shared_bits=2, seed=300)
+
+
+def test_moe_prefill_config4_sampled(hx):
+    """BASELINE config 4 shape at 512 tokens (2/3-bit experts), 6 sampled rows against the oracle."""
+    bits = [2 if e < 144 else 3 for e in range(288)]
+    _run_layer(hx, E=288, hidden=4096, inter=2048, topk=8, T=512, bits=bits, shared_bits=None, seed=400,
+               rows=[0, 1, 77, 200, 311, 511])
+
+
+def test_moe_grouped_reference_api(hx):
+    """moe_grouped with sorted_contributions, then moe_reduce_sorted, equals y += routed sum."""
+    import torch
+    exl3, moe = hx
+    E, hidden, inter, topk = 16, 256, 256, 4
+    for T in (2, 24):
+        ex = moe.ExpertSet.synthetic(E, hidden, inter, 2, seed=T)
+        r = np.random.default_rng(T)
+        x = torch.from_numpy(r.standard_normal((T, hidden)).astype(np.float16)).cuda()
+        s = torch.from_numpy(r.standard_normal((T, E)).astype(np.float16)).cuda()
+        idx = torch.empty((T, topk), dtype=torch.int64, device="cuda")
+        w = torch.empty((T, topk), dtype=torch.float16, device="cuda")
+        exl3.routing_ds3_nogroup(s, None, idx, w, T, E, topk, 2.5)
+        cnt = torch.empty(E + 1, dtype=torch.int64, device="cuda")
+        ts = torch.empty(T * topk, dtype=torch.int64, device="cuda")
+        wsr = torch.empty(T * topk, dtype=torch.float16, device="cuda")
+        r2s = torch.empty(T * topk, dtype=torch.int64, device="cuda")
+        exl3.moe_permute(idx, w, T, topk, E, cnt, ts, wsr, None, route_to_sorted=r2s)
+        contrib = torch.empty((T * topk, hidden), dtype=torch.float32, device="cuda")
+        moe.moe_grouped(x, None, cnt, ts, wsr, ex, T, topk, sorted_contributions=contrib)
+        y1 = torch.empty((T, hidden), dtype=torch.float32, device="cuda")
+        exl3.moe_reduce_sorted(y1, contrib, r2s, T, topk, hidden)
+        y2 = torch.ones((T, hidden), dtype=torch.float32, device="cuda")
+        moe.moe_grouped(x, y2, cnt, ts, wsr, ex, T, topk, route_to_sorted=r2s)
+        torch.cuda.synchronize()
+        assert torch.equal(y2 - 1.0, y1) or float((y2 - 1.0 - y1).abs().max()) < 1e-5
