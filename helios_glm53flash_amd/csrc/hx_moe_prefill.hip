@@ -239,6 +239,26 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const _Float16* D,
     }
 }
 
+// Contributions only (no token reduction): one wave per (sorted row, 128-column block).
+__global__ __launch_bounds__(256) void prefill_contrib_kernel(const _Float16* D, const int* row_expert,
+                                                             const _Float16* w_sorted, const void* const* svh_d,
+                                                             long blocks, int hidden, float* contrib)
+{
+    const int lane = threadIdx.x & 63;
+    const long b = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= blocks) return;
+    const int per = hidden / 128;
+    const long r = b / per;
+    const int c = (int)(b % per) * 128 + 2 * lane;
+    const int e = row_expert[r];
+    const hx_h2 dv = *reinterpret_cast<const hx_h2*>(D + (size_t)r * hidden + c);
+    float d0 = (float)dv.x, d1 = (float)dv.y;
+    hx_had128_wave(d0, d1);
+    const float w = (float)w_sorted[r];
+    const hx_h2 sd = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(svh_d[e]) + c);
+    *reinterpret_cast<float2*>(contrib + (size_t)r * hidden + c) = make_float2(d0 * w * (float)sd.x, d1 * w * (float)sd.y);
+}
+
 // ------------------------------------------------------------------ driver
 
 hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* shared_rows, _Float16* y,
@@ -302,6 +322,15 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     if (p.cb == 1) hipLaunchKernelGGL(grouped_gemm_kernel<1>, grid_d, dim3(MF_THREADS), 0, st, d);
     else hipLaunchKernelGGL(grouped_gemm_kernel<2>, grid_d, dim3(MF_THREADS), 0, st, d);
 
+    if (!y && !y_routed) {
+        // contributions only: per sorted row, no route_to_sorted needed
+        if (!contrib) return hipErrorInvalidValue;
+        const long rblocks = (long)p.R * (p.hidden / 128);
+        hipLaunchKernelGGL(prefill_contrib_kernel, dim3((unsigned)((rblocks + 3) / 4)), dim3(256), 0, st, D, row_expert,
+                           p.weight_sorted, p.svh[2], rblocks, p.hidden, contrib);
+        return hipGetLastError();
+    }
+    if (!p.r2s) return hipErrorInvalidValue;
     const long cblocks = (long)p.T * (p.hidden / 128);
     hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)((cblocks + 3) / 4)), dim3(256), 0, st, D, p.r2s,
                        row_expert, p.weight_sorted, p.svh[2], p.T, p.topk, p.hidden, contrib, shared_rows, y,

@@ -120,4 +120,5 @@ def test_moe_grouped_reference_api(hx):
         y2 = torch.ones((T, hidden), dtype=torch.float32, device="cuda")
         moe.moe_grouped(x, y2, cnt, ts, wsr, ex, T, topk, route_to_sorted=r2s)
         torch.cuda.synchronize()
-        assert torch.equal(y2 - 1.0, y1) or float((y2 - 1.0 - y1).abs().max()) < 1e-5
+        # y2 = 1 + sum (accumulate contract): compare up to the fp32 rounding of that addition
+        assert float((y2 - (1.0 + y1)).abs().max()) <= float(y1.abs().max()) * 2 ** -22
