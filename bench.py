@@ -1,0 +1,232 @@
+"""Benchmark of the EXL3 MoE hot path on one MI355X.
+
+Headline (BASELINE.json metric): weight GB/s of the MoE decode layer (config 3: 288 routed experts
++ 1 shared, 4096 -> 2048 -> 4096, 2-bit EXL3 (mul1 codebook), top-8 sigmoid router, 1 token),
+counting compressed EXL3 bytes (trellis + suh + svh) of the 8 routed experts and the shared expert
+read per step.  A step is one full layer: router top-k, permutation, gate/up, SiLU-gate, down,
+ordered reduction and shared-expert combine.  Weights are resident in HBM; steps rotate over
+independent layers (distinct weights, independent seeded router scores) so consecutive steps do not
+hit the 256 MB MALL with the previous step's experts.
+
+Also reported (extra): prefill expert-GEMM TFLOP/s (config 4: 4096 tokens, Zipf(1.1) routing, half
+2-bit / half 3-bit experts), the per-phase split, and the CPU baseline (the C oracle's fp32 decode +
+GEMV over the same experts, OpenMP, on this host).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = "EXL3 MoE decode weight GB/s (% of HBM peak) + prefill expert-GEMM TFLOP/s"
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+
+
+def zipf_scores(T: int, E: int, s: float, seed: int) -> np.ndarray:
+    """log(Zipf(s) popularity of a seeded expert permutation) + Gumbel noise -> fp16 logits."""
+    r = np.random.default_rng(seed)
+    perm = r.permutation(E)
+    pop = np.empty(E)
+    pop[perm] = np.arange(1, E + 1, dtype=np.float64) ** (-s)
+    logits = np.log(pop)[None, :] + r.gumbel(size=(T, E))
+    return logits.astype(np.float16)
+
+
+def bench_decode(args, torch, moe, lib):
+    E, hidden, inter, topk, bits = 288, 4096, 2048, 8, 2
+    L = args.layers
+    layers = []
+    for li in range(L):
+        ex = moe.ExpertSet.synthetic(E, hidden, inter, bits, seed=1000 + li)
+        sh = moe.synthetic_dense_mlp(hidden, inter, bits, seed=5000 + li)
+        layers.append(moe.MoeLayer(ex, sh, topk=topk))
+    nsteps = args.warmup + args.steps
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    scores = torch.randn((nsteps, 1, E), generator=g, device="cuda").to(torch.float16)
+    x = torch.randn((1, hidden), generator=g, device="cuda").to(torch.float16)
+    y = torch.empty((1, hidden), dtype=torch.float16, device="cuda")
+    ws = torch.zeros(layers[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
+    per_expert = layers[0].experts.weight_bytes([0])
+    step_bytes = 9 * per_expert  # 8 routed (distinct) + shared, all the same size
+
+    for i in range(args.warmup):
+        layers[i % L](x, scores[i], y=y, ws=ws)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t0.record()
+    for i in range(args.warmup, nsteps):
+        layers[i % L](x, scores[i], y=y, ws=ws)
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = t0.elapsed_time(t1) / args.steps
+
+    # phase split with HIP events recorded inside the library on the layer's stream
+    import ctypes as C
+    lib.hx_profile_enable(1)
+    for i in range(args.warmup, nsteps):
+        layers[i % L](x, scores[i], y=y, ws=ws)
+    tot = (C.c_double * 16)()
+    cnt = (C.c_int * 16)()
+    n = lib.hx_profile_read(tot, cnt, 16)
+    lib.hx_profile_enable(0)
+    phases = {}
+    for p in range(n):
+        if cnt[p]:
+            phases[lib.hx_profile_phase_name(p).decode()] = tot[p] / cnt[p] * 1e3  # us per call
+    gu_bytes = 9 * sum(layers[0].experts.trellis[p][0].numel() * 2 + layers[0].experts.suh[p][0].numel() * 2 +
+                       layers[0].experts.svh[p][0].numel() * 2 for p in (0, 1))
+    d_bytes = step_bytes - gu_bytes
+    dominant = max(("experts_gate_up", gu_bytes), ("experts_down", d_bytes), key=lambda kv: phases.get(kv[0], 0))
+    dom_us = phases[dominant[0]]
+    achieved = dominant[1] / (dom_us * 1e-6) / 1e9
+    return {
+        "ms_per_step": ms, "value": step_bytes / (ms * 1e-3) / 1e9, "step_bytes": step_bytes, "wall_s": wall,
+        "phases_us": phases, "dominant": dominant[0], "dominant_bytes": dominant[1], "dominant_us": dom_us,
+        "roofline_achieved": achieved, "layers": layers,
+    }
+
+
+def bench_prefill(args, torch, moe):
+    E, hidden, inter, topk, T = 288, 4096, 2048, 8, 4096
+    bits = [2 if e < E // 2 else 3 for e in range(E)]
+    ex = moe.ExpertSet.synthetic(E, hidden, inter, bits, seed=77)
+    layer = moe.MoeLayer(ex, None, topk=topk)
+    scores = torch.from_numpy(zipf_scores(T, E, 1.1, seed=11)).cuda()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    x = torch.randn((T, hidden), generator=g, device="cuda").to(torch.float16)
+    y = torch.empty((T, hidden), dtype=torch.float16, device="cuda")
+    ws = torch.zeros(layer.workspace_bytes(T), dtype=torch.uint8, device="cuda")
+    for _ in range(2):
+        layer(x, scores, y=y, ws=ws)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = args.prefill_steps
+    t0.record()
+    for _ in range(reps):
+        layer(x, scores, y=y, ws=ws)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    flops = 2.0 * T * topk * 3 * hidden * inter
+    del ws
+    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops}
+
+
+def cpu_baseline(layers, budget_s: float):
+    """The C oracle's fp32 decode + GEMV (OpenMP over column tiles) over the same experts of the
+    decode layer (gate, up, down of 8 routed + shared), timed on this host."""
+    from oracle import oracle as O
+    import torch
+    lay = layers[0]
+    ex, sh = lay.experts, lay.shared
+    rng = np.random.default_rng(0)
+    experts = [int(e) for e in rng.permutation(ex.num_experts)[:8]]
+    mats = []
+    for e in experts:
+        for p, (K, N) in enumerate([(ex.hidden, ex.inter), (ex.hidden, ex.inter), (ex.inter, ex.hidden)]):
+            mats.append((K, N, ex.bits[p][e], ex.trellis[p][e], ex.suh[p][e], ex.svh[p][e]))
+    for p, w in enumerate(sh):
+        K, N = w.in_features, w.out_features
+        mats.append((K, N, w.bits, w.trellis, w.suh, w.svh))
+    host = [(K, N, b, t.cpu().view(torch.int16).numpy().view(np.uint16), s.cpu().numpy(), v.cpu().numpy())
+            for K, N, b, t, s, v in mats]
+    x = {K: rng.standard_normal((1, K)).astype(np.float16) for K in {m[0] for m in host}}
+    threads = O.cpu_max_threads()
+    total_s, total_bytes, layers_done = 0.0, 0, 0
+    while total_s < budget_s and layers_done < 50:
+        for K, N, b, t, s, v in host:
+            _, secs = O.cpu_linear_f32(x[K], t, s, v, K, N, b, 2, threads)
+            total_s += secs
+            total_bytes += t.size * 2 + s.size * 2 + v.size * 2
+        layers_done += 1
+    return {"value": total_bytes / total_s / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{layers_done} MoE decode layers (8 routed + shared experts, gate/up/down, 2-bit, 1 token) "
+                      f"through oracle/exl3_oracle.c hx_cpu_linear_f32 (fp32 accumulate, OpenMP), "
+                      f"{total_s:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--layers", type=int, default=8, help="independent layers rotated over (MALL defeat)")
+    ap.add_argument("--prefill-steps", type=int, default=5)
+    ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (one GPU holds every expert); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from helios_glm53flash_amd import moe
+    from helios_glm53flash_amd._lib import lib
+
+    torch.cuda.set_device(0)
+    dec = bench_decode(args, torch, moe, lib)
+    pre = None if args.skip_prefill else bench_prefill(args, torch, moe)
+    cpu = None if args.skip_cpu else cpu_baseline(dec["layers"], args.cpu_budget)
+
+    out = {
+        "metric": METRIC,
+        "value": round(dec["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded uniform trellis words, +-1 suh, +-U(0.5,1.5) svh, N(0,1) activations and "
+                "router logits; random-init weights of the GLM-5.3-Flash MoE layer shape)",
+        "config": {
+            "workload": "moe_decode_layer: 288 routed experts + 1 shared, hidden 4096, intermediate 2048, "
+                        "2-bit EXL3 (mul1 codebook), sigmoid top-8 (scale 2.5), 1 token (BASELINE config 3)",
+            "tokens": 1, "experts": 288, "topk": 8, "bits": 2, "hidden": 4096, "intermediate": 2048,
+            "rotating_layers": args.layers, "bytes_per_step": dec["step_bytes"],
+            "pct_of_hbm_peak": round(100.0 * dec["value"] / HBM_PEAK_GBS, 2),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dec["dominant"],
+            "achieved": round(dec["roofline_achieved"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dec["roofline_achieved"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": dec["dominant_bytes"],
+            "avg_launch_us": round(dec["dominant_us"], 3),
+        },
+        "cpu_baseline": cpu,
+        "extra": {
+            "decode_phases_us": {k: round(v, 3) for k, v in dec["phases_us"].items()},
+            "prefill": None if pre is None else {
+                "workload": "moe_prefill: 4096 tokens, top-8 of 288 with Zipf(1.1) popularity, experts 0-143 "
+                            "2-bit / 144-287 3-bit, hidden 4096, intermediate 2048 (BASELINE config 4), routed "
+                            "experts only",
+                "ms": round(pre["ms"], 4), "tflops": round(pre["tflops"], 2),
+                "pct_of_fp16_peak": round(100.0 * pre["tflops"] / FP16_PEAK_TFLOPS, 2),
+            },
+        },
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

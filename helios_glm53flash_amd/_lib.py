@@ -35,6 +35,9 @@ SIGNATURES: dict[str, tuple] = {
     "hx_version": (C.c_char_p, []),
     "hx_last_error": (C.c_char_p, []),
     "hx_workspace_init": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p]),
+    "hx_profile_enable": (C.c_int, [C.c_int]),
+    "hx_profile_read": (C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_int), C.c_int]),
+    "hx_profile_phase_name": (C.c_char_p, [C.c_int]),
     "hx_exl3_gemm_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
     "hx_exl3_gemm": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(GroupWordsC), C.c_int, C.c_int, C.c_int, C.c_int,
                                C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_size_t]),

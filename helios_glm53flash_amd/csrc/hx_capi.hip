@@ -3,6 +3,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <vector>
+
 #include "../../include/hx/exl3.h"
 #include "hx_kernels.hpp"
 #include "hx_moe.hpp"
@@ -10,6 +12,56 @@
 
 namespace {
 thread_local char g_err[256] = "";
+
+// Optional phase profiler: HIP events recorded around each phase of hx_moe_layer on its stream.
+struct Prof {
+    bool on = false;
+    struct Rec {
+        int phase;
+        hipEvent_t a, b;
+    };
+    std::vector<Rec> recs;
+    std::vector<hipEvent_t> pool;
+    hipEvent_t take()
+    {
+        if (!pool.empty()) {
+            hipEvent_t e = pool.back();
+            pool.pop_back();
+            return e;
+        }
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        return e;
+    }
+};
+Prof g_prof;
+const char* const k_phase_names[] = {"route", "permute", "experts_gate_up", "experts_down", "combine",
+                                     "shared_expert", "prefill_plan_gather", "prefill_gemm_gate_up",
+                                     "prefill_guad", "prefill_gemm_down", "prefill_combine"};
+constexpr int k_nphases = sizeof(k_phase_names) / sizeof(k_phase_names[0]);
+
+struct Phase {
+    int id;
+    hipStream_t st;
+    hipEvent_t a = nullptr;
+    Phase(int id_, hipStream_t st_) : id(id_), st(st_)
+    {
+        if (g_prof.on) {
+            a = g_prof.take();
+            if (a) hipEventRecord(a, st);
+        }
+    }
+    ~Phase()
+    {
+        if (a) {
+            hipEvent_t b = g_prof.take();
+            if (b) {
+                hipEventRecord(b, st);
+                g_prof.recs.push_back({id, a, b});
+            }
+        }
+    }
+};
 
 int fail(int code, const char* what)
 {
@@ -33,6 +85,38 @@ extern "C" {
 
 const char* hx_version(void) { return "hx_exl3 0.1 gfx950"; }
 const char* hx_last_error(void) { return g_err; }
+
+int hx_profile_enable(int on)
+{
+    g_prof.on = on != 0;
+    return 0;
+}
+
+int hx_profile_read(double* ms_total, int* counts, int max_phases)
+{
+    if (hipDeviceSynchronize() != hipSuccess) return fail(HX_ERR_HIP, "hx_profile_read: synchronize failed");
+    for (int i = 0; i < max_phases; ++i) {
+        ms_total[i] = 0.0;
+        counts[i] = 0;
+    }
+    for (auto& r : g_prof.recs) {
+        float ms = 0.0f;
+        hipEventElapsedTime(&ms, r.a, r.b);
+        if (r.phase < max_phases) {
+            ms_total[r.phase] += ms;
+            counts[r.phase] += 1;
+        }
+        g_prof.pool.push_back(r.a);
+        g_prof.pool.push_back(r.b);
+    }
+    g_prof.recs.clear();
+    return k_nphases;
+}
+
+const char* hx_profile_phase_name(int phase)
+{
+    return (phase >= 0 && phase < k_nphases) ? k_phase_names[phase] : "";
+}
 
 int hx_workspace_init(void* workspace, size_t bytes, hx_stream_t stream)
 {
@@ -297,12 +381,19 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
     _Float16* wsorted = reinterpret_cast<_Float16*>(base + L.off_wsorted);
     int64_t* r2s = reinterpret_cast<int64_t*>(base + L.off_r2s);
 
-    int r = hip_status(hx::launch_routing(static_cast<const _Float16*>(scores), static_cast<const _Float16*>(bias), idx,
+    int r;
+    {
+        Phase ph(0, st);
+        r = hip_status(hx::launch_routing(static_cast<const _Float16*>(scores), static_cast<const _Float16*>(bias), idx,
                                           wt, tokens, num_experts, topk, routed_scale, st),
                        "hx_moe_layer(routing)");
+    }
     if (r) return r;
-    r = hip_status(hx::launch_permute(idx, wt, tokens, topk, num_experts, cnt, ts, wsorted, r2s, nullptr, st),
-                   "hx_moe_layer(permute)");
+    {
+        Phase ph(1, st);
+        r = hip_status(hx::launch_permute(idx, wt, tokens, topk, num_experts, cnt, ts, wsorted, r2s, nullptr, st),
+                       "hx_moe_layer(permute)");
+    }
     if (r) return r;
 
     if (tokens <= 8) {
@@ -326,8 +417,17 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
         a.act_limit = act_limit;
         float* contrib = reinterpret_cast<float*>(base + L.off_contrib);
         a.contrib = contrib;
-        r = hip_status(hx::run_moe_decode(a, cb, mgu, md, st), "hx_moe_layer(experts)");
+        {
+            Phase ph(2, st);
+            r = hip_status(hx::run_moe_decode(a, cb, mgu, 0, st), "hx_moe_layer(experts gate/up)");
+        }
         if (r) return r;
+        {
+            Phase ph(3, st);
+            r = hip_status(hx::run_moe_decode(a, cb, 0, md, st), "hx_moe_layer(experts down)");
+        }
+        if (r) return r;
+        Phase ph(4, st);
         return hip_status(hx::launch_moe_combine(contrib, r2s, tokens, topk, hidden_dim, shared != nullptr,
                                                  static_cast<_Float16*>(y), y_routed, false, st),
                           "hx_moe_layer(combine)");
@@ -335,6 +435,7 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
 
     const float* shared_rows = nullptr;
     if (shared) {
+        Phase ph(5, st);
         _Float16* sh_a = reinterpret_cast<_Float16*>(base + L.off_sh_a);
         float* sh_g = reinterpret_cast<float*>(base + L.off_sh_g);
         float* sh_u = reinterpret_cast<float*>(base + L.off_sh_u);
@@ -372,6 +473,7 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
     p.cb = cb;
     p.ws = base;
     p.lay = &L;
+    Phase ph(7, st);
     return hip_status(hx::run_moe_prefill(p, nullptr, shared_rows, static_cast<_Float16*>(y), y_routed, false, st),
                       "hx_moe_layer(prefill)");
 }

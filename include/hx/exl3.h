@@ -74,6 +74,15 @@ const char* hx_version(void);
 const char* hx_last_error(void);
 int hx_workspace_init(void* workspace, size_t bytes, hx_stream_t stream);
 
+/* Phase profiler (no reference counterpart; the reference times phases with HELIOS_PROF host/event
+ * timers, src/engine/runner.cpp:1006-1058): while enabled, hx_moe_layer records HIP events around
+ * each phase on its stream.  hx_profile_read synchronizes the device, writes the summed
+ * milliseconds and the number of records per phase (arrays of max_phases), clears the records and
+ * returns the number of phases; hx_profile_phase_name names phase i. */
+int hx_profile_enable(int on);
+int hx_profile_read(double* ms_total, int* counts, int max_phases);
+const char* hx_profile_phase_name(int phase);
+
 /* ---- quantized linear ------------------------------------------------------------------- */
 
 /* y[M][N] = svh . H_N( H_K(x . suh) . W_hat ), x fp16 [M][K], y fp32 (y_fp32) or fp16.
