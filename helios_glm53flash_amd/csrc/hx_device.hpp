@@ -85,6 +85,59 @@ HX_INLINE hx_h2 hx_decode2(uint32_t w0, uint32_t w1)
     }
 }
 
+// ------------------------------------------------------------------ codebook 2, register level
+
+// The 32 stream bits ending at (cyclic) stream bit E of a tile, MSB first: bit 0 is stream bit E-1.
+// Its low half is the window ending at E, its high half the window ending at E - 16.
+template <int BITS, int E>
+HX_INLINE uint32_t hx_reg_end(const uint32_t* w)
+{
+    constexpr int total = 256 * BITS, nw = 8 * BITS;
+    constexpr int e = ((E % total) + total) % total;
+    constexpr int j = e >> 5, r = e & 31;
+    if constexpr (r == 0) return w[(j - 1 + nw) % nw];
+    else return __builtin_amdgcn_alignbit(w[(j - 1 + nw) % nw], w[j % nw], 32 - r);
+}
+
+// x = window * 0x83DCD12D mod 2^32 for the 16-bit window in the low (HI = false) or high half of
+// r, whatever the other half holds: x = w*0xD12D + ((w*0x83DC mod 2^16) << 16), i.e. one
+// v_pk_mul_lo_u16 producing (w*0x83DC) << 16 and one v_mad_u32_u16 (both full rate, where
+// v_mul_lo_u32 is a quarter-rate op and would also need the window masked first).
+template <bool HI>
+HX_INLINE uint32_t hx_mul1_x(uint32_t r)
+{
+    uint32_t t, x;
+    if constexpr (!HI) {
+        asm("v_pk_mul_lo_u16 %0, %1, %2 op_sel_hi:[0,1]" : "=v"(t) : "v"(r), "s"(0x83dc0000u));
+        asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(x) : "v"(r), "s"(0xd12du), "v"(t));
+    } else {
+        asm("v_pk_mul_lo_u16 %0, %1, %2 op_sel:[1,0] op_sel_hi:[1,1]" : "=v"(t) : "v"(r), "s"(0x83dc0000u));
+        asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(x) : "v"(r), "s"(0xd12du), "v"(t));
+    }
+    return x;
+}
+
+// x of position P.  When BITS divides 16, positions D = 16/BITS apart share one register (low and
+// high half), so a tile needs one alignbit per two positions.
+template <int BITS, int P>
+HX_INLINE uint32_t hx_mul1_pos(const uint32_t* w)
+{
+    constexpr int D = (16 % BITS == 0) ? 16 / BITS : 0;
+    if constexpr (D != 0 && (P % (2 * D)) < D) return hx_mul1_x<true>(hx_reg_end<BITS, (P + D + 1) * BITS>(w));
+    else return hx_mul1_x<false>(hx_reg_end<BITS, (P + 1) * BITS>(w));
+}
+
+// Decoded fp16 pair (positions P, P+1) of codebook 2: h = fp16(0x6400 + bytesum(x)) = 1024 + s
+// exactly, v = fma(h, 0x1eee, 0xc931) rounded once (codebook.cuh:77-90).
+template <int BITS, int P>
+HX_INLINE hx_h2 hx_mul1_pair(const uint32_t* w)
+{
+    const uint32_t s0 = __builtin_amdgcn_udot4(hx_mul1_pos<BITS, P>(w), 0x01010101u, 0x6400u, false);
+    const uint32_t s1 = __builtin_amdgcn_udot4(hx_mul1_pos<BITS, P + 1>(w), 0x01010101u, 0x6400u, false);
+    const hx_h2 h = u32_as_h2((s1 << 16) | s0);
+    return __builtin_elementwise_fma(h, u32_as_h2(0x1eee1eeeu), u32_as_h2(0xc931c931u));
+}
+
 template <int CB>
 HX_INLINE _Float16 hx_decode1(uint32_t w)
 {

@@ -20,10 +20,12 @@ constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_WAVES = 4;
 
 // Tile words of one 16x16 tile into registers (2*BITS 16-byte loads).
+typedef const __attribute__((address_space(1))) hx_u4 hx_gu4;
+
 template <int BITS>
 HX_INLINE void load_tile(uint32_t* w, const uint32_t* src)
 {
-    const hx_u4* s4 = reinterpret_cast<const hx_u4*>(src);
+    hx_gu4* s4 = (hx_gu4*)(src);
 #pragma unroll
     for (int i = 0; i < 2 * BITS; ++i) {
         hx_u4 v = __builtin_nontemporal_load(s4 + i);
@@ -35,12 +37,15 @@ HX_INLINE void load_tile(uint32_t* w, const uint32_t* src)
 }
 
 // acc[m][n] += sum_k a[m][k] * W_tile[k][n] for one tile.  xa[m][kp] holds fp16 pair (2kp, 2kp+1).
+// Codebook 2 takes the register-level path of hx_mul1_pair (exact fp16 weights).
 template <int BITS, int CB, int MT, int P = 0>
 HX_INLINE void tile_mac(const uint32_t* w, const uint32_t (*xa)[8], float (*acc)[16])
 {
     if constexpr (P < 256) {
         using pos = hx_pos<P>;
-        hx_h2 v = hx_decode2<CB>(hx_window<BITS, P>(w), hx_window<BITS, P + 1>(w));
+        hx_h2 v;
+        if constexpr (CB == 2) v = hx_mul1_pair<BITS, P>(w);
+        else v = hx_decode2<CB>(hx_window<BITS, P>(w), hx_window<BITS, P + 1>(w));
 #pragma unroll
         for (int m = 0; m < MT; ++m)
             acc[m][pos::n] = __builtin_amdgcn_fdot2(v, u32_as_h2(xa[m][pos::kp]), acc[m][pos::n], false);
@@ -168,32 +173,39 @@ __device__ void gemv_split_sum(const GemvArgs& g, int cg, int s, uint32_t* a_lds
     __syncthreads();
 }
 
+// Cross-workgroup handoff of split-K partials.  An agent-scope release/acquire fence pair would
+// write back and invalidate the whole L2 of the XCD on every arrival, which costs tens of
+// microseconds per launch at thousands of workgroups.  Instead the partials themselves are
+// device-coherent (agent-scope atomic stores and loads bypass the non-coherent cache levels), the
+// workgroup waits for its stores to complete before it counts its arrival, and the arrival counter
+// is a device-scope atomic.
+
 // Store this split's partial (rows < M) to partial[s][m][cg*128 + c].
 template <int MT>
 HX_INLINE void publish_partial(float* partial, int M, int N, int cg, int s, const float* colsum)
 {
     for (int i = threadIdx.x; i < MT * 128; i += GEMV_THREADS) {
         const int m = i >> 7, c = i & 127;
-        if (m < M) partial[((size_t)s * M + m) * N + cg * 128 + c] = colsum[i];
+        if (m < M)
+            __hip_atomic_store(&partial[((size_t)s * M + m) * N + cg * 128 + c], colsum[i], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-// Release this workgroup's global writes and count its arrival; true for the last of `target`
-// arrivals, which also resets the counter (acquire side included).
+// Count this workgroup's arrival after its device-coherent stores completed; true for the last of
+// `target` arrivals, which also resets the counter for the next call.
 __device__ inline bool arrive_last(int* counter, int target)
 {
     __shared__ int last;
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0);  // every outstanding memory operation of this wave has completed
     __syncthreads();
     if (threadIdx.x == 0) {
-        int old = hx_atomic_add_acqrel(counter, 1);
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = (old == target - 1);
-        if (last) hx_atomic_store_relaxed(counter, 0);
+        if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    bool r = last;
-    if (r) __threadfence();
-    return r;
+    return last;
 }
 
 // colsum[m][c] = sum over splits (in split order) of partial[s][m][cg*128 + c].
@@ -205,7 +217,8 @@ HX_INLINE void gather_partials(const float* partial, int M, int N, int splits, i
         float v = 0.0f;
         if (m < M)
             for (int sp = 0; sp < splits; ++sp)
-                v += __builtin_nontemporal_load(&partial[((size_t)sp * M + m) * N + cg * 128 + c]);
+                v += __hip_atomic_load(&partial[((size_t)sp * M + m) * N + cg * 128 + c], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
         colsum[i] = v;
     }
     __syncthreads();

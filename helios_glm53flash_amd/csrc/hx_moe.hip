@@ -5,6 +5,8 @@
 #include "hx_kernels.hpp"
 #include "hx_moe.hpp"
 
+#include <stdlib.h>
+
 namespace hx {
 
 hipError_t launch_moe_decode_phase_m1(const MoeDecodeArgs& a, int cb, bool gu, int bits, hipStream_t st);
@@ -34,12 +36,16 @@ static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Split-K plan for `groups` column groups over K: each split covers >= 4 k-blocks of 128 (one
 // 8-tile step for each of the 4 waves) and the grid aims at >= 2048 workgroups.
-static void split_plan(int K, int groups, int* splits, int* kc)
+static void split_plan(int K, int groups, int* splits, int* kc, const char* env)
 {
     const int kblocks = K / 128;
     int max_s = kblocks / 4 > 0 ? kblocks / 4 : 1;
     int want = (2048 + groups - 1) / groups;
     int s = want < max_s ? want : max_s;
+    if (const char* v = getenv(env)) {  // tuning override: fixed number of K splits
+        int f = atoi(v);
+        if (f > 0) s = f < kblocks ? f : kblocks;
+    }
     if (s < 1) s = 1;
     const int per = (kblocks + s - 1) / s;
     *splits = (kblocks + per - 1) / per;
@@ -56,8 +62,8 @@ void MoeWs::plan(int T_, int hidden_, int inter_, int E_, int topk_, bool shared
     R = T * topk;
     routed_slots = R < E ? R : E;
     slots = routed_slots + 1;
-    split_plan(hidden, slots * 2 * (inter / 128), &splits_gu, &kc_gu);
-    split_plan(inter, slots * (hidden / 128), &splits_d, &kc_d);
+    split_plan(hidden, slots * 2 * (inter / 128), &splits_gu, &kc_gu, "HX_MOE_SPLITS_GU");
+    split_plan(inter, slots * (hidden / 128), &splits_d, &kc_d, "HX_MOE_SPLITS_D");
     size_t o = HX_COUNTER_BYTES;
     off_idx = o;      o = al(o + sizeof(int64_t) * R);
     off_w = o;        o = al(o + sizeof(_Float16) * R);
