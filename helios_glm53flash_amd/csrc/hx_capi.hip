@@ -127,7 +127,7 @@ int hx_workspace_init(void* workspace, size_t bytes, hx_stream_t stream)
 size_t hx_exl3_gemm_workspace_size(int M, int N, int K)
 {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
-    if (M <= 8) return hx::gemv_workspace_bytes(M, K, N);
+    if (M <= hx::GEMV_MAX_M) return hx::gemv_workspace_bytes(M, K, N);
     return hx::HX_COUNTER_BYTES + align256((size_t)M * K * sizeof(_Float16));
 }
 
@@ -145,7 +145,7 @@ int hx_exl3_gemm(void* y, const void* x, const hx_group_words* w, int M, int N, 
     const uint16_t* tr = static_cast<const uint16_t*>(w->trellis);
     const _Float16* suh = static_cast<const _Float16*>(w->suh);
     const _Float16* svh = static_cast<const _Float16*>(w->svh);
-    if (M <= 8) {
+    if (M <= hx::GEMV_MAX_M) {
         if (!workspace || workspace_bytes < hx::gemv_workspace_bytes(M, K, N))
             return fail(HX_ERR_WORKSPACE, "hx_exl3_gemm: workspace smaller than hx_exl3_gemm_workspace_size");
         int r = hip_status(hx::launch_linear_gemv(xh, tr, suh, svh, y, M, K, N, bits, cb, y_fp32 != 0, workspace, st),
@@ -269,6 +269,21 @@ void fill_tables(const hx_expert_tables* t, const void* const* (&tr)[3], const v
     uni[0] = Kg; uni[1] = Ku; uni[2] = Kd;
 }
 
+int max_bits_of(const hx_expert_tables* t, int Kg, int Ku, int Kd, const int* shared_bits)
+{
+    int m = 0;
+    if (t->gate_bits) {
+        for (int b = 1; b <= 8; ++b)
+            if (t->bits_mask & (1u << b)) m = b;
+    } else {
+        m = Kg > Ku ? Kg : Ku;
+        m = m > Kd ? m : Kd;
+    }
+    if (shared_bits)
+        for (int i = 0; i < 3; ++i) m = shared_bits[i] > m ? shared_bits[i] : m;
+    return m;
+}
+
 uint32_t phase_mask(const hx_expert_tables* t, int Ka, int Kb)
 {
     if (t->gate_bits) return t->bits_mask;
@@ -298,31 +313,32 @@ int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const i
         return fail(HX_ERR_INVALID, "hx_moe_grouped: y and route_to_sorted are needed without sorted_contributions");
     if (tokens == 0) return 0;
     hx::MoeWs L;
-    L.plan(tokens, hidden_dim, intermediate_dim, num_experts, topk, false);
+    L.plan(tokens, hidden_dim, intermediate_dim, num_experts, topk, false,
+           max_bits_of(tables, K_gate, K_up, K_down, nullptr));
     if (!workspace || workspace_bytes < L.total) return fail(HX_ERR_WORKSPACE, "hx_moe_grouped: workspace too small");
     char* base = static_cast<char*>(workspace);
     hipStream_t st = (hipStream_t)stream;
     const int cb = mcg ? 1 : 2;
     const _Float16* xh = static_cast<const _Float16*>(x);
     const _Float16* ws_sorted = static_cast<const _Float16*>(weight_sorted);
-    if (tokens <= 8) {
+    if (L.few_tokens()) {
         hx::MoeDecodeArgs a = L.decode_args(base);
         a.x = xh;
         a.expert_count = expert_count;
         a.token_sorted = token_sorted;
         a.weight_sorted = ws_sorted;
+        a.route_to_sorted = route_to_sorted;
         fill_tables(tables, a.tr, a.suh, a.svh, a.bits_tab, a.bits_uniform, K_gate, K_up, K_down);
         a.act_limit = act_limit;
-        float* contrib = sorted_contributions ? sorted_contributions : reinterpret_cast<float*>(base + L.off_contrib);
-        a.contrib = contrib;
-        int r = hip_status(hx::run_moe_decode(a, cb, phase_mask(tables, K_gate, K_up), phase_mask(tables, K_down, 0), st),
-                           "hx_moe_grouped(decode)");
-        if (r) return r;
-        if (!sorted_contributions)
-            r = hip_status(hx::launch_moe_combine(contrib, route_to_sorted, tokens, topk, hidden_dim, false, nullptr, y,
-                                                  true, st),
-                           "hx_moe_grouped(reduce)");
-        return r;
+        if (sorted_contributions) {
+            a.contrib = sorted_contributions;
+        } else {
+            a.combine = true;
+            a.y_routed = y;
+            a.y_accumulate = true;
+        }
+        return hip_status(hx::run_moe_decode(a, cb, phase_mask(tables, K_gate, K_up), phase_mask(tables, K_down, 0), st),
+                          "hx_moe_grouped(decode)");
     }
     hx::PrefillArgs p{};
     p.x = xh;
@@ -368,7 +384,8 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
     }
     if (tokens == 0) return 0;
     hx::MoeWs L;
-    L.plan(tokens, hidden_dim, intermediate_dim, num_experts, topk, shared != nullptr);
+    L.plan(tokens, hidden_dim, intermediate_dim, num_experts, topk, shared != nullptr,
+           max_bits_of(tables, K_gate, K_up, K_down, shared ? shared_bits : nullptr));
     if (!workspace || workspace_bytes < L.total) return fail(HX_ERR_WORKSPACE, "hx_moe_layer: workspace too small");
     char* base = static_cast<char*>(workspace);
     hipStream_t st = (hipStream_t)stream;
@@ -382,26 +399,12 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
     int64_t* r2s = reinterpret_cast<int64_t*>(base + L.off_r2s);
 
     int r;
-    {
-        Phase ph(0, st);
-        r = hip_status(hx::launch_routing(static_cast<const _Float16*>(scores), static_cast<const _Float16*>(bias), idx,
-                                          wt, tokens, num_experts, topk, routed_scale, st),
-                       "hx_moe_layer(routing)");
-    }
-    if (r) return r;
-    {
-        Phase ph(1, st);
-        r = hip_status(hx::launch_permute(idx, wt, tokens, topk, num_experts, cnt, ts, wsorted, r2s, nullptr, st),
-                       "hx_moe_layer(permute)");
-    }
-    if (r) return r;
-
-    if (tokens <= 8) {
+    if (L.few_tokens()) {
         hx::MoeDecodeArgs a = L.decode_args(base);
         a.x = xh;
-        a.expert_count = cnt;
-        a.token_sorted = ts;
-        a.weight_sorted = wsorted;
+        a.scores = static_cast<const _Float16*>(scores);
+        a.bias = static_cast<const _Float16*>(bias);
+        a.routed_scale = routed_scale;
         fill_tables(tables, a.tr, a.suh, a.svh, a.bits_tab, a.bits_uniform, K_gate, K_up, K_down);
         uint32_t mgu = phase_mask(tables, K_gate, K_up), md = phase_mask(tables, K_down, 0);
         if (shared) {
@@ -415,23 +418,32 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
             md |= 1u << shared_bits[2];
         }
         a.act_limit = act_limit;
-        float* contrib = reinterpret_cast<float*>(base + L.off_contrib);
-        a.contrib = contrib;
+        a.out_idx = idx;
+        a.out_w = wt;
+        a.combine = true;
+        a.y = static_cast<_Float16*>(y);
+        a.y_routed = y_routed;
         {
             Phase ph(2, st);
-            r = hip_status(hx::run_moe_decode(a, cb, mgu, 0, st), "hx_moe_layer(experts gate/up)");
+            r = hip_status(hx::run_moe_decode(a, cb, mgu, 0, st), "hx_moe_layer(router + experts gate/up)");
         }
         if (r) return r;
-        {
-            Phase ph(3, st);
-            r = hip_status(hx::run_moe_decode(a, cb, 0, md, st), "hx_moe_layer(experts down)");
-        }
-        if (r) return r;
-        Phase ph(4, st);
-        return hip_status(hx::launch_moe_combine(contrib, r2s, tokens, topk, hidden_dim, shared != nullptr,
-                                                 static_cast<_Float16*>(y), y_routed, false, st),
-                          "hx_moe_layer(combine)");
+        Phase ph(3, st);
+        return hip_status(hx::run_moe_decode(a, cb, 0, md, st), "hx_moe_layer(experts down + combine)");
     }
+    {
+        Phase ph(0, st);
+        r = hip_status(hx::launch_routing(static_cast<const _Float16*>(scores), static_cast<const _Float16*>(bias), idx,
+                                          wt, tokens, num_experts, topk, routed_scale, st),
+                       "hx_moe_layer(routing)");
+    }
+    if (r) return r;
+    {
+        Phase ph(1, st);
+        r = hip_status(hx::launch_permute(idx, wt, tokens, topk, num_experts, cnt, ts, wsorted, r2s, nullptr, st),
+                       "hx_moe_layer(permute)");
+    }
+    if (r) return r;
 
     const float* shared_rows = nullptr;
     if (shared) {

@@ -183,6 +183,30 @@ HX_INLINE void hx_had128_wave(float& v0, float& v1)
     v1 *= HX_RSQRT128;
 }
 
+// Workgroup barrier that waits only for this wave's LDS traffic (s_waitcnt lgkmcnt(0)), so global
+// loads issued before it stay in flight across the barrier.  The waitcnt immediate encodes
+// vmcnt = 63, expcnt = 7, lgkmcnt = 0 (gfx9 field layout).
+HX_INLINE void hx_lds_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Maximum of a u32 over the 64 lanes of a wave with DPP row shifts and row broadcasts (each step a
+// VALU op with a lane-permuted operand, no LDS round trip); every lane gets the result.
+HX_INLINE uint32_t hx_wave_max_u32(uint32_t v)
+{
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false));  // row_shr:1
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false));  // row_shr:2
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false));  // row_shr:4
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false));  // row_shr:8
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // ------------------------------------------------------------------ cross-agent handoff
 
 HX_INLINE int hx_atomic_add_acqrel(int* p, int v)

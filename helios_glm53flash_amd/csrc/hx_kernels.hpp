@@ -11,8 +11,11 @@ namespace hx {
 // zero, and no call ever stores data into it, so calls of different shapes can share a workspace.
 constexpr size_t HX_COUNTER_BYTES = 64 * 1024;
 
+// Largest M served by the decode-GEMV kernels (one MFMA row block); larger M uses the MFMA GEMM.
+constexpr int GEMV_MAX_M = 16;
+
 // small-M linear (hx_linear.hip)
-void gemv_plan(int M, int K, int N, int* splits, int* kc);
+void gemv_plan(int M, int K, int N, int bits, int* splits, int* kc);
 size_t gemv_workspace_bytes(int M, int K, int N);
 hipError_t launch_linear_gemv(const _Float16* x, const uint16_t* trellis, const _Float16* suh, const _Float16* svh,
                               void* y, int M, int K, int N, int bits, int cb, bool y_fp32, void* ws, hipStream_t st);

@@ -3,31 +3,35 @@
 #include "hx_gemv.hpp"
 #include "hx_kernels.hpp"
 
+#include <stdlib.h>
+
 namespace hx {
 
 template <int BITS>
 hipError_t launch_gemv_cb(int cb, const GemvArgs& g, const _Float16* svh, void* y, bool y_fp32, hipStream_t st);
 
-// Split-K plan: at least 4 tile-row steps of 8 tiles per split so every wave has work, and enough
-// workgroups (>= ~2048) to cover 256 CUs several times.
-void gemv_plan(int M, int K, int N, int* splits, int* kc)
+// Split-K plan: grid = (N / 128) column groups x (K / kc) splits.  kc grows until the grid would
+// drop below ~2 workgroups per CU; the activation block (M x kc fp16) stays within 32 KiB of LDS.
+void gemv_plan(int M, int K, int N, int bits, int* splits, int* kc)
 {
+    (void)bits;
     const int groups = N / 128;
-    const int kblocks = K / 128;                 // 128-wide k blocks
-    int max_splits = kblocks / 4 > 0 ? kblocks / 4 : 1;
-    int want = (2048 + groups - 1) / groups;
-    int s = want < max_splits ? want : max_splits;
-    if (s < 1) s = 1;
-    int blocks_per = (kblocks + s - 1) / s;
-    s = (kblocks + blocks_per - 1) / blocks_per;
-    *splits = s;
-    *kc = blocks_per * 128;
+    int cap = 16384 / (M < 1 ? 1 : M);
+    if (const char* v = getenv("HX_GEMV_KC")) cap = atoi(v) > 0 ? atoi(v) : cap;
+    int c = gemv_kc_for(K, cap);
+    while (c > 128 && (long)groups * (K / c) < 512) {
+        const int smaller = gemv_kc_for(K, c - 128);
+        if (smaller == c) break;
+        c = smaller;
+    }
+    *kc = c;
+    *splits = K / c;
 }
 
 size_t gemv_workspace_bytes(int M, int K, int N)
 {
     int s, kc;
-    gemv_plan(M, K, N, &s, &kc);
+    gemv_plan(M, K, N, 8, &s, &kc);
     return HX_COUNTER_BYTES + (size_t)s * M * N * sizeof(float);
 }
 
@@ -42,7 +46,7 @@ hipError_t launch_linear_gemv(const _Float16* x, const uint16_t* trellis, const 
     g.M = M;
     g.K = K;
     g.N = N;
-    gemv_plan(M, K, N, &g.splits, &g.kc);
+    gemv_plan(M, K, N, bits, &g.splits, &g.kc);
     if ((size_t)(N / 128) * sizeof(int) > HX_COUNTER_BYTES) return hipErrorInvalidValue;
     g.counter = static_cast<int*>(ws);
     g.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + HX_COUNTER_BYTES);

@@ -37,12 +37,11 @@ __global__ __launch_bounds__(GEMV_THREADS) void linear_gemv_kernel(GemvArgs g, c
                                                                   bool y_fp32)
 {
     extern __shared__ uint32_t a_lds[];
-    __shared__ float red[GEMV_WAVES * MT * 128];
     __shared__ float colsum[MT * 128];
     const int groups = g.N >> 7;
     const int cg = blockIdx.x % groups;
     const int s = blockIdx.x / groups;
-    gemv_split_sum<BITS, CB, MT>(g, cg, s, a_lds, red, colsum);
+    gemv_split_sum<BITS, CB, MT>(g, cg, s, a_lds, colsum);
     if (g.splits > 1) {
         publish_partial<MT>(g.partial, g.M, g.N, cg, s, colsum);
         if (!arrive_last(&g.counter[cg], g.splits)) return;
@@ -55,9 +54,9 @@ template <int BITS, int CB, int MT>
 hipError_t launch_gemv_t(const GemvArgs& g, const _Float16* svh, void* y, bool y_fp32, hipStream_t st)
 {
     const int groups = g.N >> 7;
-    size_t lds = (size_t)MT * g.kc * sizeof(_Float16);
-    hipLaunchKernelGGL((linear_gemv_kernel<BITS, CB, MT>), dim3(groups * g.splits), dim3(GEMV_THREADS), lds, st,
-                       g, svh, y, y_fp32);
+    const size_t lds = (size_t)MT * g.kc * sizeof(_Float16);
+    hipLaunchKernelGGL((linear_gemv_kernel<BITS, CB, MT>), dim3(groups * g.splits), dim3(GEMV_THREADS), lds, st, g,
+                       svh, y, y_fp32);
     return hipGetLastError();
 }
 
@@ -66,7 +65,8 @@ hipError_t launch_gemv_b(const GemvArgs& g, const _Float16* svh, void* y, bool y
 {
     if (g.M <= 1) return launch_gemv_t<BITS, CB, 1>(g, svh, y, y_fp32, st);
     if (g.M <= 4) return launch_gemv_t<BITS, CB, 4>(g, svh, y, y_fp32, st);
-    return launch_gemv_t<BITS, CB, 8>(g, svh, y, y_fp32, st);
+    if (g.M <= 8) return launch_gemv_t<BITS, CB, 8>(g, svh, y, y_fp32, st);
+    return launch_gemv_t<BITS, CB, 16>(g, svh, y, y_fp32, st);
 }
 
 template <int BITS>

@@ -13,46 +13,21 @@ hipError_t launch_moe_decode_phase_m1(const MoeDecodeArgs& a, int cb, bool gu, i
 hipError_t launch_moe_decode_phase_m4(const MoeDecodeArgs& a, int cb, bool gu, int bits, hipStream_t st);
 hipError_t launch_moe_decode_phase_m8(const MoeDecodeArgs& a, int cb, bool gu, int bits, hipStream_t st);
 
-// ------------------------------------------------------------------ combine
-
-// y[t][c] = fp16( (sum_j contrib[r2s[t*topk + j]][c], ascending j from +0) + shared[t][c] )
-// (glue2.cu:297-306 then runner.cpp:957-958); y_routed (optional) gets the fp32 routed sum, added to
-// its previous contents when accumulate is set (the reference's y += contributions contract).
-__global__ __launch_bounds__(256) void moe_combine_kernel(const float* contrib, const int64_t* r2s, int T, int topk,
-                                                         int hidden, bool has_shared, _Float16* y, float* y_routed,
-                                                         bool accumulate)
-{
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (size_t)T * hidden) return;
-    const int t = (int)(i / hidden), c = (int)(i % hidden);
-    float acc = 0.0f;
-    for (int j = 0; j < topk; ++j) acc += contrib[(size_t)r2s[(size_t)t * topk + j] * hidden + c];
-    if (y_routed) y_routed[i] = accumulate ? y_routed[i] + acc : acc;
-    if (has_shared) acc += contrib[((size_t)T * topk + t) * hidden + c];
-    if (y) y[i] = (_Float16)acc;
-}
-
 static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Split-K plan for `groups` column groups over K: each split covers >= 4 k-blocks of 128 (one
-// 8-tile step for each of the 4 waves) and the grid aims at >= 2048 workgroups.
-static void split_plan(int K, int groups, int* splits, int* kc, const char* env)
+// Split-K plan: K per split = largest multiple-of-128 divisor of K up to `cap` (HX_MOE_KC overrides
+// the cap for tuning); the activation block (8 x kc fp16) stays within LDS.
+static void split_plan(int K, int max_bits, int* splits, int* kc)
 {
-    const int kblocks = K / 128;
-    int max_s = kblocks / 4 > 0 ? kblocks / 4 : 1;
-    int want = (2048 + groups - 1) / groups;
-    int s = want < max_s ? want : max_s;
-    if (const char* v = getenv(env)) {  // tuning override: fixed number of K splits
-        int f = atoi(v);
-        if (f > 0) s = f < kblocks ? f : kblocks;
-    }
-    if (s < 1) s = 1;
-    const int per = (kblocks + s - 1) / s;
-    *splits = (kblocks + per - 1) / per;
-    *kc = per * 128;
+    (void)max_bits;
+    int cap = 1024;
+    if (const char* v = getenv("HX_MOE_KC")) cap = atoi(v) > 0 ? atoi(v) : cap;
+    if (cap > 2048) cap = 2048;
+    *kc = gemv_kc_for(K, cap);
+    *splits = K / *kc;
 }
 
-void MoeWs::plan(int T_, int hidden_, int inter_, int E_, int topk_, bool shared_)
+void MoeWs::plan(int T_, int hidden_, int inter_, int E_, int topk_, bool shared_, int max_bits)
 {
     T = T_;
     hidden = hidden_;
@@ -62,8 +37,8 @@ void MoeWs::plan(int T_, int hidden_, int inter_, int E_, int topk_, bool shared
     R = T * topk;
     routed_slots = R < E ? R : E;
     slots = routed_slots + 1;
-    split_plan(hidden, slots * 2 * (inter / 128), &splits_gu, &kc_gu, "HX_MOE_SPLITS_GU");
-    split_plan(inter, slots * (hidden / 128), &splits_d, &kc_d, "HX_MOE_SPLITS_D");
+    split_plan(hidden, max_bits, &splits_gu, &kc_gu);
+    split_plan(inter, max_bits, &splits_d, &kc_d);
     size_t o = HX_COUNTER_BYTES;
     off_idx = o;      o = al(o + sizeof(int64_t) * R);
     off_w = o;        o = al(o + sizeof(_Float16) * R);
@@ -71,7 +46,8 @@ void MoeWs::plan(int T_, int hidden_, int inter_, int E_, int topk_, bool shared
     off_tsorted = o;  o = al(o + sizeof(int64_t) * R);
     off_wsorted = o;  o = al(o + sizeof(_Float16) * R);
     off_r2s = o;      o = al(o + sizeof(int64_t) * R);
-    if (T <= 8) {
+    if (T <= 8 && R <= 64) {
+        off_plan = o;     o = al(o + sizeof(DecodePlan));
         off_pg = o;   o = al(o + sizeof(float) * slots * splits_gu * 8 * inter);
         off_pu = o;   o = al(o + sizeof(float) * slots * splits_gu * 8 * inter);
         off_pd = o;   o = al(o + sizeof(float) * slots * splits_d * 8 * hidden);
@@ -98,7 +74,10 @@ MoeDecodeArgs MoeWs::decode_args(char* base) const
     a.splits_d = splits_d;
     a.kc_d = kc_d;
     a.counter_gu = reinterpret_cast<int*>(base);
-    a.counter_d = reinterpret_cast<int*>(base) + 8192;
+    a.counter_d = reinterpret_cast<int*>(base) + 6144;
+    a.counter_y = reinterpret_cast<int*>(base) + 12288;
+    a.plan = reinterpret_cast<DecodePlan*>(base + off_plan);
+    a.contrib = reinterpret_cast<float*>(base + off_contrib);
     a.partial_g = reinterpret_cast<float*>(base + off_pg);
     a.partial_u = reinterpret_cast<float*>(base + off_pu);
     a.partial_d = reinterpret_cast<float*>(base + off_pd);
@@ -115,8 +94,9 @@ static hipError_t decode_phase(const MoeDecodeArgs& a, int cb, bool gu, int bits
 
 hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t mask_gu, uint32_t mask_d, hipStream_t st)
 {
-    if (a.T > 8) return hipErrorInvalidValue;
-    if (a.routed_slots + 1 > 8192 / (a.inter / 128) || a.routed_slots + 1 > 8192 / (a.hidden / 128))
+    if (a.T > 8 || a.T * a.topk > DEC_MAX_R) return hipErrorInvalidValue;
+    if ((a.routed_slots + 1) * (a.inter / 128) > 6144 || (a.routed_slots + 1) * (a.hidden / 128) > 6144 ||
+        a.hidden / 128 > 4096)
         return hipErrorInvalidValue;
     hipError_t e = hipSuccess;
     for (int b = 1; b <= 8 && e == hipSuccess; ++b)
@@ -126,14 +106,5 @@ hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t mask_gu, uint32_t m
     return e;
 }
 
-hipError_t launch_moe_combine(const float* contrib, const int64_t* r2s, int T, int topk, int hidden, bool has_shared,
-                              _Float16* y, float* y_routed, bool accumulate, hipStream_t st)
-{
-    const size_t n = (size_t)T * hidden;
-    if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, contrib, r2s, T, topk,
-                       hidden, has_shared, y, y_routed, accumulate);
-    return hipGetLastError();
-}
 
 }  // namespace hx

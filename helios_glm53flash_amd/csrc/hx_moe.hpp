@@ -16,7 +16,7 @@ struct MoeWs {
     int splits_gu = 1, kc_gu = 128, splits_d = 1, kc_d = 128;
     size_t off_idx = 0, off_w = 0, off_count = 0, off_tsorted = 0, off_wsorted = 0, off_r2s = 0;
     // few-token path
-    size_t off_pg = 0, off_pu = 0, off_pd = 0, off_act = 0, off_contrib = 0;
+    size_t off_plan = 0, off_pg = 0, off_pu = 0, off_pd = 0, off_act = 0, off_contrib = 0;
     // prefill path
     int max_jobs = 0;
     size_t off_jobs = 0, off_njobs = 0, off_row_expert = 0, off_xg = 0, off_xu = 0, off_G = 0, off_U = 0,
@@ -24,7 +24,8 @@ struct MoeWs {
     size_t prefill_end = 0;
     size_t total = 0;
 
-    void plan(int T, int hidden, int inter, int E, int topk, bool shared);
+    void plan(int T, int hidden, int inter, int E, int topk, bool shared, int max_bits = 8);
+    bool few_tokens() const { return T <= 8 && R <= 64; }
     void prefill_layout(size_t start);
     MoeDecodeArgs decode_args(char* base) const;
 };
@@ -48,8 +49,6 @@ struct PrefillArgs {
 };
 
 hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t mask_gu, uint32_t mask_d, hipStream_t st);
-hipError_t launch_moe_combine(const float* contrib, const int64_t* r2s, int T, int topk, int hidden, bool has_shared,
-                              _Float16* y, float* y_routed, bool accumulate, hipStream_t st);
 // Routed experts for T > 8 tokens: writes per-row fp32 contributions (sorted order) when contrib is
 // non-null, y = fp16(routed + shared_rows) when y is non-null, and the fp32 routed sum into
 // y_routed (added to its contents when accumulate) when y_routed is non-null.

@@ -1,51 +1,80 @@
-// hx_moe_decode.hpp -- fused MoE layer for few tokens (T <= 8) on gfx950: every active expert's
-// gate/up GEMV, the SiLU-gate, the down GEMV and the weighted contribution rows, with trellis decode
-// fused into the GEMVs, in two launches without host synchronisation.
+// hx_moe_decode.hpp -- fused MoE layer for few tokens (T <= 8, T*topk <= 64) on gfx950 in two
+// launches, without host synchronisation:
 //
-// Reference semantics: src/cuda/quant/exl3_moe_kernel.cuh:57-262 (per expert: gather, input
-// Hadamard with suh_g/suh_u, G/U GEMMs with fp16 outputs, guad epilogue, down GEMM with fp16
-// output, d epilogue with weight/sqrt(128) and svh_d), hadamard_inner.cuh:284-481, and for the
-// shared expert src/engine/runner.cpp:723-738 + glue2.cu:406-414.
+//   kernel A  router top-k + token-by-expert permutation (recomputed by every workgroup from the
+//             fp16 scores, a few hundred bytes), then one split-K slice of one expert's gate or up
+//             GEMV with the trellis decode fused; the last-arriving slice of a (slot, column group)
+//             runs the SiLU-gate epilogue and stores the down-projection input.
+//   kernel B  one split-K slice of one expert's down GEMV; the last slice of a (slot, column group)
+//             writes the weighted contribution rows; the last of all slots of a column group then
+//             reduces the contributions in routing-rank order, adds the shared expert and writes y.
 //
-// Slots: slot j < n_routed_slots is the j-th expert (in expert-index order) with a nonzero count in
-// expert_count (the reference's ticket numbering, exl3_moe_kernel.cuh:57-69); its rows are the
-// expert's sorted routing rows [start, start + count).  With a shared expert, one extra slot holds
-// all T tokens.  Each workgroup finds its slot's expert by a wave scan of expert_count, so the launch
-// grid is sized by the upper bound min(E, T*topk) and surplus workgroups exit.
+// Reference semantics: src/cuda/aux/routing.cu:211-329 (router), src/engine/glue2.cu:244-311
+// (permutation, ordered reduction), src/cuda/quant/exl3_moe_kernel.cuh:57-262 and
+// hadamard_inner.cuh:284-481 (experts), src/engine/runner.cpp:723-738,957-958 (shared expert,
+// combine).  Slot j is the j-th expert, in expert-index order, with a nonzero token count (the
+// reference's ticket numbering, exl3_moe_kernel.cuh:57-69); one extra slot holds the shared expert.
 #pragma once
 #include "hx_gemv.hpp"
 
 namespace hx {
 
+constexpr int DEC_MAX_R = 64;  // T * topk rows handled by the few-token path
+
+// Routing plan of one call: sorted rows and active-expert slots.
+struct DecodePlan {
+    int n;                     // active routed experts
+    int expert[DEC_MAX_R];
+    int start[DEC_MAX_R];
+    int count[DEC_MAX_R];
+    int token[DEC_MAX_R];      // token of sorted row r
+    float weight[DEC_MAX_R];   // routing weight of sorted row r
+    int r2s[DEC_MAX_R];        // flat routing index -> sorted row
+};
+
 struct MoeDecodeArgs {
     const _Float16* x;             // [T][hidden]
     int T, hidden, inter, E, topk;
+    // layer mode: router scores (fp16 [T][E]) and optional bias
+    const _Float16* scores;
+    const _Float16* bias;
+    float routed_scale;
+    // grouped mode (scores == null): the caller's permutation
     const int64_t* expert_count;   // [E+1]
     const int64_t* token_sorted;   // [T*topk]
     const _Float16* weight_sorted; // [T*topk]
+    const int64_t* route_to_sorted;// [T*topk] (needed only when combining)
     // routed expert tables (device arrays of device pointers), per-expert bits (nullable)
     const void* const* tr[3];
     const void* const* suh[3];
     const void* const* svh[3];
     const int32_t* bits_tab[3];
     int bits_uniform[3];
-    // shared expert (nullable trellis -> none)
+    // shared expert (null trellis -> none)
     const void* sh_tr[3];
     const void* sh_suh[3];
     const void* sh_svh[3];
     int sh_bits[3];
     float act_limit;
-    int routed_slots;              // upper bound of active experts
+    int routed_slots;              // upper bound of active experts = min(E, T*topk)
     int splits_gu, kc_gu, splits_d, kc_d;
     // workspace
     int* counter_gu;               // [slots][inter/128]
     int* counter_d;                // [slots][hidden/128]
+    int* counter_y;                // [hidden/128]
     float* partial_g;              // [slots][splits_gu][8][inter]
     float* partial_u;
     float* partial_d;              // [slots][splits_d][8][hidden]
     _Float16* act;                 // [slots][8][inter]  (down-projection input, already transformed)
+    DecodePlan* plan;              // written by workgroup 0 of kernel A
     // outputs
+    int64_t* out_idx;              // optional router outputs [T][topk]
+    _Float16* out_w;
     float* contrib;                // [T*topk (+ T)][hidden]: sorted routed rows, then shared rows
+    bool combine;                  // kernel B reduces contributions into y / y_routed
+    _Float16* y;                   // fp16(routed + shared), optional
+    float* y_routed;               // fp32 routed sum, optional
+    bool y_accumulate;             // y_routed += sum instead of =
 };
 
 struct SlotInfo {
@@ -55,43 +84,229 @@ struct SlotInfo {
     bool valid;
 };
 
-// Wave-uniform scan of expert_count for the slot-th active expert.
-HX_INLINE SlotInfo find_slot(const MoeDecodeArgs& a, int slot)
+HX_INLINE float sigmoid_stable(float x)
+{
+    const float ez = __expf(-fabsf(x));
+    const float base = ez / (1.0f + ez);
+    return x >= 0.0f ? 1.0f - base : base;
+}
+
+// Top-k of one token's scores by one wave (routing.cu:211-329: key = logit, or sigmoid + bias;
+// larger first under the monotone unsigned encoding of the fp32 key, ties to the lower index;
+// weights sigmoid(payload) * scale / (sum + 1e-20) rounded to fp16).  Lane k < topk returns
+// selection k in (e, w).
+HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, int topk, float scale, int& e_out,
+                         float& w_out)
+{
+    const int lane = threadIdx.x & 63;
+    if (!bias) {
+        // key = the fp16 logit itself: its monotone 16-bit encoding and the complemented index fit
+        // one u32 (larger = higher logit, then lower index; +0 above -0 as in the fp32 encoding)
+        constexpr int PER = 8;  // E <= 512
+        uint32_t cand[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int e = lane + 64 * i;
+            uint32_t c = 0;
+            if (e < E) {
+                uint32_t h = h_as_u16(scores[e]);
+                h = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+                c = (h << 16) | (0xffffu - (uint32_t)e);
+            }
+            cand[i] = c;
+        }
+        float sum = 0.0f;
+        e_out = 0;
+        w_out = 0.0f;
+        for (int k = 0; k < topk; ++k) {
+            uint32_t best = cand[0];
+#pragma unroll
+            for (int i = 1; i < PER; ++i) best = max(best, cand[i]);
+            best = hx_wave_max_u32(best);
+#pragma unroll
+            for (int i = 0; i < PER; ++i)
+                if (cand[i] == best) cand[i] = 0;
+            uint32_t h = best >> 16;
+            h = (h & 0x8000u) ? (h & 0x7fffu) : (~h & 0xffffu);
+            const float o = sigmoid_stable((float)u16_as_h((uint16_t)h));
+            sum += o;
+            if (lane == k) {
+                e_out = (int)(0xffffu - (best & 0xffffu));
+                w_out = o;
+            }
+        }
+        sum += 1e-20f;
+        w_out = (float)(_Float16)(w_out * scale / sum);
+        return;
+    }
+    constexpr int PER = 8;  // E <= 512
+    uint64_t cand[PER];
+    float payload[PER];
+    _Float16 sv[PER], bv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = lane + 64 * i;
+        sv[i] = e < E ? scores[e] : (_Float16)0.0f;
+        bv[i] = (bias && e < E) ? bias[e] : (_Float16)0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = lane + 64 * i;
+        cand[i] = 0;
+        payload[i] = 0.0f;
+        if (e < E) {
+            const float logit = (float)sv[i];
+            float key = logit;
+            payload[i] = logit;
+            if (bias) {
+                payload[i] = sigmoid_stable(logit);
+                key = payload[i] + (float)bv[i];
+            }
+            uint32_t u = __float_as_uint(key);
+            u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+            cand[i] = ((uint64_t)u << 32) | (uint64_t)(0xfffffu - (uint32_t)e + 1u);
+        }
+    }
+    float sum = 0.0f;
+    e_out = 0;
+    w_out = 0.0f;
+    for (int k = 0; k < topk; ++k) {
+        uint64_t best = 0;
+        float best_p = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (cand[i] > best) {
+                best = cand[i];
+                best_p = payload[i];
+            }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const uint64_t ob = __shfl_xor(best, m, 64);
+            const float op = __shfl_xor(best_p, m, 64);
+            if (ob > best) {
+                best = ob;
+                best_p = op;
+            }
+        }
+        const int e = (int)(0xfffffu + 1u - (uint32_t)(best & 0xffffffffu));
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (cand[i] == best) cand[i] = 0;
+        const float o = bias ? best_p : sigmoid_stable(best_p);
+        sum += o;
+        if (lane == k) {
+            e_out = e;
+            w_out = o;
+        }
+    }
+    sum += 1e-20f;
+    w_out = (float)(_Float16)(w_out * scale / sum);
+}
+
+// Build the plan in LDS (every workgroup computes the same plan).  Layer mode routes the tokens;
+// grouped mode reads the caller's expert_count / token_sorted / weight_sorted.
+__device__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p)
+{
+    __shared__ int sel_e[DEC_MAX_R];
+    __shared__ float sel_w[DEC_MAX_R];
+    __shared__ int first[DEC_MAX_R];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int R = a.T * a.topk;
+    if (a.scores) {
+        for (int t = wave; t < a.T; t += GEMV_WAVES) {
+            int e;
+            float w;
+            wave_topk(a.scores + (size_t)t * a.E, a.bias, a.E, a.topk, a.routed_scale, e, w);
+            if (lane < a.topk) {
+                sel_e[t * a.topk + lane] = e;
+                sel_w[t * a.topk + lane] = w;
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            // stable counting sort of the R <= 64 selections by expert (ascending flat index within an
+            // expert, glue2.cu:244-293 with a deterministic cursor)
+            const int i = lane;
+            const int ei = i < R ? sel_e[i] : 0x7fffffff;
+            int less = 0, eqb = 0, cnt = 0;
+            for (int j = 0; j < R; ++j) {
+                const int ej = sel_e[j];
+                less += ej < ei;
+                eqb += (ej == ei) && (j < i);
+                cnt += ej == ei;
+            }
+            if (i < R) first[i] = eqb == 0;
+            __builtin_amdgcn_wave_barrier();
+            int dless = 0;
+            for (int j = 0; j < R; ++j) dless += first[j] && sel_e[j] < ei;
+            if (i < R) {
+                const int pos = less + eqb;
+                p.token[pos] = i / a.topk;
+                p.weight[pos] = sel_w[i];
+                p.r2s[i] = pos;
+                if (eqb == 0) {
+                    p.expert[dless] = ei;
+                    p.start[dless] = less;
+                    p.count[dless] = cnt;
+                }
+            }
+            const uint64_t fm = __ballot(i < R && eqb == 0);
+            if (lane == 0) p.n = __popcll(fm);
+        }
+    } else {
+        if (wave == 0) {
+            // active experts in index order from expert_count (all loads issued together)
+            constexpr int PER = 8;
+            int c[PER];
+#pragma unroll
+            for (int q = 0; q < PER; ++q) {
+                const int e = lane + 64 * q;
+                c[q] = e < a.E ? (int)a.expert_count[e] : 0;
+            }
+            int seen = 0, base = 0;
+#pragma unroll
+            for (int q = 0; q < PER; ++q) {
+                int cs = c[q];
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int v = __shfl_up(cs, o, 64);
+                    if (lane >= o) cs += v;
+                }
+                const uint64_t act = __ballot(c[q] > 0);
+                const int before = __popcll(act & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
+                if (c[q] > 0 && seen + before < DEC_MAX_R) {
+                    // clamp to the R sorted rows so an inconsistent expert_count cannot index past them
+                    const int st = min(base + cs - c[q], R);
+                    p.expert[seen + before] = lane + 64 * q;
+                    p.start[seen + before] = st;
+                    p.count[seen + before] = min(c[q], R - st);
+                }
+                seen += __popcll(act);
+                base += __shfl(cs, 63, 64);
+            }
+            if (lane == 0) p.n = min(seen, DEC_MAX_R);
+            if (lane < R) {
+                p.token[lane] = min(max((int)a.token_sorted[lane], 0), a.T - 1);
+                p.weight[lane] = (float)a.weight_sorted[lane];
+                p.r2s[lane] = a.route_to_sorted ? min(max((int)a.route_to_sorted[lane], 0), R - 1) : lane;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+HX_INLINE SlotInfo slot_info(const MoeDecodeArgs& a, const DecodePlan& p, int slot)
 {
     SlotInfo si{0, 0, 0, false};
-    if (slot == a.routed_slots) {  // shared
+    if (slot == a.routed_slots) {
         si.expert = -1;
-        si.start = 0;
         si.count = a.T;
         si.valid = a.sh_tr[0] != nullptr;
-        return si;
-    }
-    const int lane = threadIdx.x & 63;
-    int seen = 0, base = 0;
-    for (int e0 = 0; e0 < a.E; e0 += 64) {
-        const int e = e0 + lane;
-        const int c = e < a.E ? (int)a.expert_count[e] : 0;
-        // inclusive scan of counts and of "active" flags across the wave
-        int cs = c;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            int v = __shfl_up(cs, o, 64);
-            if (lane >= o) cs += v;
-        }
-        const uint64_t act = __ballot(c > 0);
-        const int before = __popcll(act & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
-        const bool hit = c > 0 && seen + before == slot;
-        const uint64_t hm = __ballot(hit);
-        if (hm) {
-            const int l = __ffsll((unsigned long long)hm) - 1;
-            si.expert = e0 + l;
-            si.start = base + __shfl(cs - c, l, 64);
-            si.count = __shfl(c, l, 64);
-            si.valid = true;
-            return si;
-        }
-        seen += __popcll(act);
-        base += __shfl(cs, 63, 64);
+    } else if (slot < p.n) {
+        si.expert = p.expert[slot];
+        si.start = p.start[slot];
+        si.count = p.count[slot];
+        si.valid = si.count > 0;
     }
     return si;
 }
@@ -105,7 +320,7 @@ HX_INLINE int proj_bits(const MoeDecodeArgs& a, int proj, int expert)
 // ------------------------------------------------------------------ kernel A: gate/up + SiLU-gate
 
 // guad epilogue for rows m < count of one 128-column group (hadamard_inner.cuh:284-413 for routed
-// experts; swiglu_clamp + down-input transform for the shared expert).
+// experts; swiglu_clamp + down-input transform for the shared expert, runner.cpp:723-738).
 template <int MT>
 __device__ void guad_epilogue(const MoeDecodeArgs& a, const SlotInfo& si, int slot, int cg, const float* cs_g,
                               const float* cs_u)
@@ -164,9 +379,10 @@ template <int BITS, int CB, int MT>
 __global__ __launch_bounds__(GEMV_THREADS) void moe_decode_gu_kernel(MoeDecodeArgs a)
 {
     extern __shared__ uint32_t a_lds[];
-    __shared__ float red[GEMV_WAVES * MT * 128];
     __shared__ float cs_g[MT * 128];
     __shared__ float cs_u[MT * 128];
+    __shared__ DecodePlan plan;
+    __shared__ int rows[8];
     const int groups = a.inter >> 7;
     const int per_slot = 2 * groups * a.splits_gu;
     const int slot = blockIdx.x / per_slot;
@@ -175,14 +391,41 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_decode_gu_kernel(MoeDecodeAr
     r %= 2 * groups;
     const int proj = r / groups;  // 0 gate, 1 up
     const int cg = r % groups;
-    const SlotInfo si = find_slot(a, slot);
+
+    build_plan(a, plan);
+    if (blockIdx.x == 0) {
+        // publish the plan (and the router outputs) for kernel B and the caller
+        const int R = a.T * a.topk;
+        for (int i = threadIdx.x; i < R; i += GEMV_THREADS) {
+            a.plan->token[i] = plan.token[i];
+            a.plan->weight[i] = plan.weight[i];
+            a.plan->r2s[i] = plan.r2s[i];
+            a.plan->expert[i] = plan.expert[i];
+            a.plan->start[i] = plan.start[i];
+            a.plan->count[i] = plan.count[i];
+        }
+        if (threadIdx.x == 0) a.plan->n = plan.n;
+        if (a.out_idx)
+            for (int i = threadIdx.x; i < R; i += GEMV_THREADS) {
+                const int pos = plan.r2s[i];
+                int e = 0;
+                for (int q = 0; q < plan.n; ++q)
+                    if (pos >= plan.start[q] && pos < plan.start[q] + plan.count[q]) e = plan.expert[q];
+                a.out_idx[i] = e;
+                a.out_w[i] = (_Float16)plan.weight[pos];
+            }
+    }
+    const SlotInfo si = slot_info(a, plan, slot);
     if (!si.valid) return;
     if (proj_bits(a, proj, si.expert) != BITS) return;
     const bool shared = si.expert < 0;
+    if (threadIdx.x < 8)
+        rows[threadIdx.x] = shared ? (int)threadIdx.x : plan.token[si.start + min((int)threadIdx.x, si.count - 1)];
+    __syncthreads();
 
     GemvArgs g;
     g.x = a.x;
-    g.rows = shared ? nullptr : a.token_sorted + si.start;
+    g.rows = rows;
     g.trellis = static_cast<const uint16_t*>(shared ? a.sh_tr[proj] : a.tr[proj][si.expert]);
     g.suh = static_cast<const _Float16*>(shared ? a.sh_suh[proj] : a.suh[proj][si.expert]);
     g.M = si.count;
@@ -194,7 +437,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_decode_gu_kernel(MoeDecodeAr
     float* partial = (proj == 0 ? a.partial_g : a.partial_u) + (size_t)slot * a.splits_gu * 8 * a.inter;
     g.partial = partial;
 
-    gemv_split_sum<BITS, CB, MT>(g, cg, s, a_lds, red, cs_g);
+    gemv_split_sum<BITS, CB, MT>(g, cg, s, a_lds, cs_g);
     publish_partial<MT>(partial, g.M, g.N, cg, s, cs_g);
     if (!arrive_last(&a.counter_gu[slot * groups + cg], 2 * a.splits_gu)) return;
     gather_partials<MT>(a.partial_g + (size_t)slot * a.splits_gu * 8 * a.inter, g.M, g.N, a.splits_gu, cg, cs_g);
@@ -202,10 +445,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_decode_gu_kernel(MoeDecodeAr
     guad_epilogue<MT>(a, si, slot, cg, cs_g, cs_u);
 }
 
-// ------------------------------------------------------------------ kernel B: down + contributions
+// ------------------------------------------------------------------ kernel B: down + contributions + combine
 
+// Weighted contribution rows of one 128-column group (hadamard_inner.cuh:418-481: D rounded to fp16,
+// transform, times weight / sqrt(128) and svh_d in fp32; the shared expert keeps D in fp32).
 template <int MT>
-__device__ void down_epilogue(const MoeDecodeArgs& a, const SlotInfo& si, int cg, const float* cs)
+__device__ void down_epilogue(const MoeDecodeArgs& a, const DecodePlan& p, const SlotInfo& si, int cg,
+                              const float* cs)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = cg * 128 + 2 * lane;
@@ -217,10 +463,9 @@ __device__ void down_epilogue(const MoeDecodeArgs& a, const SlotInfo& si, int cg
         float d0, d1, wgt;
         size_t row;
         if (!shared) {
-            // D as fp16 (reference GEMM output), transform, times weight / sqrt(128) and svh_d in fp32
             d0 = (float)(_Float16)cs[m * 128 + 2 * lane];
             d1 = (float)(_Float16)cs[m * 128 + 2 * lane + 1];
-            wgt = (float)a.weight_sorted[si.start + m];
+            wgt = p.weight[si.start + m];
             row = (size_t)(si.start + m);
         } else {
             d0 = cs[m * 128 + 2 * lane];
@@ -231,7 +476,30 @@ __device__ void down_epilogue(const MoeDecodeArgs& a, const SlotInfo& si, int cg
         hx_had128_wave(d0, d1);
         d0 = d0 * wgt * (float)sd.x;
         d1 = d1 * wgt * (float)sd.y;
-        *reinterpret_cast<float2*>(a.contrib + row * a.hidden + c) = make_float2(d0, d1);
+        float* dst = a.contrib + row * a.hidden + c;
+        __hip_atomic_store(dst, d0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(dst + 1, d1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// y[t][c] = fp16((sum_j contrib[r2s[t*topk + j]][c], ascending j from +0) + shared[t][c])
+// (glue2.cu:297-306 then runner.cpp:957-958) for one 128-column group.
+__device__ void combine_columns(const MoeDecodeArgs& a, const DecodePlan& p, int cg, bool has_shared)
+{
+    const int R = a.T * a.topk;
+    for (int i = threadIdx.x; i < a.T * 128; i += GEMV_THREADS) {
+        const int t = i >> 7;
+        const int c = cg * 128 + (i & 127);
+        float acc = 0.0f;
+        for (int j = 0; j < a.topk; ++j)
+            acc += __hip_atomic_load(a.contrib + (size_t)p.r2s[t * a.topk + j] * a.hidden + c, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        const size_t o = (size_t)t * a.hidden + c;
+        if (a.y_routed) a.y_routed[o] = a.y_accumulate ? a.y_routed[o] + acc : acc;
+        if (has_shared)
+            acc += __hip_atomic_load(a.contrib + (size_t)(R + t) * a.hidden + c, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        if (a.y) a.y[o] = (_Float16)acc;
     }
 }
 
@@ -239,15 +507,28 @@ template <int BITS, int CB, int MT>
 __global__ __launch_bounds__(GEMV_THREADS) void moe_decode_d_kernel(MoeDecodeArgs a)
 {
     extern __shared__ uint32_t a_lds[];
-    __shared__ float red[GEMV_WAVES * MT * 128];
     __shared__ float cs[MT * 128];
+    __shared__ DecodePlan plan;
     const int groups = a.hidden >> 7;
     const int per_slot = groups * a.splits_d;
     const int slot = blockIdx.x / per_slot;
     const int r = blockIdx.x % per_slot;
     const int s = r / groups;
     const int cg = r % groups;
-    const SlotInfo si = find_slot(a, slot);
+
+    // plan from kernel A
+    const int R = a.T * a.topk;
+    for (int i = threadIdx.x; i < R; i += GEMV_THREADS) {
+        plan.token[i] = a.plan->token[i];
+        plan.weight[i] = a.plan->weight[i];
+        plan.r2s[i] = a.plan->r2s[i];
+        plan.expert[i] = a.plan->expert[i];
+        plan.start[i] = a.plan->start[i];
+        plan.count[i] = a.plan->count[i];
+    }
+    if (threadIdx.x == 0) plan.n = a.plan->n;
+    __syncthreads();
+    const SlotInfo si = slot_info(a, plan, slot);
     if (!si.valid) return;
     if (proj_bits(a, 2, si.expert) != BITS) return;
     const bool shared = si.expert < 0;
@@ -266,13 +547,17 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_decode_d_kernel(MoeDecodeArg
     float* partial = a.partial_d + (size_t)slot * a.splits_d * 8 * a.hidden;
     g.partial = partial;
 
-    gemv_split_sum<BITS, CB, MT>(g, cg, s, a_lds, red, cs);
+    gemv_split_sum<BITS, CB, MT>(g, cg, s, a_lds, cs);
     if (a.splits_d > 1) {
         publish_partial<MT>(partial, g.M, g.N, cg, s, cs);
         if (!arrive_last(&a.counter_d[slot * groups + cg], a.splits_d)) return;
         gather_partials<MT>(partial, g.M, g.N, a.splits_d, cg, cs);
     }
-    down_epilogue<MT>(a, si, cg, cs);
+    down_epilogue<MT>(a, plan, si, cg, cs);
+    if (!a.combine) return;
+    const bool has_shared = a.sh_tr[0] != nullptr;
+    if (!arrive_last(&a.counter_y[cg], plan.n + (has_shared ? 1 : 0))) return;
+    combine_columns(a, plan, cg, has_shared);
 }
 
 }  // namespace hx

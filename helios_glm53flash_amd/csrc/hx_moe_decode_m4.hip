@@ -8,15 +8,11 @@ template <int BITS, int CB>
 static void launch_pair(const MoeDecodeArgs& a, bool gu, hipStream_t st)
 {
     const int slots = a.routed_slots + 1;
-    if (gu) {
-        const int blocks = slots * 2 * (a.inter / 128) * a.splits_gu;
-        hipLaunchKernelGGL((moe_decode_gu_kernel<BITS, CB, 4>), dim3(blocks), dim3(GEMV_THREADS),
-                           (size_t)4 * a.kc_gu * sizeof(_Float16), st, a);
-    } else {
-        const int blocks = slots * (a.hidden / 128) * a.splits_d;
-        hipLaunchKernelGGL((moe_decode_d_kernel<BITS, CB, 4>), dim3(blocks), dim3(GEMV_THREADS),
-                           (size_t)4 * a.kc_d * sizeof(_Float16), st, a);
-    }
+    const int kc = gu ? a.kc_gu : a.kc_d;
+    const int blocks = gu ? slots * 2 * (a.inter / 128) * a.splits_gu : slots * (a.hidden / 128) * a.splits_d;
+    const size_t lds = (size_t)4 * kc * sizeof(_Float16);
+    if (gu) hipLaunchKernelGGL((moe_decode_gu_kernel<BITS, CB, 4>), dim3(blocks), dim3(GEMV_THREADS), lds, st, a);
+    else hipLaunchKernelGGL((moe_decode_d_kernel<BITS, CB, 4>), dim3(blocks), dim3(GEMV_THREADS), lds, st, a);
 }
 
 template <int CB>

@@ -17,6 +17,7 @@ import torch
 from ._lib import GroupWordsC, HX_GEMM_PATH_GEMV, HX_GEMM_PATH_MFMA, HxError, check, lib
 
 MUL1 = 0x83DCD12D
+GEMV_MAX_M = 16  # largest M served by the fused decode-GEMV (one MFMA row block)
 MUL1_I32 = MUL1 - (1 << 32)  # the int32 value stored in checkpoints
 
 
@@ -100,7 +101,7 @@ def gemm(y: torch.Tensor, x: torch.Tensor, w: GroupWords, M: int, N: int, K: int
     if a_had is not None:
         _need(a_had, "a_had", (torch.float16,))
     nbytes = lib.hx_exl3_gemm_workspace_size(M, N, K)
-    ws = workspace(nbytes, x.device) if (M <= 8 or a_had is None) else None
+    ws = workspace(nbytes, x.device) if (M <= GEMV_MAX_M or a_had is None) else None
     gw = w.c()
     return check(lib.hx_exl3_gemm(y.data_ptr(), x.data_ptr(), C.byref(gw), M, N, K, bits, int(y_fp32),
                                   _stream(stream), _ptr(a_had), int(mcg), _ptr(ws), ws.numel() if ws is not None else 0),
@@ -108,9 +109,9 @@ def gemm(y: torch.Tensor, x: torch.Tensor, w: GroupWords, M: int, N: int, K: int
 
 
 def gemv(y, x, w: GroupWords, M, N, K, bits, y_fp32=False, stream=None, a_had=None, mcg=False) -> None:
-    """Forced small-M path (reference gemv, exl3_gemm.cuh:70-83); M must be <= 8."""
-    if M > 8:
-        raise ValueError("gemv requires M <= 8")
+    """Forced small-M path (reference gemv, exl3_gemm.cuh:70-83); M must be <= 16."""
+    if M > GEMV_MAX_M:
+        raise ValueError(f"gemv requires M <= {GEMV_MAX_M}")
     gemm(y, x, w, M, N, K, bits, y_fp32, stream, a_had, mcg)
 
 

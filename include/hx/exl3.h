@@ -87,7 +87,7 @@ const char* hx_profile_phase_name(int phase);
 
 /* y[M][N] = svh . H_N( H_K(x . suh) . W_hat ), x fp16 [M][K], y fp32 (y_fp32) or fp16.
  * Replaces helios::exl3::gemm (src/cuda/quant/exl3_gemm.cuh:51-66, exl3_gemm.cu:81-243).
- * M <= 8 runs the fused decode-GEMV (returns HX_GEMM_PATH_GEMV), else the MFMA path (returns
+ * M <= 16 runs the fused decode-GEMV (returns HX_GEMM_PATH_GEMV), else the MFMA GEMM (returns
  * HX_GEMM_PATH_MFMA), which needs a_had (M*K fp16 scratch, as in the reference) or, when
  * a_had is NULL, takes it from the workspace.  K % 128 == 0, N % 128 == 0, bits 1..8. */
 size_t hx_exl3_gemm_workspace_size(int M, int N, int K);

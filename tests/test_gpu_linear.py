@@ -65,8 +65,8 @@ def _run_linear(hx, M, K, N, bits, cb, y_fp32, seed=0):
     return path, y.float().cpu().numpy(), ref
 
 
-@pytest.mark.parametrize("M", [1, 4, 8])
-@pytest.mark.parametrize("bits,cb", [(2, 2), (3, 2), (4, 2), (4, 0), (5, 1), (6, 2), (8, 2), (1, 0)])
+@pytest.mark.parametrize("M", [1, 3, 8, 13, 16])
+@pytest.mark.parametrize("bits,cb", [(2, 2), (3, 2), (4, 2), (4, 0), (5, 1), (6, 2), (8, 2), (1, 0), (7, 1)])
 def test_gemv_parity(hx, M, bits, cb):
     path, got, ref = _run_linear(hx, M, 1024, 512, bits, cb, True, seed=M * 10 + bits)
     assert path == hx.HX_GEMM_PATH_GEMV
@@ -87,7 +87,7 @@ def test_gemv_attention_projection_shape(hx):
         assert_close(got, ref, what=f"attn proj M={M}")
 
 
-@pytest.mark.parametrize("M", [9, 16, 100, 256])
+@pytest.mark.parametrize("M", [17, 32, 100, 256])
 @pytest.mark.parametrize("bits,cb", [(2, 2), (3, 2), (4, 0), (5, 2)])
 def test_mfma_parity(hx, M, bits, cb):
     path, got, ref = _run_linear(hx, M, 512, 384, bits, cb, True, seed=M + bits)
