@@ -107,6 +107,8 @@ def bench_decode(args, torch, moe, lib):
     gu_bytes = 9 * sum(layers[0].experts.trellis[p][0].numel() * 2 + layers[0].experts.suh[p][0].numel() * 2 +
                        layers[0].experts.svh[p][0].numel() * 2 for p in (0, 1))
     d_bytes = step_bytes - gu_bytes
+    # phase 2 = kernel A (router + permutation + gate/up GEMVs + SiLU-gate), phase 3 = kernel B (down
+    # GEMVs + contributions + ordered reduction + shared combine); one launch each for a uniform layer
     dominant = max(("experts_gate_up", gu_bytes), ("experts_down", d_bytes), key=lambda kv: phases.get(kv[0], 0))
     dom_us = phases[dominant[0]]
     achieved = dominant[1] / (dom_us * 1e-6) / 1e9
@@ -145,6 +147,80 @@ def bench_prefill(args, torch, moe):
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops}
 
 
+def graph_time_us(torch, fn, reps: int = 20) -> float:
+    """Average microseconds of fn() replayed from a HIP graph (fn must be capture-safe)."""
+    fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps * 1e3
+
+
+def bench_linears(torch, moe, exl3):
+    """BASELINE configs 1, 2 and 5a: single EXL3 linears (weight GB/s at M <= 16, TFLOP/s on MFMA)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    out = {}
+    cases = [("config1_K4096_N2048_2bit_M1", 4096, 2048, 2, 1),
+             ("config2_K4096_N12288_4bit_M1", 4096, 12288, 4, 1),
+             ("config2_K4096_N12288_4bit_M4", 4096, 12288, 4, 4),
+             ("config2_K4096_N12288_4bit_M8", 4096, 12288, 4, 8),
+             ("config5a_lmhead_K4096_N151552_5bit_M1", 4096, 151552, 5, 1),
+             ("config5a_lmhead_K4096_N151552_5bit_M512", 4096, 151552, 5, 512)]
+    for name, K, N, bits, M in cases:
+        copies = 4 if K * N * bits // 8 < 256 << 20 else 1   # rotate copies so the 256 MB MALL does not hold them
+        ws_ = [exl3.GroupWords(*moe.synthetic_linear(K, N, bits, g), exl3.MUL1) for _ in range(copies)]
+        x = torch.randn((M, K), generator=g, device="cuda").half()
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        a_had = torch.empty((M, K), dtype=torch.float16, device="cuda") if M > exl3.GEMV_MAX_M else None
+
+        def run():
+            for w in ws_:
+                exl3.gemm(y, x, w, M, N, K, bits, True, a_had=a_had)
+        us = graph_time_us(torch, run) / copies
+        wbytes = K * N * bits / 8 + 2 * K + 2 * N
+        out[name] = {"us": round(us, 2), "weight_gbs": round(wbytes / us / 1e3, 1),
+                     "pct_hbm": round(100 * wbytes / us / 1e3 / HBM_PEAK_GBS, 2),
+                     "tflops": round(2.0 * M * K * N / us / 1e6, 2)}
+        del ws_
+    return out
+
+
+def bench_sweep(torch, moe, layers_n: int = 42):
+    """BASELINE config 5b: 42 resident MoE layers (288 x 2-bit experts each), 1 token, independent
+    seeded routing per layer; one step = the 42 layers back to back."""
+    E, hidden, inter = 288, 4096, 2048
+    layers = [moe.MoeLayer(moe.ExpertSet.synthetic(E, hidden, inter, 2, seed=20000 + i), None, topk=8)
+              for i in range(layers_n)]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    scores = torch.randn((layers_n, 1, E), generator=g, device="cuda").half()
+    x = torch.randn((1, hidden), generator=g, device="cuda").half()
+    ys = [torch.empty((1, hidden), dtype=torch.float16, device="cuda") for _ in range(layers_n)]
+    ws = torch.zeros(layers[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
+
+    def run():
+        for i in range(layers_n):
+            layers[i](x, scores[i], y=ys[i], ws=ws)
+    us = graph_time_us(torch, run, reps=10)
+    step_bytes = layers_n * 8 * layers[0].experts.weight_bytes([0])
+    del layers
+    return {"layers": layers_n, "us_per_step": round(us, 1), "us_per_layer": round(us / layers_n, 2),
+            "weight_gbs": round(step_bytes / us / 1e3, 1),
+            "pct_hbm": round(100 * step_bytes / us / 1e3 / HBM_PEAK_GBS, 2),
+            "note": "routed experts only (8 per layer); weights of all 42 layers resident (~71 GiB)"}
+
+
 def cpu_baseline(layers, budget_s: float):
     """The C oracle's fp32 decode + GEMV (OpenMP over column tiles) over the same experts of the
     decode layer (gate, up, down of 8 routed + shared), timed on this host."""
@@ -166,7 +242,7 @@ def cpu_baseline(layers, budget_s: float):
     x = {K: rng.standard_normal((1, K)).astype(np.float16) for K in {m[0] for m in host}}
     threads = O.cpu_max_threads()
     total_s, total_bytes, layers_done = 0.0, 0, 0
-    while total_s < budget_s and layers_done < 50:
+    while total_s < budget_s and layers_done < 2000:
         for K, N, b, t, s, v in host:
             _, secs = O.cpu_linear_f32(x[K], t, s, v, K, N, b, 2, threads)
             total_s += secs
@@ -176,6 +252,63 @@ def cpu_baseline(layers, budget_s: float):
             "sample": f"{layers_done} MoE decode layers (8 routed + shared experts, gate/up/down, 2-bit, 1 token) "
                       f"through oracle/exl3_oracle.c hx_cpu_linear_f32 (fp32 accumulate, OpenMP), "
                       f"{total_s:.1f} s"}
+
+
+def traffic_from_profile(phase: str):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (profiles/moe_decode_layer_traffic.json, made by the command recorded in
+    it), or None when that summary is absent."""
+    from pathlib import Path
+    f = Path(__file__).resolve().parent / "profiles" / "moe_decode_layer_traffic.json"
+    if not f.exists():
+        return None
+    try:
+        d = json.loads(f.read_text())
+        return d["kernels"][phase]["hbm_bytes_per_launch"]
+    except Exception:
+        return None
+
+
+def profile_only(torch, moe):
+    """Workload for rocprofv3 --pmc runs: 3 plain copies of 256 MiB (the calibration kernel whose
+    byte count is known), then 10 eager steps of the decode layer over 2 rotating layers."""
+    src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    # weights: device copies of host-generated random blocks (the counter-collection pass of
+    # rocprofv3 is kept away from device RNG kernels)
+    from helios_glm53flash_amd import exl3
+    E, hidden, inter, bits = 288, 4096, 2048, 2
+    r = np.random.default_rng(0)
+    blk = torch.from_numpy(r.integers(-32768, 32768, size=hidden * inter // 8, dtype=np.int16)).cuda()
+    sgn = torch.from_numpy(r.choice([-1.0, 1.0], 4096).astype(np.float16)).cuda()
+    scl = torch.from_numpy((r.choice([-1.0, 1.0], 4096) * r.uniform(0.5, 1.5, 4096)).astype(np.float16)).cuda()
+
+    def lin(K, N, off):
+        t = torch.roll(blk, off).view(K // 16, N // 16, 16 * bits).clone()
+        return t, sgn[:K].clone(), scl[:N].clone()
+
+    shapes = [(hidden, inter), (hidden, inter), (inter, hidden)]
+    layers = []
+    for li in range(2):
+        tr, su, sv, bt = [[], [], []], [[], [], []], [[], [], []], [[], [], []]
+        for e in range(E):
+            for p, (K, N) in enumerate(shapes):
+                a, b_, c = lin(K, N, 8 * (li * 1000 + 3 * e + p))
+                tr[p].append(a)
+                su[p].append(b_)
+                sv[p].append(c)
+                bt[p].append(bits)
+        sh = [exl3.GroupWords(*lin(K, N, 17 + p), exl3.MUL1) for p, (K, N) in enumerate(shapes)]
+        layers.append(moe.MoeLayer(moe.ExpertSet(hidden, inter, tr, su, sv, bt, True), sh, topk=8))
+    scores = torch.from_numpy(r.standard_normal((10, 1, E)).astype(np.float16)).cuda()
+    x = torch.from_numpy(r.standard_normal((1, hidden)).astype(np.float16)).cuda()
+    ws = torch.zeros(layers[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
+    for i in range(10):
+        layers[i % 2](x, scores[i], ws=ws)
+    torch.cuda.synchronize()
+    print("profile workload done: copy 256 MiB x3, 10 decode-layer steps")
 
 
 def main():
@@ -188,6 +321,9 @@ def main():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--skip-extra", action="store_true", help="skip the linear and 42-layer sweep configs")
+    ap.add_argument("--profile-only", action="store_true",
+                    help="counter-collection driver: a 256 MiB device copy (calibration), then eager decode steps")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (one GPU holds every expert); "
@@ -199,8 +335,14 @@ def main():
     from helios_glm53flash_amd._lib import lib
 
     torch.cuda.set_device(0)
+    if args.profile_only:
+        profile_only(torch, moe)
+        return
+    from helios_glm53flash_amd import exl3
     dec = bench_decode(args, torch, moe, lib)
     pre = None if args.skip_prefill else bench_prefill(args, torch, moe)
+    lin = None if args.skip_extra else bench_linears(torch, moe, exl3)
+    sweep = None if args.skip_extra else bench_sweep(torch, moe)
     cpu = None if args.skip_cpu else cpu_baseline(dec["layers"], args.cpu_budget)
 
     out = {
@@ -226,12 +368,12 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
+            "traffic": traffic_from_profile(dec["dominant"]),
             "kernel": dec["dominant"],
             "achieved": round(dec["roofline_achieved"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dec["roofline_achieved"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
             "bytes_per_launch": dec["dominant_bytes"],
             "avg_launch_us": round(dec["dominant_us"], 3),
         },
@@ -242,6 +384,8 @@ def main():
             "decode_eager_gbs": round(dec["step_bytes"] / (dec["ms_eager"] * 1e-3) / 1e9, 2),
             "decode_timing": "value/ms_per_step: HIP-graph replay of the layer steps (%d steps); eager: one "
                              "host call per step" % dec["graph_steps"],
+            "linears": lin,
+            "sweep_42_layers": sweep,
             "prefill": None if pre is None else {
                 "workload": "moe_prefill: 4096 tokens, top-8 of 288 with Zipf(1.1) popularity, experts 0-143 "
                             "2-bit / 144-287 3-bit, hidden 4096, intermediate 2048 (BASELINE config 4), routed "

@@ -1,0 +1,82 @@
+"""Summaries of rocprofv3 result databases (rocpd SQLite) for the profiles/ directory.
+
+  python -m helios_glm53flash_amd.profiling stats <kernel-trace.db>
+      per-kernel dispatch count and average / min / max duration (us)
+  python -m helios_glm53flash_amd.profiling traffic <fetch.db> <write.db> [--cmd "..."]
+      HBM bytes per launch of the MoE decode kernels from FETCH_SIZE and WRITE_SIZE passes, each
+      scaled by what the same counter reads for the calibration copy (256 MiB read + 256 MiB write)
+      of bench.py --profile-only
+"""
+from __future__ import annotations
+
+import json
+import sqlite3
+import sys
+
+COPY_BYTES = 256 << 20
+
+
+def kernel_stats(db: str) -> list[dict]:
+    c = sqlite3.connect(db)
+    rows = c.execute("select name, count(*), avg(end-start), min(end-start), max(end-start) from kernels "
+                     "group by name order by sum(end-start) desc").fetchall()
+    return [{"kernel": n, "calls": k, "avg_us": a / 1e3, "min_us": lo / 1e3, "max_us": hi / 1e3}
+            for n, k, a, lo, hi in rows]
+
+
+def counter_means(db: str, counter: str) -> dict[str, float]:
+    c = sqlite3.connect(db)
+    rows = c.execute("select kernel_name, avg(value) from counters_collection where counter_name = ? "
+                     "group by kernel_name", (counter,)).fetchall()
+    return {n: v for n, v in rows}
+
+
+def calibration_value(db: str, counter: str) -> float:
+    """Counter value of the 256 MiB calibration copy: the largest copy dispatch of the run (the
+    runtime's blit kernel also serves the small host transfers, which read far less)."""
+    c = sqlite3.connect(db)
+    (v,) = c.execute("select max(value) from counters_collection where counter_name = ? and "
+                     "kernel_name like '%copy%'", (counter,)).fetchone()
+    return float(v)
+
+
+def _pick(d: dict[str, float], key: str) -> float:
+    vals = [v for n, v in d.items() if key in n]
+    if not vals:
+        raise KeyError(key)
+    return sum(vals) / len(vals)
+
+
+def traffic(fetch_db: str, write_db: str, cmd: str = "") -> dict:
+    f = counter_means(fetch_db, "FETCH_SIZE")
+    w = counter_means(write_db, "WRITE_SIZE")
+    copy_f = calibration_value(fetch_db, "FETCH_SIZE")
+    copy_w = calibration_value(write_db, "WRITE_SIZE")
+    kf = COPY_BYTES / (copy_f * 1024.0)   # bytes per reported KiB, read side
+    kw = COPY_BYTES / (copy_w * 1024.0)
+    out = {"command": cmd, "copy_calibration": {"bytes": COPY_BYTES, "FETCH_SIZE_KiB": copy_f,
+                                                "WRITE_SIZE_KiB": copy_w, "read_scale": kf, "write_scale": kw},
+           "kernels": {}}
+    for phase, key in (("experts_gate_up", "moe_decode_gu_kernel"), ("experts_down", "moe_decode_d_kernel")):
+        fk, wk = _pick(f, key), _pick(w, key)
+        out["kernels"][phase] = {"FETCH_SIZE_KiB": fk, "WRITE_SIZE_KiB": wk,
+                                 "read_bytes": fk * 1024 * kf, "write_bytes": wk * 1024 * kw,
+                                 "hbm_bytes_per_launch": round(fk * 1024 * kf + wk * 1024 * kw)}
+    return out
+
+
+def main(argv: list[str]) -> None:
+    if len(argv) >= 2 and argv[0] == "stats":
+        for r in kernel_stats(argv[1]):
+            print(f"{r['calls']:6d}  avg {r['avg_us']:10.3f} us  min {r['min_us']:10.3f}  max {r['max_us']:10.3f}  "
+                  f"{r['kernel'][:110]}")
+    elif len(argv) >= 3 and argv[0] == "traffic":
+        cmd = argv[argv.index("--cmd") + 1] if "--cmd" in argv else ""
+        print(json.dumps(traffic(argv[1], argv[2], cmd), indent=1))
+    else:
+        print(__doc__)
+        sys.exit(2)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:])

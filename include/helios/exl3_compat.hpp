@@ -1,0 +1,223 @@
+// helios/exl3_compat.hpp -- header-only C++ layer that re-creates the reference engine's EXL3,
+// router and MoE-glue signatures on top of the C ABI in hx/exl3.h, so the engine's call sites
+// (src/engine/runner.cpp) compile unchanged against libhx_exl3.so.
+//
+// Differences a caller sees: errors throw helios::exl3::Error (the reference aborts); the fused
+// kernels need a workspace, which this layer keeps per device (allocated on first use, zeroed once,
+// never freed while the process runs) unless the caller installs one with set_workspace().
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+
+#include "../hx/exl3.h"
+
+namespace helios {
+
+using Stream = hipStream_t;
+
+namespace exl3 {
+
+struct Error : std::runtime_error {
+    explicit Error(const std::string& s) : std::runtime_error(s) {}
+};
+
+inline int check(int code, const char* what)
+{
+    if (code < 0) throw Error(std::string(what) + ": " + hx_last_error());
+    return code;
+}
+
+// Per-device workspace (the reference keeps its lock buffer in a per-device singleton,
+// src/cuda/quant/exl3_devctx.cu:60-71).
+class Workspace {
+public:
+    static Workspace& get()
+    {
+        static Workspace w;
+        return w;
+    }
+    void* acquire(size_t bytes, Stream s)
+    {
+        std::lock_guard<std::mutex> g(mu_);
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        Slot& slot = slots_[dev];
+        if (slot.bytes < bytes) {
+            if (slot.ptr && slot.owned) {
+                (void)hipStreamSynchronize(s);
+                (void)hipFree(slot.ptr);
+            }
+            if (hipMalloc(&slot.ptr, bytes) != hipSuccess) throw Error("workspace allocation failed");
+            check(hx_workspace_init(slot.ptr, bytes, (hx_stream_t)s), "hx_workspace_init");
+            slot.bytes = bytes;
+            slot.owned = true;
+        }
+        return slot.ptr;
+    }
+    size_t size()
+    {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        return slots_[dev].bytes;
+    }
+    // Install a caller-owned, zero-filled workspace for the current device.
+    void set(void* ptr, size_t bytes)
+    {
+        std::lock_guard<std::mutex> g(mu_);
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        slots_[dev] = Slot{ptr, bytes, false};
+    }
+
+private:
+    struct Slot {
+        void* ptr = nullptr;
+        size_t bytes = 0;
+        bool owned = false;
+    };
+    std::mutex mu_;
+    std::unordered_map<int, Slot> slots_;
+};
+
+inline void set_workspace(void* ptr, size_t bytes) { Workspace::get().set(ptr, bytes); }
+
+// reference: src/cuda/quant/exl3_gemm.cuh:30-36
+struct GroupWords {
+    const uint16_t* trellis;
+    const void* suh;
+    const void* svh;
+    int mul1;
+};
+
+// reference: src/cuda/quant/exl3_gemm.cuh:51-66 (force_shape_idx / force_num_sms are accepted and
+// ignored: the kernel choice is by M)
+inline int gemm(void* y, const void* x, const GroupWords& w, int M, int N, int K, int bits, bool y_fp32 = false,
+                Stream s = 0, void* a_had = nullptr, bool mcg = false, int force_shape_idx = 0, int force_num_sms = 0)
+{
+    (void)force_shape_idx;
+    (void)force_num_sms;
+    const hx_group_words g{w.trellis, w.suh, w.svh, w.mul1};
+    const size_t ws_bytes = hx_exl3_gemm_workspace_size(M, N, K);
+    void* ws = Workspace::get().acquire(ws_bytes, s);
+    return check(hx_exl3_gemm(y, x, &g, M, N, K, bits, y_fp32, (hx_stream_t)s, a_had, mcg, ws,
+                              Workspace::get().size()),
+                 "helios::exl3::gemm");
+}
+
+// reference: src/cuda/quant/exl3_gemm.cuh:70-83 (small-M path; M <= 16 here)
+inline void gemv(void* y, const void* x, const GroupWords& w, int M, int N, int K, int bits, bool y_fp32 = false,
+                 Stream s = 0, void* a_had = nullptr, bool mcg = false)
+{
+    if (M > 16) throw Error("helios::exl3::gemv: M must be <= 16");
+    gemm(y, x, w, M, N, K, bits, y_fp32, s, a_had, mcg);
+}
+
+// reference: src/cuda/quant/reconstruct.cuh:15-63
+inline void reconstruct_slice(void* unpacked, const void* packed, int packed_rows, int packed_cols, int unpacked_cols,
+                              int K, bool mcg, bool mul1, int64_t n_offset, Stream s = 0)
+{
+    check(hx_exl3_reconstruct_slice(unpacked, packed, packed_rows, packed_cols, unpacked_cols, K, mcg, mul1, n_offset,
+                                    (hx_stream_t)s),
+          "helios::exl3::reconstruct_slice");
+}
+inline void reconstruct(void* unpacked, const void* packed, int packed_rows, int packed_cols, int unpacked_cols, int K,
+                        bool mcg, bool mul1, Stream s = 0)
+{
+    reconstruct_slice(unpacked, packed, packed_rows, packed_cols, unpacked_cols, K, mcg, mul1, 0, s);
+}
+
+// reference: src/cuda/quant/exl3_moe.cuh:20-31
+struct ExpertTables {
+    const uint16_t** gate_trellis;
+    const void** gate_suh;
+    const void** gate_svh;
+    const uint16_t** up_trellis;
+    const void** up_suh;
+    const void** up_svh;
+    const uint16_t** down_trellis;
+    const void** down_suh;
+    const void** down_svh;
+};
+
+// reference: src/cuda/quant/exl3_moe.cuh:74-105.  Without sorted_contributions the reference
+// accumulates into y atomically; this build adds the routed sum in routing-rank order, which needs
+// the permutation's route_to_sorted (pass it as the last argument).
+inline void moe_grouped(const void* x, void* y, const int64_t* expert_count, const int64_t* token_sorted,
+                        const void* weight_sorted, void* temp_state_g, void* temp_state_u, void* temp_intermediate_g,
+                        void* temp_intermediate_u, const ExpertTables& tables, int tokens, int hidden_dim,
+                        int intermediate_dim, int num_experts, int topk, int max_tokens_per_expert, int concurrency,
+                        int K_gate, int K_up, int K_down, bool mcg = false, bool mul1 = false, float act_limit = 10.0f,
+                        int act_function = 0, int num_active = -1, Stream s = 0,
+                        float* sorted_contributions = nullptr, const int64_t* route_to_sorted = nullptr)
+{
+    const hx_expert_tables t{reinterpret_cast<const void* const*>(tables.gate_trellis),
+                             reinterpret_cast<const void* const*>(tables.gate_suh),
+                             reinterpret_cast<const void* const*>(tables.gate_svh),
+                             reinterpret_cast<const void* const*>(tables.up_trellis),
+                             reinterpret_cast<const void* const*>(tables.up_suh),
+                             reinterpret_cast<const void* const*>(tables.up_svh),
+                             reinterpret_cast<const void* const*>(tables.down_trellis),
+                             reinterpret_cast<const void* const*>(tables.down_suh),
+                             reinterpret_cast<const void* const*>(tables.down_svh),
+                             nullptr, nullptr, nullptr, 0u};
+    const size_t ws_bytes = hx_moe_workspace_size(tokens, hidden_dim, intermediate_dim, num_experts, topk);
+    void* ws = Workspace::get().acquire(ws_bytes, s);
+    check(hx_moe_grouped(x, static_cast<float*>(y), expert_count, token_sorted, weight_sorted, temp_state_g,
+                         temp_state_u, temp_intermediate_g, temp_intermediate_u, &t, tokens, hidden_dim,
+                         intermediate_dim, num_experts, topk, max_tokens_per_expert, concurrency, K_gate, K_up, K_down,
+                         mcg, mul1, act_limit, act_function, num_active, (hx_stream_t)s, sorted_contributions,
+                         route_to_sorted, ws, Workspace::get().size()),
+          "helios::exl3::moe_grouped");
+}
+
+// reference: src/cuda/quant/hadamard.cuh:14-43 (fp16)
+inline void had_r_128(const void* input, void* output, const void* pre_scale, const void* post_scale, int64_t rows,
+                      int cols, float r_scale = 0.088388347648f, Stream s = 0)
+{
+    check(hx_had_r_128(input, output, pre_scale, post_scale, rows, cols, r_scale, (hx_stream_t)s),
+          "helios::exl3::had_r_128");
+}
+
+}  // namespace exl3
+
+namespace aux {
+// reference: src/cuda/aux/routing.cuh:36-49
+inline void routing_ds3_nogroup(const void* scores, const void* bias, int64_t* topk_indices, void* topk_weights,
+                                int bsz, int num_experts, int K, float scaling_factor, bool use_topk = true,
+                                int act_fn = 0, Stream s = 0)
+{
+    exl3::check(hx_routing_ds3_nogroup(scores, bias, topk_indices, topk_weights, bsz, num_experts, K, scaling_factor,
+                                       use_topk, act_fn, (hx_stream_t)s),
+                "helios::aux::routing_ds3_nogroup");
+}
+}  // namespace aux
+
+namespace glue {
+// reference: src/engine/glue2.cuh:44-49, :64
+inline void moe_permute(const int64_t* ids, const void* weights, int M, int topk, int E, int64_t* expert_count,
+                        int64_t* token_sorted, void* weight_sorted, int64_t* workspace, Stream s = 0,
+                        int64_t* route_to_sorted = nullptr)
+{
+    exl3::check(hx_moe_permute(ids, weights, M, topk, E, expert_count, token_sorted, weight_sorted, workspace,
+                               (hx_stream_t)s, route_to_sorted),
+                "helios::glue::moe_permute");
+}
+inline void moe_reduce_sorted(float* y, const float* contributions, const int64_t* route_to_sorted, int M, int topk,
+                              int hidden, Stream s = 0)
+{
+    exl3::check(hx_moe_reduce_sorted(y, contributions, route_to_sorted, M, topk, hidden, (hx_stream_t)s),
+                "helios::glue::moe_reduce_sorted");
+}
+inline void swiglu_clamp(const float* gate, const float* up, void* out, size_t n, float limit, Stream s = 0)
+{
+    exl3::check(hx_swiglu_clamp(gate, up, out, n, limit, (hx_stream_t)s), "helios::glue::swiglu_clamp");
+}
+}  // namespace glue
+
+}  // namespace helios

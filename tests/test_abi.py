@@ -43,3 +43,25 @@ def test_host_side_validation_without_gpu():
     r = _lib.lib.hx_routing_ds3_nogroup(1, None, 1, 1, 1, 288, 8, 2.5, 0, 0, None)
     assert r == _lib.HX_ERR_UNSUPPORTED
     assert _lib.lib.hx_exl3_gemm_workspace_size(1, 2048, 4096) > 0
+
+
+def test_cpp_compat_header_compiles_and_links(tmp_path):
+    """include/helios/exl3_compat.hpp (reference-signature C++ layer) compiles with hipcc and
+    links against the library; nothing is executed."""
+    import shutil
+    import subprocess
+    from helios_glm53flash_amd import _lib
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    src = tmp_path / "t.cpp"
+    src.write_text('#include "helios/exl3_compat.hpp"\n'
+                   "int main(int argc, char**) {\n"
+                   "  if (argc > 5) {\n"
+                   "    helios::exl3::GroupWords w{nullptr, nullptr, nullptr, 0};\n"
+                   "    helios::exl3::gemm(nullptr, nullptr, w, 1, 128, 128, 2);\n"
+                   "    helios::glue::moe_permute(nullptr, nullptr, 1, 8, 288, nullptr, nullptr, nullptr, nullptr);\n"
+                   "  }\n  return 0;\n}\n")
+    lib = Path(_lib.LIB_PATH)
+    r = subprocess.run([hipcc, "-std=c++17", "-Werror", "-I", str(ROOT / "include"), str(src), "-o",
+                        str(tmp_path / "t"), "-L", str(lib.parent), "-lhx_exl3", f"-Wl,-rpath,{lib.parent}"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
