@@ -37,7 +37,7 @@ struct Prof {
 Prof g_prof;
 const char* const k_phase_names[] = {"route", "permute", "experts_gate_up", "experts_down", "combine",
                                      "shared_expert", "prefill_plan_gather", "prefill_gemm_gate_up",
-                                     "prefill_guad", "prefill_gemm_down", "prefill_combine"};
+                                     "prefill_guad", "prefill_gemm_down", "prefill_combine", "moe_decode"};
 constexpr int k_nphases = sizeof(k_phase_names) / sizeof(k_phase_names[0]);
 
 struct Phase {
@@ -337,7 +337,7 @@ int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const i
             a.y_routed = y;
             a.y_accumulate = true;
         }
-        return hip_status(hx::run_moe_decode(a, cb, phase_mask(tables, K_gate, K_up), phase_mask(tables, K_down, 0), st),
+        return hip_status(hx::run_moe_decode(a, cb, phase_mask(tables, K_gate, K_up) | phase_mask(tables, K_down, 0), st),
                           "hx_moe_grouped(decode)");
     }
     hx::PrefillArgs p{};
@@ -423,13 +423,8 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
         a.combine = true;
         a.y = static_cast<_Float16*>(y);
         a.y_routed = y_routed;
-        {
-            Phase ph(2, st);
-            r = hip_status(hx::run_moe_decode(a, cb, mgu, 0, st), "hx_moe_layer(router + experts gate/up)");
-        }
-        if (r) return r;
-        Phase ph(3, st);
-        return hip_status(hx::run_moe_decode(a, cb, 0, md, st), "hx_moe_layer(experts down + combine)");
+        Phase ph(11, st);
+        return hip_status(hx::run_moe_decode(a, cb, mgu | md, st), "hx_moe_layer(decode)");
     }
     {
         Phase ph(0, st);

@@ -48,6 +48,40 @@ HX_INLINE void load_quarter(uint32_t* r, const uint32_t* tile, int q)
     for (int i = 0; i < BITS; ++i) r[i + 1] = __builtin_nontemporal_load(t + q * BITS + i);
 }
 
+// The same words through a buffer resource: the per-lane byte offsets are fixed for a whole
+// range (voff0 of the wrapped first word, voff1 of the rest) and the step moves only the scalar
+// offset, so a step's loads cost no vector ALU address arithmetic; a read past the tensor's end
+// (num_records) returns zeros instead of faulting.
+typedef unsigned int hx_u2 __attribute__((ext_vector_type(2)));
+typedef unsigned int hx_u3 __attribute__((ext_vector_type(3)));
+typedef unsigned int hx_u4v __attribute__((ext_vector_type(4)));
+constexpr int HX_BUF_NT = 2;  // nontemporal: the tile words are read once
+
+template <int N>
+HX_INLINE void buf_words(uint32_t* r, __amdgpu_buffer_rsrc_t rs, int voff, int soff)
+{
+    if constexpr (N >= 4) {
+        const hx_u4v v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, HX_BUF_NT);
+        r[0] = v.x, r[1] = v.y, r[2] = v.z, r[3] = v.w;
+        if constexpr (N > 4) buf_words<N - 4>(r + 4, rs, voff + 16, soff);
+    } else if constexpr (N == 3) {
+        const hx_u3 v = __builtin_amdgcn_raw_buffer_load_b96(rs, voff, soff, HX_BUF_NT);
+        r[0] = v.x, r[1] = v.y, r[2] = v.z;
+    } else if constexpr (N == 2) {
+        const hx_u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, HX_BUF_NT);
+        r[0] = v.x, r[1] = v.y;
+    } else if constexpr (N == 1) {
+        r[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, HX_BUF_NT);
+    }
+}
+
+template <int BITS>
+HX_INLINE void load_quarter_buf(uint32_t* r, __amdgpu_buffer_rsrc_t rs, int voff0, int voff1, int soff)
+{
+    r[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff0, soff, HX_BUF_NT);
+    buf_words<BITS>(r + 1, rs, voff1, soff);
+}
+
 // The 32 bits ending at local bit E of the quarter registers (bit 0 = local bit E-1).
 template <int E>
 HX_INLINE uint32_t quarter_reg(const uint32_t* r)
@@ -178,6 +212,51 @@ HX_INLINE void quarter_decode(const uint32_t* r, uint32_t* out)
     }
 }
 
+// ---- codebook 2 in affine form
+//
+// The cb2 weight is v = fp16(h * S + B) with h = fp16(0x6400 + bytesum(w * 0x83DCD12D)) = 1024 + s
+// and S = fp16 0x1eee, B = fp16 0xc931 (codebook.cuh:77-90).  The GEMV feeds h itself to the matrix
+// cores and applies the map once per output: sum_k a_k (h_k S + B) = S sum_k a_k h_k + B sum_k a_k.
+// This drops one rounding per weight (|v - (hS + B)| <= 2^-10, against outputs that are sums of
+// thousands of terms) and the fma per weight pair.  A window costs one v_bfe_u32 (one v_alignbit_b32
+// per word more for the windows that straddle two words) and one v_mul_lo_u32 (full rate on gfx950),
+// and a pair of products one v_sad_u8 + one v_sad_hi_u8, which leave h as packed fp16 directly.
+constexpr float CB2_SCALE = 0.00676727294921875f;  // fp16 0x1eee
+constexpr float CB2_BIAS = -10.3828125f;           // fp16 0xc931
+
+// Window of local position P of a quarter: it ends at local bit E = (P+1)*BITS + 32 (MSB first);
+// M[j] = the 32 bits ending at local bit 32j + 16, for windows across words j-1 and j.
+template <int BITS, int P>
+HX_INLINE uint32_t quarter_window(const uint32_t* r, const uint32_t* M)
+{
+    constexpr int E = (P + 1) * BITS + 32;
+    constexpr int j = E >> 5, rr = E & 31;
+    if constexpr (rr == 0) return __builtin_amdgcn_ubfe(r[j - 1], 0, 16);
+    else if constexpr (rr >= 16) return __builtin_amdgcn_ubfe(r[j], 32 - rr, 16);
+    else return __builtin_amdgcn_ubfe(M[j], 16 - rr, 16);
+}
+
+template <int BITS, int P = 0>
+HX_INLINE void quarter_affine_pairs(const uint32_t* r, const uint32_t* M, uint32_t* out)
+{
+    if constexpr (P < 32) {
+        const uint32_t x0 = quarter_window<BITS, P>(r, M) * 0x83DCD12Du;
+        const uint32_t x1 = quarter_window<BITS, P + 1>(r, M) * 0x83DCD12Du;
+        out[P / 2] = __builtin_amdgcn_sad_hi_u8(x1, 0u, __builtin_amdgcn_sad_u8(x0, 0u, 0x64006400u));
+        quarter_affine_pairs<BITS, P + 2>(r, M, out);
+    }
+}
+
+// h of a quarter as fp16 pairs: out[i] = positions (2i, 2i+1) = (k, k+1) of one column.
+template <int BITS>
+HX_INLINE void quarter_affine(const uint32_t* r, uint32_t* out)
+{
+    uint32_t M[BITS + 1];
+#pragma unroll
+    for (int j = 1; j <= BITS; ++j) M[j] = __builtin_amdgcn_alignbit(r[j - 1], r[j], 16);
+    quarter_affine_pairs<BITS>(r, M, out);
+}
+
 // MFMA B operand (nh, kh) of a decoded quarter: column 8nh+q, k = 8kh + 0..7, i.e. local positions
 // 2kh + 4nh + 8j + {0, 1} for j = 0..3.
 template <int NH, int KH>
@@ -195,31 +274,85 @@ HX_INLINE hx_h8 quarter_operand(const uint32_t* d)
 
 // Input transform of rows [0, M) over k in [k0, k0 + kc) into LDS as fp16:
 //   a = fp16(H128(fp16(x . suh)))   (reference had_hf_r_128_inner<true,false>)
-// When pre_transformed, x already holds a (copied as is).
-HX_INLINE void input_to_lds(uint32_t* a_lds, const _Float16* x, const int* rows, const _Float16* suh, int M,
-                            int K, int k0, int kc, bool pre_transformed)
+// When pre_transformed, x already holds a (copied as is, read with device-coherent loads because
+// another workgroup of the same launch may have produced it).
+//
+// Job j (row m, 128-wide block b) is done by wave j % 4.  The loads of a wave's first IN_PRE jobs are
+// issued separately (input_issue) so that a caller can put them ahead of the tile prefetch: the
+// vector-memory counter completes in issue order, so an input load issued after the prefetch would
+// make the transform wait for every prefetched tile.
+constexpr int IN_PRE = 4;
+
+struct InputRegs {
+    uint32_t xv[IN_PRE];
+    uint32_t sv[IN_PRE];
+};
+
+HX_INLINE uint32_t input_word(const _Float16* x, const int* rows, int M, int K, int k0, int blocks, int job, int lane,
+                              bool pre_transformed)
+{
+    const int m = job / blocks, b = job % blocks;
+    const int k = k0 + b * 128 + 2 * lane;
+    const size_t row = rows ? (size_t)rows[m] : (size_t)m;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(x + row * K + k);
+    if (pre_transformed) return __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return *(hx_gu32*)src;
+}
+
+HX_INLINE void input_issue(InputRegs& r, const _Float16* x, const int* rows, const _Float16* suh, int M, int K, int k0,
+                           int kc, bool pre_transformed)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int blocks = kc >> 7;
-    for (int job = wave; job < M * blocks; job += GEMV_WAVES) {
-        const int m = job / blocks, b = job % blocks;
-        const int k = k0 + b * 128 + 2 * lane;
-        const size_t row = rows ? (size_t)rows[m] : (size_t)m;
-        uint32_t xv = *reinterpret_cast<const uint32_t*>(x + row * K + k);
-        uint32_t out;
-        if (pre_transformed) {
-            out = xv;
-        } else {
-            hx_h2 s = *reinterpret_cast<const hx_h2*>(suh + k);
-            hx_h2 p = u32_as_h2(xv) * s;
-            float v0 = (float)p.x, v1 = (float)p.y;
-            hx_had128_wave(v0, v1);
-            hx_h2 r = {(_Float16)v0, (_Float16)v1};
-            out = h2_as_u32(r);
+#pragma unroll
+    for (int i = 0; i < IN_PRE; ++i) {
+        const int job = wave + GEMV_WAVES * i;
+        r.xv[i] = 0;
+        r.sv[i] = 0;
+        if (job < M * blocks) {
+            r.xv[i] = input_word(x, rows, M, K, k0, blocks, job, lane, pre_transformed);
+            if (!pre_transformed)
+                r.sv[i] = *(hx_gu32*)(suh + k0 + (job % blocks) * 128 + 2 * lane);
         }
-        a_lds[(m * kc + b * 128) / 2 + lane] = out;
     }
 }
+
+HX_INLINE uint32_t input_transform(uint32_t xv, uint32_t sv, bool pre_transformed)
+{
+    if (pre_transformed) return xv;
+    hx_h2 p = u32_as_h2(xv) * u32_as_h2(sv);
+    float v0 = (float)p.x, v1 = (float)p.y;
+    hx_had128_wave(v0, v1);
+    hx_h2 r = {(_Float16)v0, (_Float16)v1};
+    return h2_as_u32(r);
+}
+
+// Transform and store all jobs: the first IN_PRE per wave from r, the rest loaded here.
+HX_INLINE void input_finish(uint32_t* a_lds, const InputRegs& r, const _Float16* x, const int* rows,
+                            const _Float16* suh, int M, int K, int k0, int kc, bool pre_transformed)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int blocks = kc >> 7;
+#pragma unroll
+    for (int i = 0; i < IN_PRE; ++i) {
+        const int job = wave + GEMV_WAVES * i;
+        if (job < M * blocks) {
+            const int m = job / blocks, b = job % blocks;
+            a_lds[(m * kc + b * 128) / 2 + lane] = input_transform(r.xv[i], r.sv[i], pre_transformed);
+        }
+    }
+    for (int job = wave + GEMV_WAVES * IN_PRE; job < M * blocks; job += GEMV_WAVES) {
+        const int m = job / blocks, b = job % blocks;
+        const uint32_t xv = input_word(x, rows, M, K, k0, blocks, job, lane, pre_transformed);
+        const uint32_t sv =
+            pre_transformed ? 0u : *(hx_gu32*)(suh + k0 + b * 128 + 2 * lane);
+        a_lds[(m * kc + b * 128) / 2 + lane] = input_transform(xv, sv, pre_transformed);
+    }
+}
+
+struct NoHook {
+    HX_INLINE void operator()() const {}
+};
 
 struct GemvArgs {
     const _Float16* x;       // M x K fp16 (or pre-transformed a)
@@ -234,40 +367,71 @@ struct GemvArgs {
     bool pre_transformed;
 };
 
-// This workgroup's (column group cg, split s) partial sum of the GEMV: on return colsum[m][c]
-// (LDS fp32, MT x 128) holds sum over k in the split of a[m][k] * W[k][cg*128 + c].
+// This workgroup's partial sum of the GEMV over k in [k0, k0 + kc) (kc a multiple of 128): on
+// return colsum[m][c] (LDS fp32, MT x 128) holds sum over that range of a[m][k] * W[k][cg*128 + c].
 // a_lds must hold MT * kc fp16.  MT <= 16.
-template <int BITS, int CB, int MT>
-__device__ void gemv_split_sum(const GemvArgs& g, int cg, int s, uint32_t* a_lds, float* colsum)
+//
+// before_input() runs after the tile prefetch is issued and before a pre-transformed input is read
+// (a consumer waits there for its producer); after_input() runs once the input is in LDS.
+template <int BITS, int CB, int MT, class Before = NoHook, class After = NoHook>
+__device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, int kc, uint32_t* a_lds, float* colsum,
+                                           Before before_input = Before(), After after_input = After())
 {
     static_assert(MT <= 16, "one MFMA holds 16 rows");
+    constexpr bool AFFINE = CB == 2;
+    __shared__ float asum[MT];  // sum of the transformed input over the range, per row (affine cb2)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int gq = lane >> 4;             // tile row within the 4-row step (MFMA k-group)
     const int t = (lane >> 3) & 1;        // tile column of the wave's pair
     const int q = lane & 7;               // quarter
-    const int k0 = s * g.kc;
-    const int kc = min(g.kc, g.K - k0);
     const int tiles_n = g.N >> 4;
     constexpr int NW = 8 * BITS;
     const uint32_t* tw = reinterpret_cast<const uint32_t*>(g.trellis);
     const int tn = cg * 8 + 2 * wave + t;
 
     // software pipeline: PF steps of tile words in flight.  The first PF are issued before the input
-    // transform so their HBM latency overlaps it; every step then consumes one ring slot and refills
-    // it PF steps ahead (past the end the load repeats the split's last tile row, so the number of
-    // loads in flight is the same at every step and each wait is a static count).
+    // transform (after the input loads themselves) so their HBM latency overlaps it; every step then
+    // consumes one ring slot and refills it PF steps ahead (past the end the load repeats the range's
+    // last tile row, so the number of loads in flight is the same at every step and each wait is a
+    // static count).
     constexpr int PF = BITS <= 4 ? 8 : 4;
     const int steps = kc >> 6;
     uint32_t buf[PF][BITS + 1];
-    const uint32_t* tcol = tw + (size_t)tn * NW;
-    const size_t row_stride = (size_t)tiles_n * NW;
-    const int tk0 = (k0 >> 4) + gq;
-    const int tk_last = (k0 >> 4) + 4 * (steps - 1) + gq;
+    // byte offsets: lane part (tile row gq of the step, tile column tn, quarter q) and step part
+    // (tile rows k0/16 + 4*st); the tensor is (K/16) x (N/16) tiles
+    // the base is uniform: state it, or every buffer load gets a loop over the lanes' descriptors
+    const uint64_t twu = reinterpret_cast<uint64_t>(tw);
+    // (readfirstlane returns int: each half goes through uint32_t so the low half is not sign-extended)
+    const uint64_t twb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(twu >> 32)) << 32) |
+                         (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)twu);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void*>(twb), 0, (int)min((size_t)0x7fffffff, (size_t)(g.K >> 4) * tiles_n * NW * 4),
+        0x00020000);
+    const int lane_off = ((gq * tiles_n + tn) * NW) * 4;
+    const int voff0 = lane_off + ((q * BITS + NW - 1) % NW) * 4, voff1 = lane_off + q * BITS * 4;
+    const int row_bytes = tiles_n * NW * 4;
+    const int soff0 = (k0 >> 4) * row_bytes, step_bytes = 4 * row_bytes;
+    InputRegs in;
+    if (!g.pre_transformed) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, false);
 #pragma unroll
-    for (int j = 0; j < PF; ++j) load_quarter<BITS>(buf[j], tcol + (size_t)min(tk0 + 4 * j, tk_last) * row_stride, q);
+    for (int j = 0; j < PF; ++j) load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff0 + min(j, steps - 1) * step_bytes);
 
-    input_to_lds(a_lds, g.x, g.rows, g.suh, g.M, g.K, k0, kc, g.pre_transformed);
+    before_input();
+    if (g.pre_transformed) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, true);
+    input_finish(a_lds, in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, g.pre_transformed);
     hx_lds_barrier();
+    after_input();
+    HX_TS(2);
+    if constexpr (AFFINE) {
+        for (int m = wave; m < g.M && m < MT; m += GEMV_WAVES) {
+            const _Float16* row = reinterpret_cast<const _Float16*>(a_lds) + (size_t)m * kc;
+            float v = 0.0f;
+            for (int k = lane; k < kc; k += 64) v += (float)row[k];
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+            if (lane == 0) asum[m] = v;
+        }
+    }
 
     hx_f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
     const int am = min(lane & 15, g.M - 1);  // A row of this lane (rows >= M repeat the last row)
@@ -276,9 +440,18 @@ __device__ void gemv_split_sum(const GemvArgs& g, int cg, int s, uint32_t* a_lds
 #pragma unroll
         for (int j = 0; j < PF; ++j) {
             const int st = st0 + j;
+            // progress-based wave priority: a wave entering a group of PF steps outranks the waves
+            // of its SIMD that are further into theirs, so co-resident waves advance at the same
+            // rate instead of the oldest first (a starved wave would hold back every workgroup that
+            // waits for its range)
+            if (j == 0) HX_SETPRIO(3);
+            if (j == PF / 4) HX_SETPRIO(2);
+            if (j == PF / 2) HX_SETPRIO(1);
+            if (j == 3 * PF / 4) HX_SETPRIO(0);
             uint32_t d[16];
-            quarter_decode<BITS, CB>(buf[j], d);
-            load_quarter<BITS>(buf[j], tcol + (size_t)min(tk0 + 4 * (st + PF), tk_last) * row_stride, q);
+            if constexpr (AFFINE) quarter_affine<BITS>(buf[j], d);
+            else quarter_decode<BITS, CB>(buf[j], d);
+            load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff0 + min(st + PF, steps - 1) * step_bytes);
             if (st < steps) {
                 const int kl = 64 * st + 16 * gq;
                 const hx_h8 a0 = *reinterpret_cast<const hx_h8*>(arow + kl);
@@ -291,17 +464,35 @@ __device__ void gemv_split_sum(const GemvArgs& g, int cg, int s, uint32_t* a_lds
         }
     }
 
+    HX_SETPRIO(3);  // the split-K handoff and epilogues are on the critical path
+    if constexpr (AFFINE) hx_lds_barrier();  // asum of every row is in LDS
+
     // C: lane holds rows 4*(lane/16) + i of column label lane%16 = 8t + q; label -> column
     // 16*(2*wave + t) + 8*nh + q of the group
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = 4 * gq + i;
         if (m < MT && m < g.M) {
-            colsum[m * 128 + 16 * (2 * wave + t) + q] = acc0[i];
-            colsum[m * 128 + 16 * (2 * wave + t) + 8 + q] = acc1[i];
+            float c0 = acc0[i], c1 = acc1[i];
+            if constexpr (AFFINE) {
+                const float b = CB2_BIAS * asum[m];
+                c0 = fmaf(c0, CB2_SCALE, b);
+                c1 = fmaf(c1, CB2_SCALE, b);
+            }
+            colsum[m * 128 + 16 * (2 * wave + t) + q] = c0;
+            colsum[m * 128 + 16 * (2 * wave + t) + 8 + q] = c1;
         }
     }
     __syncthreads();
+}
+
+// Split s of K in chunks of g.kc (the last may be shorter).
+template <int BITS, int CB, int MT, class Before = NoHook, class After = NoHook>
+__device__ __forceinline__ void gemv_split_sum(const GemvArgs& g, int cg, int s, uint32_t* a_lds, float* colsum,
+                                               Before before_input = Before(), After after_input = After())
+{
+    const int k0 = s * g.kc;
+    gemv_range<BITS, CB, MT>(g, cg, k0, min(g.kc, g.K - k0), a_lds, colsum, before_input, after_input);
 }
 
 // Cross-workgroup handoff of split-K partials.  An agent-scope release/acquire fence pair would
@@ -343,13 +534,25 @@ __device__ inline bool arrive_last(int* counter, int target)
 template <int MT>
 HX_INLINE void gather_partials(const float* partial, int M, int N, int splits, int cg, float* colsum)
 {
+    // the loads of 8 splits are issued together, then added in split order
+    constexpr int B = 8;
     for (int i = threadIdx.x; i < MT * 128; i += GEMV_THREADS) {
         const int m = i >> 7, c = i & 127;
         float v = 0.0f;
-        if (m < M)
-            for (int sp = 0; sp < splits; ++sp)
-                v += __hip_atomic_load(&partial[((size_t)sp * M + m) * N + cg * 128 + c], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+        if (m < M) {
+            const float* p = partial + (size_t)m * N + cg * 128 + c;
+            const size_t stride = (size_t)M * N;
+            for (int s0 = 0; s0 < splits; s0 += B) {
+                float t[B];
+#pragma unroll
+                for (int j = 0; j < B; ++j)
+                    t[j] = __hip_atomic_load(p + (size_t)min(s0 + j, splits - 1) * stride, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int j = 0; j < B; ++j)
+                    if (s0 + j < splits) v += t[j];
+            }
+        }
         colsum[i] = v;
     }
     __syncthreads();

@@ -7,25 +7,41 @@
 
 #include <stdlib.h>
 
+#include <mutex>
+#include <vector>
+
 namespace hx {
 
-hipError_t launch_moe_decode_phase_m1(const MoeDecodeArgs& a, int cb, bool gu, int bits, hipStream_t st);
-hipError_t launch_moe_decode_phase_m4(const MoeDecodeArgs& a, int cb, bool gu, int bits, hipStream_t st);
-hipError_t launch_moe_decode_phase_m8(const MoeDecodeArgs& a, int cb, bool gu, int bits, hipStream_t st);
+hipError_t launch_moe_decode_m1(const MoeDecodeArgs& a, int cb, int bits, hipStream_t st);
+hipError_t launch_moe_decode_m4(const MoeDecodeArgs& a, int cb, int bits, hipStream_t st);
+hipError_t launch_moe_decode_m8(const MoeDecodeArgs& a, int cb, int bits, hipStream_t st);
+
+// Workgroups of `kernel` (256 threads, `lds` dynamic LDS bytes) that fit on the current device at
+// once: CU count times blocks per CU, cached per (device, kernel, lds).
+int resident_blocks(const void* kernel, size_t lds)
+{
+    struct Key {
+        int dev;
+        const void* k;
+        size_t lds;
+        int n;
+    };
+    static std::mutex mu;
+    static std::vector<Key> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Key& c : cache)
+        if (c.dev == dev && c.k == kernel && c.lds == lds) return c.n;
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, GEMV_THREADS, lds) != hipSuccess || per <= 0)
+        per = 1;
+    cache.push_back({dev, kernel, lds, cus * per});
+    return cus * per;
+}
 
 static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
-
-// Split-K plan: K per split = largest multiple-of-128 divisor of K up to `cap` (HX_MOE_KC overrides
-// the cap for tuning); the activation block (8 x kc fp16) stays within LDS.
-static void split_plan(int K, int max_bits, int* splits, int* kc)
-{
-    (void)max_bits;
-    int cap = 1024;
-    if (const char* v = getenv("HX_MOE_KC")) cap = atoi(v) > 0 ? atoi(v) : cap;
-    if (cap > 2048) cap = 2048;
-    *kc = gemv_kc_for(K, cap);
-    *splits = K / *kc;
-}
 
 void MoeWs::plan(int T_, int hidden_, int inter_, int E_, int topk_, bool shared_, int max_bits)
 {
@@ -37,8 +53,7 @@ void MoeWs::plan(int T_, int hidden_, int inter_, int E_, int topk_, bool shared
     R = T * topk;
     routed_slots = R < E ? R : E;
     slots = routed_slots + 1;
-    split_plan(hidden, max_bits, &splits_gu, &kc_gu);
-    split_plan(inter, max_bits, &splits_d, &kc_d);
+    (void)max_bits;
     size_t o = HX_COUNTER_BYTES;
     off_idx = o;      o = al(o + sizeof(int64_t) * R);
     off_w = o;        o = al(o + sizeof(_Float16) * R);
@@ -48,9 +63,13 @@ void MoeWs::plan(int T_, int hidden_, int inter_, int E_, int topk_, bool shared
     off_r2s = o;      o = al(o + sizeof(int64_t) * R);
     if (T <= 8 && R <= 64) {
         off_plan = o;     o = al(o + sizeof(DecodePlan));
-        off_pg = o;   o = al(o + sizeof(float) * slots * splits_gu * 8 * inter);
-        off_pu = o;   o = al(o + sizeof(float) * slots * splits_gu * 8 * inter);
-        off_pd = o;   o = al(o + sizeof(float) * slots * splits_d * 8 * hidden);
+        // partial sums: one 8 x 128 slot per (slot, column group, segment); a column group has at
+        // most K/128 segments (every share holds at least one 128-k block)
+        const size_t seg_g = (size_t)slots * (inter / 128) * (hidden / 128 + 1) * 8 * 128;
+        const size_t seg_d = (size_t)slots * (hidden / 128) * (inter / 128 + 1) * 8 * 128;
+        off_pg = o;   o = al(o + sizeof(float) * seg_g);
+        off_pu = o;   o = al(o + sizeof(float) * seg_g);
+        off_pd = o;   o = al(o + sizeof(float) * seg_d);
         off_act = o;  o = al(o + sizeof(_Float16) * slots * 8 * inter);
         off_contrib = o; o = al(o + sizeof(float) * (size_t)(R + T) * hidden);
     } else {
@@ -69,14 +88,15 @@ MoeDecodeArgs MoeWs::decode_args(char* base) const
     a.E = E;
     a.topk = topk;
     a.routed_slots = routed_slots;
-    a.splits_gu = splits_gu;
-    a.kc_gu = kc_gu;
-    a.splits_d = splits_d;
-    a.kc_d = kc_d;
     a.counter_gu = reinterpret_cast<int*>(base);
-    a.counter_d = reinterpret_cast<int*>(base) + 6144;
-    a.counter_y = reinterpret_cast<int*>(base) + 12288;
-    a.plan = reinterpret_cast<DecodePlan*>(base + off_plan);
+    int* ctr = reinterpret_cast<int*>(base);
+    a.counter_d = ctr + 4096;
+    a.counter_y = ctr + 8192;
+    a.exit_count = ctr + 10240;
+    a.queue_gu = ctr + 10241;
+    a.queue_d = ctr + 10242;
+    a.ready = ctr + 10304;
+    a.status = reinterpret_cast<int*>(base + off_plan);
     a.contrib = reinterpret_cast<float*>(base + off_contrib);
     a.partial_g = reinterpret_cast<float*>(base + off_pg);
     a.partial_u = reinterpret_cast<float*>(base + off_pu);
@@ -85,25 +105,20 @@ MoeDecodeArgs MoeWs::decode_args(char* base) const
     return a;
 }
 
-static hipError_t decode_phase(const MoeDecodeArgs& a, int cb, bool gu, int bits, hipStream_t st)
-{
-    if (a.T <= 1) return launch_moe_decode_phase_m1(a, cb, gu, bits, st);
-    if (a.T <= 4) return launch_moe_decode_phase_m4(a, cb, gu, bits, st);
-    return launch_moe_decode_phase_m8(a, cb, gu, bits, st);
-}
-
-hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t mask_gu, uint32_t mask_d, hipStream_t st)
+hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t bits_mask, hipStream_t st)
 {
     if (a.T > 8 || a.T * a.topk > DEC_MAX_R) return hipErrorInvalidValue;
-    if ((a.routed_slots + 1) * (a.inter / 128) > 6144 || (a.routed_slots + 1) * (a.hidden / 128) > 6144 ||
-        a.hidden / 128 > 4096)
+    // counter area (ints): counter_gu [0, 4096), counter_d [4096, 8192), counter_y [8192, 10240),
+    // exit 10240, queue_gu 10241, queue_d 10242, ready [10304, 16384)
+    const int slots = a.routed_slots + 1;
+    if (slots * (a.inter / 128) > 4096 || slots * (a.hidden / 128) > 4096 || a.hidden / 128 > 2048 ||
+        slots * (a.inter / 128) > 6080)
         return hipErrorInvalidValue;
-    hipError_t e = hipSuccess;
-    for (int b = 1; b <= 8 && e == hipSuccess; ++b)
-        if (mask_gu & (1u << b)) e = decode_phase(a, cb, true, b, st);
-    for (int b = 1; b <= 8 && e == hipSuccess; ++b)
-        if (mask_d & (1u << b)) e = decode_phase(a, cb, false, b, st);
-    return e;
+    // one bit width everywhere -> the fixed-width kernel; several -> per-unit dispatch
+    const int bits = (bits_mask & (bits_mask - 1)) ? 0 : __builtin_ctz(bits_mask);
+    if (a.T <= 1) return launch_moe_decode_m1(a, cb, bits, st);
+    if (a.T <= 4) return launch_moe_decode_m4(a, cb, bits, st);
+    return launch_moe_decode_m8(a, cb, bits, st);
 }
 
 

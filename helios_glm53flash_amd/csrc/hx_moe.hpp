@@ -13,7 +13,6 @@ struct MoeDecodeArgs;
 struct MoeWs {
     int T = 0, hidden = 0, inter = 0, E = 0, topk = 0, R = 0;
     int routed_slots = 0, slots = 0;
-    int splits_gu = 1, kc_gu = 128, splits_d = 1, kc_d = 128;
     size_t off_idx = 0, off_w = 0, off_count = 0, off_tsorted = 0, off_wsorted = 0, off_r2s = 0;
     // few-token path
     size_t off_plan = 0, off_pg = 0, off_pu = 0, off_pd = 0, off_act = 0, off_contrib = 0;
@@ -48,7 +47,9 @@ struct PrefillArgs {
     const MoeWs* lay;
 };
 
-hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t mask_gu, uint32_t mask_d, hipStream_t st);
+// Few-token layer (one persistent launch); bits_mask has bit b set for every bit width b in use.
+hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t bits_mask, hipStream_t st);
+int resident_blocks(const void* kernel, size_t lds);
 // Routed experts for T > 8 tokens: writes per-row fp32 contributions (sorted order) when contrib is
 // non-null, y = fp16(routed + shared_rows) when y is non-null, and the fp32 routed sum into
 // y_routed (added to its contents when accumulate) when y_routed is non-null.

@@ -57,16 +57,19 @@ struct MoeDecodeArgs {
     int sh_bits[3];
     float act_limit;
     int routed_slots;              // upper bound of active experts = min(E, T*topk)
-    int splits_gu, kc_gu, splits_d, kc_d;
     // workspace
     int* counter_gu;               // [slots][inter/128]
     int* counter_d;                // [slots][hidden/128]
     int* counter_y;                // [hidden/128]
-    float* partial_g;              // [slots][splits_gu][8][inter]
+    float* partial_g;              // [slots][inter/128][hidden/128 + 1 segments][8][128]
     float* partial_u;
-    float* partial_d;              // [slots][splits_d][8][hidden]
+    float* partial_d;              // [slots][hidden/128][inter/128 + 1 segments][8][128]
     _Float16* act;                 // [slots][8][inter]  (down-projection input, already transformed)
-    DecodePlan* plan;              // written by workgroup 0 of kernel A
+    int* exit_count;               // workgroups that finished (zero between calls)
+    int* queue_gu;                 // next dynamic chunk of the gate/up and down phases
+    int* queue_d;
+    int* ready;                    // [slots][inter/128] 1 once the guad epilogue stored that block
+    int* status;                   // set to 1 when a bounded wait gave up (never expected)
     // outputs
     int64_t* out_idx;              // optional router outputs [T][topk]
     _Float16* out_w;
@@ -104,16 +107,16 @@ HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, in
         // one u32 (larger = higher logit, then lower index; +0 above -0 as in the fp32 encoding)
         constexpr int PER = 8;  // E <= 512
         uint32_t cand[PER];
+        uint16_t raw[PER];
+        // all loads first (clamped addresses, no branches) so their latencies overlap
+#pragma unroll
+        for (int i = 0; i < PER; ++i) raw[i] = h_as_u16(scores[min(lane + 64 * i, E - 1)]);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int e = lane + 64 * i;
-            uint32_t c = 0;
-            if (e < E) {
-                uint32_t h = h_as_u16(scores[e]);
-                h = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
-                c = (h << 16) | (0xffffu - (uint32_t)e);
-            }
-            cand[i] = c;
+            uint32_t h = raw[i];
+            h = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+            cand[i] = e < E ? (h << 16) | (0xffffu - (uint32_t)e) : 0u;
         }
         float sum = 0.0f;
         e_out = 0;
@@ -145,9 +148,9 @@ HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, in
     _Float16 sv[PER], bv[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const int e = lane + 64 * i;
-        sv[i] = e < E ? scores[e] : (_Float16)0.0f;
-        bv[i] = (bias && e < E) ? bias[e] : (_Float16)0.0f;
+        const int e = min(lane + 64 * i, E - 1);
+        sv[i] = scores[e];
+        bv[i] = bias[e];
     }
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -205,7 +208,7 @@ HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, in
 
 // Build the plan in LDS (every workgroup computes the same plan).  Layer mode routes the tokens;
 // grouped mode reads the caller's expert_count / token_sorted / weight_sorted.
-__device__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p)
+__device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p)
 {
     __shared__ int sel_e[DEC_MAX_R];
     __shared__ float sel_w[DEC_MAX_R];
@@ -311,18 +314,46 @@ HX_INLINE SlotInfo slot_info(const MoeDecodeArgs& a, const DecodePlan& p, int sl
     return si;
 }
 
-HX_INLINE int proj_bits(const MoeDecodeArgs& a, int proj, int expert)
+// Element `i` of a 3-array member of the kernel arguments, by selects rather than a run-time index:
+// indexing an argument array at run time makes the compiler copy the whole argument block into
+// per-lane scratch memory.
+// The loaded values pass through an empty asm so that the compiler cannot turn the selects back
+// into one load from a computed address.
+template <class T>
+HX_INLINE T opaque_value(T v)
 {
-    if (expert < 0) return a.sh_bits[proj];
-    return a.bits_tab[proj] ? a.bits_tab[proj][expert] : a.bits_uniform[proj];
+    static_assert(sizeof(T) == 8 || sizeof(T) == 4, "pointer or 32-bit value");
+    if constexpr (sizeof(T) == 8) {
+        uint64_t u = __builtin_bit_cast(uint64_t, v);
+        asm volatile("" : "+s"(u));
+        return __builtin_bit_cast(T, u);
+    } else {
+        uint32_t u = __builtin_bit_cast(uint32_t, v);
+        asm volatile("" : "+s"(u));
+        return __builtin_bit_cast(T, u);
+    }
 }
 
-// ------------------------------------------------------------------ kernel A: gate/up + SiLU-gate
+template <class T>
+HX_INLINE T pick3(const T (&v)[3], int i)
+{
+    const T v0 = opaque_value(v[0]), v1 = opaque_value(v[1]), v2 = opaque_value(v[2]);
+    return i == 0 ? v0 : (i == 1 ? v1 : v2);
+}
+
+HX_INLINE int proj_bits(const MoeDecodeArgs& a, int proj, int expert)
+{
+    if (expert < 0) return pick3(a.sh_bits, proj);
+    const int32_t* bt = pick3(a.bits_tab, proj);
+    return bt ? bt[expert] : pick3(a.bits_uniform, proj);
+}
+
+// ------------------------------------------------------------------ epilogues
 
 // guad epilogue for rows m < count of one 128-column group (hadamard_inner.cuh:284-413 for routed
 // experts; swiglu_clamp + down-input transform for the shared expert, runner.cpp:723-738).
 template <int MT>
-__device__ void guad_epilogue(const MoeDecodeArgs& a, const SlotInfo& si, int slot, int cg, const float* cs_g,
+__device__ __forceinline__ void guad_epilogue(const MoeDecodeArgs& a, const SlotInfo& si, int slot, int cg, const float* cs_g,
                               const float* cs_u)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -371,86 +402,17 @@ __device__ void guad_epilogue(const MoeDecodeArgs& a, const SlotInfo& si, int sl
         float p0 = (float)p.x, p1 = (float)p.y;
         hx_had128_wave(p0, p1);
         hx_h2 o = {(_Float16)p0, (_Float16)p1};
-        *reinterpret_cast<hx_h2*>(a.act + ((size_t)slot * 8 + m) * a.inter + c) = o;
+        // read by the down-projection units of other workgroups of this launch
+        __hip_atomic_store(reinterpret_cast<uint32_t*>(a.act + ((size_t)slot * 8 + m) * a.inter + c), h2_as_u32(o),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-template <int BITS, int CB, int MT>
-__global__ __launch_bounds__(GEMV_THREADS) void moe_decode_gu_kernel(MoeDecodeArgs a)
-{
-    extern __shared__ uint32_t a_lds[];
-    __shared__ float cs_g[MT * 128];
-    __shared__ float cs_u[MT * 128];
-    __shared__ DecodePlan plan;
-    __shared__ int rows[8];
-    const int groups = a.inter >> 7;
-    const int per_slot = 2 * groups * a.splits_gu;
-    const int slot = blockIdx.x / per_slot;
-    int r = blockIdx.x % per_slot;
-    const int s = r / (2 * groups);
-    r %= 2 * groups;
-    const int proj = r / groups;  // 0 gate, 1 up
-    const int cg = r % groups;
-
-    build_plan(a, plan);
-    if (blockIdx.x == 0) {
-        // publish the plan (and the router outputs) for kernel B and the caller
-        const int R = a.T * a.topk;
-        for (int i = threadIdx.x; i < R; i += GEMV_THREADS) {
-            a.plan->token[i] = plan.token[i];
-            a.plan->weight[i] = plan.weight[i];
-            a.plan->r2s[i] = plan.r2s[i];
-            a.plan->expert[i] = plan.expert[i];
-            a.plan->start[i] = plan.start[i];
-            a.plan->count[i] = plan.count[i];
-        }
-        if (threadIdx.x == 0) a.plan->n = plan.n;
-        if (a.out_idx)
-            for (int i = threadIdx.x; i < R; i += GEMV_THREADS) {
-                const int pos = plan.r2s[i];
-                int e = 0;
-                for (int q = 0; q < plan.n; ++q)
-                    if (pos >= plan.start[q] && pos < plan.start[q] + plan.count[q]) e = plan.expert[q];
-                a.out_idx[i] = e;
-                a.out_w[i] = (_Float16)plan.weight[pos];
-            }
-    }
-    const SlotInfo si = slot_info(a, plan, slot);
-    if (!si.valid) return;
-    if (proj_bits(a, proj, si.expert) != BITS) return;
-    const bool shared = si.expert < 0;
-    if (threadIdx.x < 8)
-        rows[threadIdx.x] = shared ? (int)threadIdx.x : plan.token[si.start + min((int)threadIdx.x, si.count - 1)];
-    __syncthreads();
-
-    GemvArgs g;
-    g.x = a.x;
-    g.rows = rows;
-    g.trellis = static_cast<const uint16_t*>(shared ? a.sh_tr[proj] : a.tr[proj][si.expert]);
-    g.suh = static_cast<const _Float16*>(shared ? a.sh_suh[proj] : a.suh[proj][si.expert]);
-    g.M = si.count;
-    g.K = a.hidden;
-    g.N = a.inter;
-    g.splits = a.splits_gu;
-    g.kc = a.kc_gu;
-    g.pre_transformed = false;
-    float* partial = (proj == 0 ? a.partial_g : a.partial_u) + (size_t)slot * a.splits_gu * 8 * a.inter;
-    g.partial = partial;
-
-    gemv_split_sum<BITS, CB, MT>(g, cg, s, a_lds, cs_g);
-    publish_partial<MT>(partial, g.M, g.N, cg, s, cs_g);
-    if (!arrive_last(&a.counter_gu[slot * groups + cg], 2 * a.splits_gu)) return;
-    gather_partials<MT>(a.partial_g + (size_t)slot * a.splits_gu * 8 * a.inter, g.M, g.N, a.splits_gu, cg, cs_g);
-    gather_partials<MT>(a.partial_u + (size_t)slot * a.splits_gu * 8 * a.inter, g.M, g.N, a.splits_gu, cg, cs_u);
-    guad_epilogue<MT>(a, si, slot, cg, cs_g, cs_u);
-}
-
-// ------------------------------------------------------------------ kernel B: down + contributions + combine
 
 // Weighted contribution rows of one 128-column group (hadamard_inner.cuh:418-481: D rounded to fp16,
 // transform, times weight / sqrt(128) and svh_d in fp32; the shared expert keeps D in fp32).
 template <int MT>
-__device__ void down_epilogue(const MoeDecodeArgs& a, const DecodePlan& p, const SlotInfo& si, int cg,
+__device__ __forceinline__ void down_epilogue(const MoeDecodeArgs& a, const DecodePlan& p, const SlotInfo& si, int cg,
                               const float* cs)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -484,53 +446,153 @@ __device__ void down_epilogue(const MoeDecodeArgs& a, const DecodePlan& p, const
 
 // y[t][c] = fp16((sum_j contrib[r2s[t*topk + j]][c], ascending j from +0) + shared[t][c])
 // (glue2.cu:297-306 then runner.cpp:957-958) for one 128-column group.
-__device__ void combine_columns(const MoeDecodeArgs& a, const DecodePlan& p, int cg, bool has_shared)
+__device__ __forceinline__ void combine_columns(const MoeDecodeArgs& a, const DecodePlan& p, int cg, bool has_shared)
 {
     const int R = a.T * a.topk;
     for (int i = threadIdx.x; i < a.T * 128; i += GEMV_THREADS) {
         const int t = i >> 7;
         const int c = cg * 128 + (i & 127);
+        // the loads of 8 contributions (and the shared row) are issued together, then added in
+        // routing-rank order
+        constexpr int B = 8;
         float acc = 0.0f;
-        for (int j = 0; j < a.topk; ++j)
-            acc += __hip_atomic_load(a.contrib + (size_t)p.r2s[t * a.topk + j] * a.hidden + c, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
+        for (int j0 = 0; j0 < a.topk; j0 += B) {
+            float v[B];
+#pragma unroll
+            for (int j = 0; j < B; ++j)
+                v[j] = __hip_atomic_load(a.contrib + (size_t)p.r2s[t * a.topk + min(j0 + j, a.topk - 1)] * a.hidden + c,
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int j = 0; j < B; ++j)
+                if (j0 + j < a.topk) acc += v[j];
+        }
+        const float sh = has_shared ? __hip_atomic_load(a.contrib + (size_t)(R + t) * a.hidden + c, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT)
+                                    : 0.0f;
         const size_t o = (size_t)t * a.hidden + c;
         if (a.y_routed) a.y_routed[o] = a.y_accumulate ? a.y_routed[o] + acc : acc;
-        if (has_shared)
-            acc += __hip_atomic_load(a.contrib + (size_t)(R + t) * a.hidden + c, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
+        if (has_shared) acc += sh;
         if (a.y) a.y[o] = (_Float16)acc;
     }
 }
 
-template <int BITS, int CB, int MT>
-__global__ __launch_bounds__(GEMV_THREADS) void moe_decode_d_kernel(MoeDecodeArgs a)
-{
-    extern __shared__ uint32_t a_lds[];
-    __shared__ float cs[MT * 128];
-    __shared__ DecodePlan plan;
-    const int groups = a.hidden >> 7;
-    const int per_slot = groups * a.splits_d;
-    const int slot = blockIdx.x / per_slot;
-    const int r = blockIdx.x % per_slot;
-    const int s = r / groups;
-    const int cg = r % groups;
 
-    // plan from kernel A
-    const int R = a.T * a.topk;
-    for (int i = threadIdx.x; i < R; i += GEMV_THREADS) {
-        plan.token[i] = a.plan->token[i];
-        plan.weight[i] = a.plan->weight[i];
-        plan.r2s[i] = a.plan->r2s[i];
-        plan.expert[i] = a.plan->expert[i];
-        plan.start[i] = a.plan->start[i];
-        plan.count[i] = a.plan->count[i];
+// ------------------------------------------------------------------ the layer kernel
+//
+// One launch per layer call, every workgroup resident at once (the grid never exceeds what fits).
+// Work is split in 128-k blocks, balanced exactly: the gate/up blocks of all active slots
+// (ordered slot, projection, column group, k) are cut into gridDim.x equal contiguous shares, then
+// the down blocks likewise.  A share covers at most a few (slot, projection, column group) segments;
+// each segment's partial sum goes to its own workspace slot and the last of the segments of a column
+// group adds them in segment order (deterministic), then runs the epilogue.  A workgroup that
+// finishes its gate/up share requests the tile words of its down share first and only then waits
+// for the activations it needs (per slot and 128-column block), so the down projection's HBM
+// latency overlaps the end of the gate/up phase.
+
+// Bounded wait of thread 0 for *flag >= target (the producers are resident workgroups that do not
+// wait for anything themselves, so the wait ends; the bound only turns a bug into a flagged wrong
+// result instead of a hung device).
+HX_INLINE void wait_flag(const int* flag, int target, int* status)
+{
+    int spins = 0;
+    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+        __builtin_amdgcn_s_sleep(8);
+        if (++spins > (1 << 22)) {
+            __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
     }
-    if (threadIdx.x == 0) plan.n = a.plan->n;
-    __syncthreads();
+}
+
+// Work split of n blocks: the first ns are cut into g equal contiguous static shares (share w is
+// [sstart(w), sstart(w+1))), the rest into chunks of `chunk` blocks that finished workgroups take
+// from a counter, so that workgroups that run slower (later dispatch, a busier XCD) take fewer.  A
+// column group c (blocks [c*kb, c*kb + kb)) is covered by static segments, then chunk segments;
+// segment indices count in k order, so the partial sums are always added in the same order.
+struct Split {
+    long n, ns;
+    int g, chunk;
+    HX_INLINE long sstart(int w) const { return (long)w * ns / g; }
+    HX_INLINE int sowner(long x) const { return (int)(((x + 1) * g - 1) / ns); }
+    HX_INLINE long nchunks() const { return (n - ns + chunk - 1) / chunk; }
+    HX_INLINE int count(long c, int kb) const
+    {
+        const long lo = c * kb, hi = lo + kb;
+        int cnt = 0;
+        if (lo < ns) cnt += sowner(min(hi, ns) - 1) - sowner(lo) + 1;
+        if (hi > ns) cnt += (int)((hi - 1 - ns) / chunk - (max(lo, ns) - ns) / chunk + 1);
+        return cnt;
+    }
+    HX_INLINE int index(long c, int kb, long b) const  // b: first block of the segment
+    {
+        const long lo = c * kb;
+        if (b < ns) return sowner(b) - sowner(lo);
+        const int cs = lo < ns ? sowner(min(lo + kb, ns) - 1) - sowner(lo) + 1 : 0;
+        return cs + (int)((b - ns) / chunk - (max(lo, ns) - ns) / chunk);
+    }
+};
+
+// Three quarters static, the rest in chunks of 2 blocks; every static share holds at least one
+// block.
+HX_INLINE Split make_split(long n, int G)
+{
+    Split sp;
+    sp.n = n;
+    sp.g = (int)min((long)G, n);
+    sp.ns = n;  // all static (a dynamic tail costs a ramp per chunk, more than it balances)
+    sp.chunk = 2;
+    return sp;
+}
+
+template <int BITS, int CB, int MT>
+__device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, long c,
+                                           int kb0, int kb1, uint32_t* a_lds, float* cs_g, float* cs_u, int* rows)
+{
+    const int gg = a.inter >> 7, KB = a.hidden >> 7;
+    const int aslot = (int)(c / (2 * gg)), proj = (int)((c / gg) & 1), cg = (int)(c % gg);
+    const int slot = aslot < plan.n ? aslot : a.routed_slots;
     const SlotInfo si = slot_info(a, plan, slot);
-    if (!si.valid) return;
-    if (proj_bits(a, 2, si.expert) != BITS) return;
+    const bool shared = si.expert < 0;
+    if (threadIdx.x < 8)
+        rows[threadIdx.x] = shared ? (int)threadIdx.x : plan.token[si.start + min((int)threadIdx.x, si.count - 1)];
+    hx_lds_barrier();
+
+    GemvArgs g;
+    g.x = a.x;
+    g.rows = rows;
+    g.trellis = static_cast<const uint16_t*>(shared ? pick3(a.sh_tr, proj) : pick3(a.tr, proj)[si.expert]);
+    g.suh = static_cast<const _Float16*>(shared ? pick3(a.sh_suh, proj) : pick3(a.suh, proj)[si.expert]);
+    g.M = si.count;
+    g.K = a.hidden;
+    g.N = a.inter;
+    g.pre_transformed = false;
+    gemv_range<BITS, CB, MT>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
+
+    // partial of segment i of (slot, proj, cg): partial_{g,u}[((slot*gg + cg) * (KB + 1) + i) * 8 + m][128]
+    float* pbase = (proj == 0 ? a.partial_g : a.partial_u) + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
+    publish_partial<MT>(pbase, si.count, 128, 0, sp.index(c, KB, c * KB + kb0), cs_g);
+    const long cgate = c - proj * gg, cup = cgate + gg;
+    const int ng = sp.count(cgate, KB), nu = sp.count(cup, KB);
+    if (!arrive_last(&a.counter_gu[slot * gg + cg], ng + nu)) return;
+    float* pg = a.partial_g + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
+    float* pu = a.partial_u + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
+    gather_partials<MT>(pg, si.count, 128, ng, 0, cs_g);
+    gather_partials<MT>(pu, si.count, 128, nu, 0, cs_u);
+    guad_epilogue<MT>(a, si, slot, cg, cs_g, cs_u);
+    // the activations of this block are stored (device-coherent): flag them for the down phase
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(&a.ready[slot * gg + cg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int BITS, int CB, int MT>
+__device__ __forceinline__ void d_segment(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, long c,
+                                          int kb0, int kb1, uint32_t* a_lds, float* cs)
+{
+    const int gd = a.hidden >> 7, gg = a.inter >> 7, KB = a.inter >> 7;
+    const int aslot = (int)(c / gd), cg = (int)(c % gd);
+    const int slot = aslot < plan.n ? aslot : a.routed_slots;
+    const SlotInfo si = slot_info(a, plan, slot);
     const bool shared = si.expert < 0;
 
     GemvArgs g;
@@ -541,23 +603,158 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_decode_d_kernel(MoeDecodeArg
     g.M = si.count;
     g.K = a.inter;
     g.N = a.hidden;
-    g.splits = a.splits_d;
-    g.kc = a.kc_d;
     g.pre_transformed = true;
-    float* partial = a.partial_d + (size_t)slot * a.splits_d * 8 * a.hidden;
-    g.partial = partial;
+    // the input blocks kb0..kb1-1 of this slot are the guad outputs of gate/up column groups kb0..kb1-1
+    auto wait_inputs = [&]() {
+        if (threadIdx.x == 0)
+            for (int kb = kb0; kb < kb1; ++kb) wait_flag(&a.ready[slot * gg + kb], 1, a.status);
+        hx_lds_barrier();
+    };
+    gemv_range<BITS, CB, MT>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs, wait_inputs);
 
-    gemv_split_sum<BITS, CB, MT>(g, cg, s, a_lds, cs);
-    if (a.splits_d > 1) {
-        publish_partial<MT>(partial, g.M, g.N, cg, s, cs);
-        if (!arrive_last(&a.counter_d[slot * groups + cg], a.splits_d)) return;
-        gather_partials<MT>(partial, g.M, g.N, a.splits_d, cg, cs);
-    }
+    const int count = sp.count(c, KB);
+    float* pbase = a.partial_d + (size_t)(slot * gd + cg) * (KB + 1) * 8 * 128;
+    publish_partial<MT>(pbase, si.count, 128, 0, sp.index(c, KB, c * KB + kb0), cs);
+    if (!arrive_last(&a.counter_d[slot * gd + cg], count)) return;
+    gather_partials<MT>(pbase, si.count, 128, count, 0, cs);
     down_epilogue<MT>(a, plan, si, cg, cs);
     if (!a.combine) return;
     const bool has_shared = a.sh_tr[0] != nullptr;
     if (!arrive_last(&a.counter_y[cg], plan.n + (has_shared ? 1 : 0))) return;
     combine_columns(a, plan, cg, has_shared);
+}
+
+// Bits of a projection of a slot's expert (the shared slot uses the shared expert's).
+HX_INLINE int slot_bits(const MoeDecodeArgs& a, const DecodePlan& p, int slot, int proj)
+{
+    const SlotInfo si = slot_info(a, p, slot);
+    return proj_bits(a, proj, si.valid ? si.expert : 0);
+}
+
+// Runs the blocks [b, e) of a phase as segments of single column groups.
+template <int BITS, int CB, int MT>
+__device__ __forceinline__ void run_blocks(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, int KB,
+                                           bool gu, long b, long e, uint32_t* a_lds, float* cs_g, float* cs_u,
+                                           int* rows)
+{
+    const int gg = a.inter >> 7, gd = a.hidden >> 7;
+    while (b < e) {
+        const long c = b / KB;
+        const int kb0 = (int)(b % KB);
+        const int kb1 = (int)min((long)KB, kb0 + (e - b));
+        int bits = BITS;
+        if constexpr (BITS == 0) {
+            const int aslot = (int)(gu ? c / (2 * gg) : c / gd);
+            bits = slot_bits(a, plan, aslot < plan.n ? aslot : a.routed_slots, gu ? (int)((c / gg) & 1) : 2);
+        }
+        switch (bits) {
+#define HX_SEG_CASE(B)                                                                             \
+    case B:                                                                                        \
+        if constexpr (BITS == 0 || BITS == B) {                                                    \
+            if (gu) gu_segment<B, CB, MT>(a, plan, sp, c, kb0, kb1, a_lds, cs_g, cs_u, rows);        \
+            else d_segment<B, CB, MT>(a, plan, sp, c, kb0, kb1, a_lds, cs_g);                        \
+        }                                                                                          \
+        break;
+            HX_SEG_CASE(1) HX_SEG_CASE(2) HX_SEG_CASE(3) HX_SEG_CASE(4)
+            HX_SEG_CASE(5) HX_SEG_CASE(6) HX_SEG_CASE(7) HX_SEG_CASE(8)
+#undef HX_SEG_CASE
+            default: break;
+        }
+        b += kb1 - kb0;
+    }
+}
+
+// One phase: the static share, then chunks from the phase's counter until none is left.
+template <int BITS, int CB, int MT>
+__device__ __forceinline__ void run_phase(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, int KB,
+                                          bool gu, int* queue, uint32_t* a_lds, float* cs_g, float* cs_u, int* rows)
+{
+    __shared__ int chunk_id;
+    const int w = blockIdx.x;
+    if (w < sp.g) run_blocks<BITS, CB, MT>(a, plan, sp, KB, gu, sp.sstart(w), sp.sstart(w + 1), a_lds, cs_g, cs_u, rows);
+    const long nch = sp.nchunks();
+    for (;;) {
+        __syncthreads();
+        if (threadIdx.x == 0)
+            chunk_id = nch > 0 ? __hip_atomic_fetch_add(queue, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+        __syncthreads();
+        const long j = __builtin_amdgcn_readfirstlane(chunk_id);  // uniform: keeps the unit math scalar
+        if (j >= nch) break;
+        const long b = sp.ns + j * sp.chunk;
+        run_blocks<BITS, CB, MT>(a, plan, sp, KB, gu, b, min(sp.n, b + sp.chunk), a_lds, cs_g, cs_u, rows);
+    }
+}
+
+// BITS = 0 dispatches each segment on its projection's bit width at run time (mixed-bit layers).
+template <int BITS, int CB, int MT>
+__device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
+{
+    extern __shared__ uint32_t a_lds[];
+    __shared__ float cs_g[MT * 128];
+    __shared__ float cs_u[MT * 128];
+    __shared__ DecodePlan plan;
+    __shared__ int rows[8];
+    HX_SETPRIO(3);  // the routing plan gates every workgroup
+    HX_TS_BASE(0);
+    HX_TS(0);
+    build_plan(a, plan);
+    HX_TS(1);
+    HX_TS_BASE(8);
+    if (blockIdx.x == 0 && a.out_idx) {
+        const int R = a.T * a.topk;
+        for (int i = threadIdx.x; i < R; i += GEMV_THREADS) {
+            const int pos = plan.r2s[i];
+            int e = 0;
+            for (int qq = 0; qq < plan.n; ++qq)
+                if (pos >= plan.start[qq] && pos < plan.start[qq] + plan.count[qq]) e = plan.expert[qq];
+            a.out_idx[i] = e;
+            a.out_w[i] = (_Float16)plan.weight[pos];
+        }
+    }
+    const bool has_shared = a.sh_tr[0] != nullptr;
+    const int nact = plan.n + (has_shared ? 1 : 0);
+    const int gg = a.inter >> 7, gd = a.hidden >> 7;
+    const int w = blockIdx.x, G = gridDim.x;
+
+    // gate/up: blocks (aslot, proj, cg, kb) with kb < hidden/128; then down: (aslot, cg, kb), kb < inter/128
+    run_phase<BITS, CB, MT>(a, plan, make_split((long)nact * 2 * gg * (a.hidden >> 7), G), a.hidden >> 7, true,
+                            a.queue_gu, a_lds, cs_g, cs_u, rows);
+    HX_TS_BASE(0);
+    HX_TS(3);
+    HX_TS_BASE(16);
+    run_phase<BITS, CB, MT>(a, plan, make_split((long)nact * gd * (a.inter >> 7), G), a.inter >> 7, false,
+                            a.queue_d, a_lds, cs_g, cs_u, rows);
+
+    HX_TS_BASE(0);
+    HX_TS(4);
+    // the last workgroup to finish clears the activation flags for the next call
+    __shared__ bool last;
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(a.exit_count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
+    __syncthreads();
+    if (last) {
+        for (int i = threadIdx.x; i < (a.routed_slots + 1) * gg; i += GEMV_THREADS)
+            __hip_atomic_store(&a.ready[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) {
+            __hip_atomic_store(a.queue_gu, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.queue_d, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.exit_count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// Fixed bit width: at most 128 VGPRs so that four workgroups share a CU.
+template <int BITS, int CB, int MT>
+__global__ __launch_bounds__(GEMV_THREADS, 4) void moe_decode_kernel(MoeDecodeArgs a)
+{
+    moe_decode_body<BITS, CB, MT>(a);
+}
+
+// Mixed bit widths (per-segment dispatch); the larger code keeps the default register budget.
+template <int CB, int MT>
+__global__ __launch_bounds__(GEMV_THREADS) void moe_decode_mixed_kernel(MoeDecodeArgs a)
+{
+    moe_decode_body<0, CB, MT>(a);
 }
 
 }  // namespace hx
