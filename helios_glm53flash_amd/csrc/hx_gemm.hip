@@ -31,16 +31,17 @@ hipError_t launch_input_had(const _Float16* x, const _Float16* suh, _Float16* a,
 }
 
 // Output epilogue for a staged 64-row half: y[row][cg*128 + c] = svh . H128(C[row][:]).
-__device__ void linear_tile_epilogue(const MfmaSmem& sm, int row0, int rows, const _Float16* svh, void* y, int N,
+template <int CB>
+__device__ void linear_tile_epilogue(const MfmaSmem& sm, int half, int rows, const _Float16* svh, void* y, int N,
                                      int cg, bool y_fp32)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = cg * 128 + 2 * lane;
     const hx_h2 sv = *reinterpret_cast<const hx_h2*>(svh + c);
     for (int r = wave; r < 64; r += 4) {
-        const int row = row0 + r;
+        const int row = 64 * half + r;
         if (row >= rows) break;
-        float v0 = sm.c[r * MF_LDC + 2 * lane], v1 = sm.c[r * MF_LDC + 2 * lane + 1];
+        float v0 = staged_value<CB>(sm, half, r, 2 * lane), v1 = staged_value<CB>(sm, half, r, 2 * lane + 1);
         hx_had128_wave(v0, v1);
         if (y_fp32) {
             *reinterpret_cast<float2*>(static_cast<float*>(y) + (size_t)row * N + c) =
@@ -61,13 +62,13 @@ __global__ __launch_bounds__(MF_THREADS) void linear_mfma_kernel(const _Float16*
     const int cg = blockIdx.x;
     const int m0 = blockIdx.y * MF_BM;
     const int rows = min(MF_BM, M - m0);
-    hx_f4 acc[4][4];
-    mfma_tile<BITS, CB>(a + (size_t)m0 * K, K, rows, trellis, K, N, cg * 8, sm, acc);
+    hx_f4 acc[MF_BM / 32][4];
+    mfma_tile<BITS, CB, MF_BM>(a + (size_t)m0 * K, K, rows, trellis, K, N, cg * 8, sm, acc);
     void* yt = y_fp32 ? (void*)(static_cast<float*>(y) + (size_t)m0 * N) : (void*)(static_cast<_Float16*>(y) + (size_t)m0 * N);
     for (int half = 0; half < 2; ++half) {
-        stage_c_half(acc, half, sm);
+        stage_c_half<MF_BM>(acc, half, sm);
         __syncthreads();
-        linear_tile_epilogue(sm, 64 * half, rows, svh, yt, N, cg, y_fp32);
+        linear_tile_epilogue<CB>(sm, half, rows, svh, yt, N, cg, y_fp32);
         __syncthreads();
     }
 }

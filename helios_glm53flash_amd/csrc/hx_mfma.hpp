@@ -1,132 +1,195 @@
-// hx_mfma.hpp -- EXL3 decode-to-LDS + MFMA tile core for gfx950 (M >= 16 path).
+// hx_mfma.hpp -- EXL3 decode-to-LDS + MFMA tile core for gfx950 (M > 16 paths: the dense linear
+// and the grouped expert GEMM of the prefill).
 //
-// Workgroup = 4 waves, output tile 128 rows x 128 columns (one Hadamard block wide), K consumed
-// in chunks of 64.  Per chunk:
-//   * A (128 x 64 fp16, already input-transformed) is staged to LDS with 16-byte loads;
-//   * B (64 x 128) is decoded from 4 x 8 trellis tiles straight into LDS as fp16 in [n][k] order:
-//     8 threads per tile, thread q of a tile owns positions 32q..32q+31 (columns q and q+8, all 16
-//     k).  Those windows live in stream words [q*bits - 1, q*bits + bits) of the tile, so each
-//     thread loads bits+1 words and every window offset is a compile-time constant;
-//   * each wave computes a 64 x 64 quarter with v_mfma_f32_16x16x32_f16 (fp32 accumulate).
+// Workgroup = 4 waves, output tile BM x 128 (BM = 128 or 64; 128 columns = one Hadamard block),
+// K consumed in chunks of 64, double-buffered in LDS:
+//   * while the matrix cores work on chunk c (from LDS buffer c & 1), the waves load chunk c+1:
+//     A (BM x 64 fp16, already input-transformed) with 16-byte buffer loads, and the trellis words
+//     of its 4 x 8 tiles (thread q of a tile owns positions 32q..32q+31, i.e. columns q and q+8 of
+//     all 16 k; those windows live in stream words [q*bits - 1, q*bits + bits)), then decode the
+//     words on the VALU and store B (128 x 64, [n][k]) and A into the other buffer; one barrier per
+//     chunk.
+//   * each wave computes a (BM/2) x 64 quarter with v_mfma_f32_16x16x32_f16 (fp32 accumulate).
+// Codebook 2 is decoded in affine form (h = 1024 + bytesum, see hx_gemv.hpp): the tile computes
+// sum_k a h, and the epilogue adds the map with the per-row input sums that the tile accumulates
+// from the staged A (v_dot2_f32_f16 against ones).
 // Operand layout of v_mfma_f32_16x16x32_f16 (64 lanes): A: lane l holds row l%16,
 // k = 8*(l/16)..+7; B: column l%16, same k; C: column l%16, rows 4*(l/16)..+3.
 #pragma once
-#include "hx_device.hpp"
+#include "hx_gemv.hpp"
 
 namespace hx {
 
 constexpr int MF_THREADS = 256;
-constexpr int MF_BM = 128;
+constexpr int MF_BM = 128;  // largest row tile
 constexpr int MF_BN = 128;
 constexpr int MF_BK = 64;
 constexpr int MF_LDA = MF_BK + 8;  // halves per LDS row (pad against bank conflicts)
 constexpr int MF_LDC = MF_BN + 4;  // floats per LDS row in the epilogue
+constexpr int MF_AB = (MF_BM + MF_BN) * MF_LDA;  // halves of one A + B buffer
 
 struct MfmaSmem {
     union {
-        struct {
-            _Float16 a[MF_BM * MF_LDA];
-            _Float16 b[MF_BN * MF_LDA];
-        } ab;
-        float c[64 * MF_LDC];
+        _Float16 ab[2][MF_AB];  // [buffer][A rows (MF_BM x LDA), then B columns (128 x LDA)]
+        float c[64 * MF_LDC];   // epilogue staging of 64 rows
     };
+    float rowsum[MF_BM];        // sum_k of each staged A row (codebook-2 map)
 };
 
-// Thread-local decode of 32 positions of one tile: r[0..BITS] are stream words q*BITS-1 .. q*BITS+BITS-1.
-template <int BITS, int CB, int I = 0>
-HX_INLINE void decode_quarter(const uint32_t* r, int q, _Float16* bcol /* Bs + (16*tc)*LDA + 16*tr */)
+HX_INLINE __amdgpu_buffer_rsrc_t mf_rsrc(const void* base, size_t bytes)
 {
-    if constexpr (I < 32) {
-        constexpr int e0 = (I + 1) * BITS + 32, e1 = (I + 2) * BITS + 32;
-        constexpr int s0 = e0 - 16, s1 = e1 - 16;
-        uint32_t w0, w1;
-        if constexpr ((s0 & 31) <= 16) w0 = (r[s0 >> 5] >> (16 - (s0 & 31))) & 0xffffu;
-        else w0 = __builtin_amdgcn_alignbit(r[s0 >> 5], r[(s0 >> 5) + 1], 48 - (s0 & 31)) & 0xffffu;
-        if constexpr ((s1 & 31) <= 16) w1 = (r[s1 >> 5] >> (16 - (s1 & 31))) & 0xffffu;
-        else w1 = __builtin_amdgcn_alignbit(r[s1 >> 5], r[(s1 >> 5) + 1], 48 - (s1 & 31)) & 0xffffu;
-        hx_h2 v = hx_decode2<CB>(w0, w1);
-        constexpr int j = I & 7;
-        constexpr int k = 2 * ((I >> 3) & 3) + 8 * ((j >> 1) & 1);
-        constexpr int nn = 8 * (j >> 2);
-        *reinterpret_cast<hx_h2*>(bcol + (nn + q) * MF_LDA + k) = v;
-        decode_quarter<BITS, CB, I + 2>(r, q, bcol);
-    }
+    const uint64_t u = reinterpret_cast<uint64_t>(base);
+    const uint64_t b = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(u >> 32)) << 32) |
+                       (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)u);
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(b), 0,
+                                             (int)(bytes > 0x7fffffffull ? 0x7fffffffull : bytes), 0x00020000);
 }
 
-// acc[mb][nb] (float4) for this wave's 64 x 64 quarter of the 128 x 128 tile.
-//   A: rows [0, rows) of an fp16 row-major matrix with leading dimension lda (k offset 0 = k 0)
-//   trellis: tile words of the weight; tn0 = first tile column (8 tiles = 128 columns); N columns total.
-template <int BITS, int CB>
-__device__ void mfma_tile(const _Float16* A, long lda, int rows, const uint32_t* trellis, int K, int N, int tn0,
-                          MfmaSmem& sm, hx_f4 (&acc)[4][4])
+// acc[mb][nb] (float4) for this wave's (BM/2) x 64 quarter of the BM x 128 tile; on return
+// sm.rowsum[r] = sum_k A[r][k] when CB == 2.
+//   A: `rows` rows of an fp16 row-major matrix with leading dimension lda (rows past `rows` read 0)
+//   trellis: tile words of the K x N weight; tn0 = first tile column (8 tiles = 128 columns).
+template <int BITS, int CB, int BM>
+__device__ __forceinline__ void mfma_tile(const _Float16* A, long lda, int rows, const uint32_t* trellis, int K, int N,
+                                          int tn0, MfmaSmem& sm, hx_f4 (&acc)[BM / 32][4])
 {
+    static_assert(BM == 64 || BM == 128, "row tile");
+    constexpr int WM = BM / 2, MB = WM / 16;  // wave rows, 16-row blocks per wave
+    constexpr int NA = BM / 32;               // 16-byte A loads per thread per chunk
+    constexpr int NW = 8 * BITS;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int tiles_n = N >> 4;
-    constexpr int NW = 8 * BITS;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = hx_f4{0.f, 0.f, 0.f, 0.f};
 
+    const __amdgpu_buffer_rsrc_t ra = mf_rsrc(A, (size_t)max(rows, 0) * lda * sizeof(_Float16));
+    const __amdgpu_buffer_rsrc_t rt = mf_rsrc(trellis, (size_t)(K >> 4) * tiles_n * NW * 4);
+    // A role: loads i = 0..NA-1 cover row (t + 256 i) / 8, halves 8 * (t % 8) .. +7 of the chunk
+    int a_voff[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int idx = t + MF_THREADS * i;
+        a_voff[i] = (int)(((idx >> 3) * lda + 8 * (idx & 7)) * sizeof(_Float16));
+    }
     // decode role: tile (tr, tc) of the 4 x 8 chunk, quarter q
     const int dtile = t >> 3, q = t & 7;
     const int tr = dtile >> 3, tc = dtile & 7;
+    const int t_off = ((tr * tiles_n + tn0 + tc) * NW) * 4;
+    const int voff0 = t_off + ((q * BITS + NW - 1) % NW) * 4, voff1 = t_off + q * BITS * 4;
+    const int row_bytes = tiles_n * NW * 4;
 
-    for (int k0 = 0; k0 < K; k0 += MF_BK) {
-        // stage A
+    hx_u4v av[NA];
+    uint32_t wv[BITS + 1];
+    float rs[NA];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NA; ++i) rs[i] = 0.0f;
+
+    auto load_chunk = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) av[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[i], k0 * 2, 0);
+        load_quarter_buf<BITS>(wv, rt, voff0, voff1, (k0 >> 4) * row_bytes);
+    };
+    auto store_chunk = [&](int buf, bool count) {
+        _Float16* as = sm.ab[buf];
+        _Float16* bs = sm.ab[buf] + MF_BM * MF_LDA;
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
             const int idx = t + MF_THREADS * i;
-            const int row = idx >> 3, c = idx & 7;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (row < rows) v = *reinterpret_cast<const uint4*>(A + (size_t)row * lda + k0 + 8 * c);
-            *reinterpret_cast<uint4*>(&sm.ab.a[row * MF_LDA + 8 * c]) = v;
+            *reinterpret_cast<hx_u4v*>(&as[(idx >> 3) * MF_LDA + 8 * (idx & 7)]) = av[i];
+            if (CB == 2 && count) {
+                const hx_h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+                float s = rs[i];
+                s = __builtin_amdgcn_fdot2(u32_as_h2(av[i].x), one, s, false);
+                s = __builtin_amdgcn_fdot2(u32_as_h2(av[i].y), one, s, false);
+                s = __builtin_amdgcn_fdot2(u32_as_h2(av[i].z), one, s, false);
+                s = __builtin_amdgcn_fdot2(u32_as_h2(av[i].w), one, s, false);
+                rs[i] = s;
+            }
         }
-        // decode B
-        {
-            const int tk = (k0 >> 4) + tr;
-            const uint32_t* tw = trellis + ((size_t)tk * tiles_n + tn0 + tc) * NW;
-            uint32_t r[BITS + 1];
-            r[0] = tw[(q * BITS + NW - 1) % NW];
-#pragma unroll
-            for (int i = 0; i < BITS; ++i) r[i + 1] = tw[q * BITS + i];
-            decode_quarter<BITS, CB>(r, q, &sm.ab.b[(16 * tc) * MF_LDA + 16 * tr]);
-        }
-        __syncthreads();
+        uint32_t d[16];
+        if constexpr (CB == 2) quarter_affine<BITS>(wv, d);
+        else quarter_decode<BITS, CB>(wv, d);
+        _Float16* bcol = bs + (16 * tc + q) * MF_LDA + 16 * tr;
+        *reinterpret_cast<hx_h8*>(bcol) = quarter_operand<0, 0>(d);
+        *reinterpret_cast<hx_h8*>(bcol + 8) = quarter_operand<0, 1>(d);
+        *reinterpret_cast<hx_h8*>(bcol + 8 * MF_LDA) = quarter_operand<1, 0>(d);
+        *reinterpret_cast<hx_h8*>(bcol + 8 * MF_LDA + 8) = quarter_operand<1, 1>(d);
+    };
+
+    const int nk = K / MF_BK;
+    load_chunk(0);
+    store_chunk(0, true);
+    __syncthreads();
+    for (int c = 0; c < nk; ++c) {
+        const int cur = c & 1;
+        // next chunk's loads (the last iteration repeats the last chunk; its decode is not used)
+        const bool more = c + 1 < nk;
+        load_chunk(min(c + 1, nk - 1) * MF_BK);
+        const _Float16* as = sm.ab[cur];
+        const _Float16* bs = sm.ab[cur] + MF_BM * MF_LDA;
 #pragma unroll
         for (int kk = 0; kk < MF_BK; kk += 32) {
-            hx_h8 af[4], bf[4];
+            hx_h8 af[MB], bf[4];
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
-                af[mb] = *reinterpret_cast<const hx_h8*>(&sm.ab.a[(64 * wm + 16 * mb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
+            for (int mb = 0; mb < MB; ++mb)
+                af[mb] = *reinterpret_cast<const hx_h8*>(&as[(WM * wm + 16 * mb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb)
-                bf[nb] = *reinterpret_cast<const hx_h8*>(&sm.ab.b[(64 * wn + 16 * nb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
+                bf[nb] = *reinterpret_cast<const hx_h8*>(&bs[(64 * wn + 16 * nb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
+            for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
                 for (int nb = 0; nb < 4; ++nb)
                     acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mb], bf[nb], acc[mb][nb], 0, 0, 0);
+        }
+        store_chunk(cur ^ 1, more);
+        __syncthreads();
+    }
+    if constexpr (CB == 2) {
+        // the 8 threads of a row are consecutive lanes
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            float s = rs[i];
+            s += __shfl_xor(s, 1, 64);
+            s += __shfl_xor(s, 2, 64);
+            s += __shfl_xor(s, 4, 64);
+            if ((t & 7) == 0) sm.rowsum[(t + MF_THREADS * i) >> 3] = s;
         }
         __syncthreads();
     }
 }
 
 // Stage rows [64*half, 64*half + 64) of the accumulated tile to LDS (sm.c[row - 64*half][col]).
-HX_INLINE void stage_c_half(const hx_f4 (&acc)[4][4], int half, MfmaSmem& sm)
+template <int BM>
+HX_INLINE void stage_c_half(const hx_f4 (&acc)[BM / 32][4], int half, MfmaSmem& sm)
 {
+    constexpr int WM = BM / 2, MB = WM / 16;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    if (wm == half) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < MB; ++mb) {
+        const int row0 = WM * wm + 16 * mb;  // tile row of this block
+        if (row0 >= 64 * half && row0 < 64 * half + 64) {
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    sm.c[(16 * mb + 4 * (lane >> 4) + r) * MF_LDC + 64 * wn + 16 * nb + (lane & 15)] = acc[mb][nb][r];
+                    sm.c[(row0 - 64 * half + 4 * (lane >> 4) + r) * MF_LDC + 64 * wn + 16 * nb + (lane & 15)] =
+                        acc[mb][nb][r];
+        }
     }
+}
+
+// Staged value of tile row r (within the half) and column c, with the codebook-2 map applied.
+template <int CB>
+HX_INLINE float staged_value(const MfmaSmem& sm, int half, int r, int c)
+{
+    const float v = sm.c[r * MF_LDC + c];
+    if constexpr (CB == 2) return fmaf(v, CB2_SCALE, CB2_BIAS * sm.rowsum[64 * half + r]);
+    else return v;
 }
 
 }  // namespace hx

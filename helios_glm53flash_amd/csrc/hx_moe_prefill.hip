@@ -19,7 +19,7 @@ namespace hx {
 static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Job {
-    int expert, row0, rows, pad;
+    int expert, row0, rows, bm;  // bm: row tile (128, or 64 for a remainder of at most 64 rows)
 };
 
 void MoeWs::prefill_layout(size_t o)
@@ -55,7 +55,10 @@ __global__ __launch_bounds__(256) void prefill_plan_kernel(const int64_t* expert
         for (int e = 0; e < E; ++e) {
             off[e] = acc;
             const int c = (int)expert_count[e];
-            for (int m0 = 0; m0 < c; m0 += MF_BM) jobs[n++] = Job{e, acc + m0, min(MF_BM, c - m0), 0};
+            for (int m0 = 0; m0 < c; m0 += MF_BM) {
+                const int rows = min(MF_BM, c - m0);
+                jobs[n++] = Job{e, acc + m0, rows, rows <= 64 ? 64 : MF_BM};
+            }
             acc += c;
         }
         off[E] = acc;
@@ -115,6 +118,28 @@ struct GroupedGemmArgs {
     int K, N, nproj;
 };
 
+template <int BITS, int CB, int BM>
+__device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job& job, int proj, int cg, MfmaSmem& sm)
+{
+    const _Float16* A = g.A[proj] + (size_t)job.row0 * g.K;
+    const uint32_t* tr = static_cast<const uint32_t*>(g.tr[proj][job.expert]);
+    hx_f4 acc[BM / 32][4];
+    mfma_tile<BITS, CB, BM>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc);
+    _Float16* out = g.out[proj] + (size_t)job.row0 * g.N + cg * 128;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int half = 0; half < BM / 64; ++half) {
+        stage_c_half<BM>(acc, half, sm);
+        __syncthreads();
+        for (int r = wave; r < 64; r += 4) {
+            const int row = 64 * half + r;
+            if (row >= job.rows) break;
+            hx_h2 h = {(_Float16)staged_value<CB>(sm, half, r, 2 * lane), (_Float16)staged_value<CB>(sm, half, r, 2 * lane + 1)};
+            *reinterpret_cast<hx_h2*>(out + (size_t)row * g.N + 2 * lane) = h;
+        }
+        __syncthreads();
+    }
+}
+
 template <int CB>
 __global__ __launch_bounds__(MF_THREADS) void grouped_gemm_kernel(GroupedGemmArgs g)
 {
@@ -126,32 +151,17 @@ __global__ __launch_bounds__(MF_THREADS) void grouped_gemm_kernel(GroupedGemmArg
     const int proj = blockIdx.x / ntiles;
     const int cg = blockIdx.x % ntiles;
     const int bits = g.bits_tab[proj] ? g.bits_tab[proj][job.expert] : g.bits_uniform[proj];
-    const _Float16* A = g.A[proj] + (size_t)job.row0 * g.K;
-    const uint32_t* tr = static_cast<const uint32_t*>(g.tr[proj][job.expert]);
-    hx_f4 acc[4][4];
+#define HX_GG_CASE(B)                                                                      \
+    case B:                                                                                \
+        if (job.bm == 64) grouped_tile<B, CB, 64>(g, job, proj, cg, sm);                    \
+        else grouped_tile<B, CB, MF_BM>(g, job, proj, cg, sm);                              \
+        break;
     switch (bits) {
-        case 1: mfma_tile<1, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
-        case 2: mfma_tile<2, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
-        case 3: mfma_tile<3, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
-        case 4: mfma_tile<4, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
-        case 5: mfma_tile<5, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
-        case 6: mfma_tile<6, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
-        case 7: mfma_tile<7, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
-        default: mfma_tile<8, CB>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc); break;
+        HX_GG_CASE(1) HX_GG_CASE(2) HX_GG_CASE(3) HX_GG_CASE(4)
+        HX_GG_CASE(5) HX_GG_CASE(6) HX_GG_CASE(7) HX_GG_CASE(8)
+        default: break;
     }
-    _Float16* out = g.out[proj] + (size_t)job.row0 * g.N + cg * 128;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int half = 0; half < 2; ++half) {
-        stage_c_half(acc, half, sm);
-        __syncthreads();
-        for (int r = wave; r < 64; r += 4) {
-            const int row = 64 * half + r;
-            if (row >= job.rows) break;
-            hx_h2 h = {(_Float16)sm.c[r * MF_LDC + 2 * lane], (_Float16)sm.c[r * MF_LDC + 2 * lane + 1]};
-            *reinterpret_cast<hx_h2*>(out + (size_t)row * g.N + 2 * lane) = h;
-        }
-        __syncthreads();
-    }
+#undef HX_GG_CASE
 }
 
 // ------------------------------------------------------------------ guad
