@@ -435,7 +435,9 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
     if (r) return r;
     {
         Phase ph(1, st);
-        r = hip_status(hx::launch_permute(idx, wt, tokens, topk, num_experts, cnt, ts, wsorted, r2s, nullptr, st),
+        r = hip_status(hx::launch_permute_chunked(idx, wt, tokens, topk, num_experts, cnt, ts, wsorted, r2s,
+                                                  reinterpret_cast<int*>(base + L.off_perm),
+                                                  reinterpret_cast<int*>(base) + 10250, st),
                        "hx_moe_layer(permute)");
     }
     if (r) return r;

@@ -35,6 +35,11 @@ hipError_t launch_routing(const _Float16* scores, const _Float16* bias, int64_t*
 hipError_t launch_permute(const int64_t* ids, const _Float16* w, int M, int topk, int E, int64_t* expert_count,
                           int64_t* token_sorted, _Float16* weight_sorted, int64_t* route_to_sorted,
                           int64_t* workspace, hipStream_t st);
+// Chunked permutation for many routes (same result as launch_permute): scratch holds
+// 2 * ceil(M*topk/1024) * E ints, arrive is a zero-initialised counter (left zero).
+hipError_t launch_permute_chunked(const int64_t* ids, const _Float16* w, int M, int topk, int E, int64_t* expert_count,
+                                  int64_t* token_sorted, _Float16* weight_sorted, int64_t* route_to_sorted,
+                                  int* scratch, int* arrive, hipStream_t st);
 hipError_t launch_reduce_sorted(float* y, const float* contrib, const int64_t* route_to_sorted, int M, int topk,
                                 int hidden, hipStream_t st);
 hipError_t launch_swiglu_clamp(const float* g, const float* u, _Float16* out, size_t n, float limit, hipStream_t st);

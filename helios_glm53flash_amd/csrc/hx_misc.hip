@@ -184,6 +184,46 @@ hipError_t launch_routing(const _Float16* scores, const _Float16* bias, int64_t*
 constexpr int PERM_THREADS = 1024;
 constexpr int PERM_EMAX = 512;
 
+// Scatter of the routes [base, base + PERM_THREADS) given each expert's next free position in
+// cursor[] (LDS): the waves rank their lanes by ballot and run in wave order, so positions ascend
+// with the flat index within each expert.
+__device__ __forceinline__ void permute_scatter_chunk(const int64_t* ids, const _Float16* w, int total, int topk, int E,
+                                                      int base, int* cursor, int64_t* token_sorted,
+                                                      _Float16* weight_sorted, int64_t* route_to_sorted)
+{
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const int i = base + t;
+    const int64_t e64 = i < total ? ids[i] : -1;
+    const bool valid = e64 >= 0 && e64 < E;
+    const int e = valid ? (int)e64 : -1;
+    int rank = 0, group = 0;
+    bool leader = false;
+    uint64_t remaining = __ballot(valid);
+    while (remaining) {
+        const int ld = __ffsll((unsigned long long)remaining) - 1;
+        const int le = __shfl(e, ld, 64);
+        const uint64_t m = __ballot(valid && e == le);
+        if (valid && e == le) {
+            rank = __popcll(m & lt_mask);
+            group = __popcll(m);
+            leader = (lane == ld);
+        }
+        remaining &= ~m;
+    }
+    for (int wv = 0; wv < PERM_THREADS / 64; ++wv) {
+        if (wave == wv && valid) {
+            const int pos = cursor[e] + rank;
+            __builtin_amdgcn_wave_barrier();
+            if (leader) cursor[e] += group;
+            token_sorted[pos] = i / topk;
+            weight_sorted[pos] = w[i];
+            if (route_to_sorted) route_to_sorted[i] = pos;
+        }
+        __syncthreads();
+    }
+}
+
 __global__ __launch_bounds__(PERM_THREADS) void permute_kernel(const int64_t* ids, const _Float16* w, int total,
                                                                int topk, int E, int64_t* expert_count,
                                                                int64_t* token_sorted, _Float16* weight_sorted,
@@ -191,7 +231,7 @@ __global__ __launch_bounds__(PERM_THREADS) void permute_kernel(const int64_t* id
 {
     __shared__ int cnt[PERM_EMAX];
     __shared__ int cursor[PERM_EMAX];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t = threadIdx.x;
     for (int e = t; e < PERM_EMAX; e += PERM_THREADS) cnt[e] = 0;
     __syncthreads();
     for (int i = t; i < total; i += PERM_THREADS) {
@@ -208,39 +248,90 @@ __global__ __launch_bounds__(PERM_THREADS) void permute_kernel(const int64_t* id
     }
     __syncthreads();
     for (int e = t; e <= E; e += PERM_THREADS) expert_count[e] = e < E ? cnt[e] : 0;
+    for (int base = 0; base < total; base += PERM_THREADS)
+        permute_scatter_chunk(ids, w, total, topk, E, base, cursor, token_sorted, weight_sorted, route_to_sorted);
+}
 
-    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int base = 0; base < total; base += PERM_THREADS) {
-        const int i = base + t;
-        const int64_t e64 = i < total ? ids[i] : -1;
-        const bool valid = e64 >= 0 && e64 < E;
-        const int e = valid ? (int)e64 : -1;
-        int rank = 0, group = 0;
-        bool leader = false;
-        uint64_t remaining = __ballot(valid);
-        while (remaining) {
-            const int ld = __ffsll((unsigned long long)remaining) - 1;
-            const int le = __shfl(e, ld, 64);
-            const uint64_t m = __ballot(valid && e == le);
-            if (valid && e == le) {
-                rank = __popcll(m & lt_mask);
-                group = __popcll(m);
-                leader = (lane == ld);
-            }
-            remaining &= ~m;
-        }
-        for (int wv = 0; wv < PERM_THREADS / 64; ++wv) {
-            if (wave == wv && valid) {
-                const int pos = cursor[e] + rank;
-                __builtin_amdgcn_wave_barrier();
-                if (leader) cursor[e] += group;
-                token_sorted[pos] = i / topk;
-                weight_sorted[pos] = w[i];
-                if (route_to_sorted) route_to_sorted[i] = pos;
-            }
-            __syncthreads();
-        }
+// Many routes: per-chunk histograms, then (last chunk to arrive) each chunk's starting position
+// per expert, then an independent scatter per chunk.  Same positions as permute_kernel.
+__global__ __launch_bounds__(PERM_THREADS) void permute_count_kernel(const int64_t* ids, int total, int E,
+                                                                     int* counts, int* offs, int* arrive,
+                                                                     int64_t* expert_count)
+{
+    __shared__ int hist[PERM_EMAX];
+    __shared__ int tot[PERM_EMAX];
+    __shared__ bool last;
+    const int t = threadIdx.x, chunks = gridDim.x;
+    for (int e = t; e < PERM_EMAX; e += PERM_THREADS) hist[e] = 0;
+    __syncthreads();
+    const int i = blockIdx.x * PERM_THREADS + t;
+    if (i < total) {
+        const int64_t e = ids[i];
+        if (e >= 0 && e < E) atomicAdd(&hist[(int)e], 1);
     }
+    __syncthreads();
+    for (int e = t; e < E; e += PERM_THREADS)
+        __hip_atomic_store(&counts[blockIdx.x * E + e], hist[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t == 0) {
+        last = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == chunks - 1;
+        if (last) __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+    for (int e = t; e < E; e += PERM_THREADS) {
+        int run = 0;
+        for (int c = 0; c < chunks; ++c) {
+            const int v = __hip_atomic_load(&counts[c * E + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            offs[c * E + e] = run;
+            run += v;
+        }
+        tot[e] = run;
+    }
+    __syncthreads();
+    if (t == 0) {
+        int acc = 0;
+        for (int e = 0; e < E; ++e) {
+            const int v = tot[e];
+            tot[e] = acc;
+            acc += v;
+            expert_count[e] = v;
+        }
+        expert_count[E] = 0;
+    }
+    __syncthreads();
+    for (int e = t; e < E; e += PERM_THREADS)
+        for (int c = 0; c < chunks; ++c) offs[c * E + e] += tot[e];
+}
+
+__global__ __launch_bounds__(PERM_THREADS) void permute_scatter_kernel(const int64_t* ids, const _Float16* w, int total,
+                                                                       int topk, int E, const int* offs,
+                                                                       int64_t* token_sorted, _Float16* weight_sorted,
+                                                                       int64_t* route_to_sorted)
+{
+    __shared__ int cursor[PERM_EMAX];
+    for (int e = threadIdx.x; e < E; e += PERM_THREADS) cursor[e] = offs[blockIdx.x * E + e];
+    __syncthreads();
+    permute_scatter_chunk(ids, w, total, topk, E, blockIdx.x * PERM_THREADS, cursor, token_sorted, weight_sorted,
+                          route_to_sorted);
+}
+
+hipError_t launch_permute_chunked(const int64_t* ids, const _Float16* w, int M, int topk, int E, int64_t* expert_count,
+                                  int64_t* token_sorted, _Float16* weight_sorted, int64_t* route_to_sorted,
+                                  int* scratch, int* arrive, hipStream_t st)
+{
+    if (E > PERM_EMAX || E < 1) return hipErrorInvalidValue;
+    const int total = M * topk;
+    const int chunks = (total + PERM_THREADS - 1) / PERM_THREADS;
+    if (chunks == 0) return hipSuccess;
+    int* counts = scratch;
+    int* offs = scratch + (size_t)chunks * E;
+    hipLaunchKernelGGL(permute_count_kernel, dim3(chunks), dim3(PERM_THREADS), 0, st, ids, total, E, counts, offs, arrive,
+                       expert_count);
+    hipLaunchKernelGGL(permute_scatter_kernel, dim3(chunks), dim3(PERM_THREADS), 0, st, ids, w, total, topk, E, offs,
+                       token_sorted, weight_sorted, route_to_sorted);
+    return hipGetLastError();
 }
 
 hipError_t launch_permute(const int64_t* ids, const _Float16* w, int M, int topk, int E, int64_t* expert_count,

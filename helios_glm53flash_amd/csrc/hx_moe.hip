@@ -109,7 +109,7 @@ hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t bits_mask, hipStrea
 {
     if (a.T > 8 || a.T * a.topk > DEC_MAX_R) return hipErrorInvalidValue;
     // counter area (ints): counter_gu [0, 4096), counter_d [4096, 8192), counter_y [8192, 10240),
-    // exit 10240, queue_gu 10241, queue_d 10242, ready [10304, 16384)
+    // exit 10240, queue_gu 10241, queue_d 10242, prefill permutation arrival 10250, ready [10304, 16384)
     const int slots = a.routed_slots + 1;
     if (slots * (a.inter / 128) > 4096 || slots * (a.hidden / 128) > 4096 || a.hidden / 128 > 2048 ||
         slots * (a.inter / 128) > 6080)

@@ -26,6 +26,7 @@ void MoeWs::prefill_layout(size_t o)
 {
     max_jobs = (R + MF_BM - 1) / MF_BM + E;
     const int kmax = hidden > inter ? hidden : inter;
+    off_perm = o;       o = al(o + sizeof(int) * 2 * (size_t)((R + 1023) / 1024) * E);
     off_jobs = o;       o = al(o + sizeof(Job) * max_jobs);
     off_njobs = o;      o = al(o + sizeof(int));
     off_row_expert = o; o = al(o + sizeof(int) * R);
@@ -45,27 +46,40 @@ void MoeWs::prefill_layout(size_t o)
 
 // ------------------------------------------------------------------ plan
 
-__global__ __launch_bounds__(256) void prefill_plan_kernel(const int64_t* expert_count, int E, int R, Job* jobs,
+// Every block scans the expert counts (E <= 512) in LDS; block 0 writes the tile jobs, and each
+// block maps its 256 rows to their expert.
+__global__ __launch_bounds__(512) void prefill_plan_kernel(const int64_t* expert_count, int E, int R, Job* jobs,
                                                           int* njobs, int* row_expert)
 {
-    __shared__ int off[513];
+    __shared__ int off[513];   // exclusive scan of the row counts
+    __shared__ int joff[513];  // exclusive scan of the job counts
     const int t = threadIdx.x;
-    if (t == 0) {
-        int acc = 0, n = 0;
-        for (int e = 0; e < E; ++e) {
-            off[e] = acc;
-            const int c = (int)expert_count[e];
-            for (int m0 = 0; m0 < c; m0 += MF_BM) {
-                const int rows = min(MF_BM, c - m0);
-                jobs[n++] = Job{e, acc + m0, rows, rows <= 64 ? 64 : MF_BM};
-            }
-            acc += c;
+    const int c = t < E ? (int)expert_count[t] : 0;
+    const int nj = (c + MF_BM - 1) / MF_BM;
+    off[t] = c;
+    joff[t] = nj;
+    __syncthreads();
+    for (int d = 1; d < 512; d <<= 1) {  // inclusive Hillis-Steele scans
+        const int a = t >= d ? off[t - d] : 0, b = t >= d ? joff[t - d] : 0;
+        __syncthreads();
+        off[t] += a;
+        joff[t] += b;
+        __syncthreads();
+    }
+    const int r0 = off[t] - c, j0 = joff[t] - nj;  // exclusive
+    if (blockIdx.x == 0) {
+        for (int k = 0; k < nj; ++k) {
+            const int rows = min(MF_BM, c - k * MF_BM);
+            jobs[j0 + k] = Job{t, r0 + k * MF_BM, rows, rows <= 64 ? 64 : MF_BM};
         }
-        off[E] = acc;
-        *njobs = n;
+        if (t == 511) *njobs = joff[511];
     }
     __syncthreads();
-    for (int r = t; r < R; r += 256) {
+    off[t] = r0;
+    if (t == 0) off[512] = 0x7fffffff;
+    __syncthreads();
+    const int r = blockIdx.x * 512 + t;
+    if (r < R) {
         int lo = 0, hi = E;  // largest e with off[e] <= r
         while (hi - lo > 1) {
             const int mid = (lo + hi) >> 1;
@@ -287,8 +301,8 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     _Float16* D = reinterpret_cast<_Float16*>(ws + L.off_D);
     if (p.E > 512) return hipErrorInvalidValue;
 
-    hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(256), 0, st, p.expert_count, p.E, p.R, jobs, njobs,
-                       row_expert);
+    hipLaunchKernelGGL(prefill_plan_kernel, dim3((unsigned)((p.R + 511) / 512)), dim3(512), 0, st, p.expert_count,
+                       p.E, p.R, jobs, njobs, row_expert);
     const long gblocks = (long)p.R * (p.hidden / 128);
     hipLaunchKernelGGL(prefill_gather_kernel, dim3((unsigned)((gblocks + 3) / 4)), dim3(256), 0, st, p.x,
                        p.token_sorted, row_expert, p.suh[0], p.suh[1], xg, xu, gblocks, p.hidden);
