@@ -193,3 +193,75 @@ HX_INLINE float staged_value(const MfmaSmem& sm, int half, int r, int c)
 }
 
 }  // namespace hx
+
+namespace hx {
+
+// ---- Hadamard-128 on the matrix cores
+//
+// Y = X . H128 / sqrt(128) for BM rows of a 128-column block staged in LDS as fp16 (row-major,
+// leading dimension MF_LDA2): H128[k][n] = (-1)^popcount(k & n) is exact in fp16 and symmetric, and
+// the products are exact in fp32, so this equals the reference's fp32 butterfly up to the order of
+// the fp32 additions.  The result lands in the GEMM's accumulator layout (wave (wm, wn) holds rows
+// BM/2*wm + 16*mb + 4*(lane/16) + i, columns 64*wn + 16*nb + lane%16).
+constexpr int MF_LDA2 = 128 + 8;  // halves per row of a staged 128-column block
+
+// H128 as a B operand block ([n][k], leading dimension MF_LDA2).
+HX_INLINE void h128_to_lds(_Float16* h)
+{
+    for (int i = threadIdx.x; i < 128 * 64; i += MF_THREADS) {
+        const int n = i >> 6, k = 2 * (i & 63);
+        const uint32_t s0 = __builtin_popcount(n & k) & 1, s1 = __builtin_popcount(n & (k + 1)) & 1;
+        *reinterpret_cast<uint32_t*>(&h[n * MF_LDA2 + k]) = (0x3c00u | (s0 << 15)) | ((0x3c00u | (s1 << 15)) << 16);
+    }
+}
+
+// fp16 of a float accumulator tile into X (row-major, MF_LDA2): X[row][col] = fp16(f(row, col, v)).
+template <int BM, class F>
+HX_INLINE void acc_to_lds_f16(const hx_f4 (&acc)[BM / 32][4], _Float16* x, F f)
+{
+    constexpr int WM = BM / 2, MB = WM / 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = WM * wm + 16 * mb + 4 * (lane >> 4) + r, col = 64 * wn + 16 * nb + (lane & 15);
+                x[row * MF_LDA2 + col] = (_Float16)f(row, col, acc[mb][nb][r]);
+            }
+}
+
+template <int BM>
+HX_INLINE void hadamard_mfma(const _Float16* x, const _Float16* h, hx_f4 (&y)[BM / 32][4])
+{
+    constexpr int WM = BM / 2, MB = WM / 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) y[mb][nb] = hx_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 128; kk += 32) {
+        hx_h8 af[MB], bf[4];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+            af[mb] = *reinterpret_cast<const hx_h8*>(&x[(WM * wm + 16 * mb + (lane & 15)) * MF_LDA2 + kk + 8 * (lane >> 4)]);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+            bf[nb] = *reinterpret_cast<const hx_h8*>(&h[(64 * wn + 16 * nb + (lane & 15)) * MF_LDA2 + kk + 8 * (lane >> 4)]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+                y[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mb], bf[nb], y[mb][nb], 0, 0, 0);
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) y[mb][nb] = y[mb][nb] * HX_RSQRT128;
+}
+
+}  // namespace hx

@@ -178,6 +178,155 @@ __global__ __launch_bounds__(MF_THREADS) void grouped_gemm_kernel(GroupedGemmArg
 #undef HX_GG_CASE
 }
 
+// ------------------------------------------------------------------ fused gate/up + SiLU-gate
+
+struct GuArgs {
+    const Job* jobs;
+    const int* njobs;
+    const _Float16* xg;  // [R][hidden] transformed gate inputs
+    const _Float16* xu;
+    const void* const* tr[2];
+    const void* const* svh[2];
+    const void* const* suh_d;
+    const int32_t* bits_tab[2];
+    int bits_uniform[2];
+    int K, N;            // hidden, inter
+    float act_limit;
+    _Float16* act;       // [R][inter] down-projection inputs
+    _Float16* g_scratch; // [R][inter] fp16 G, then u, of the tiles in flight
+    _Float16* u_scratch;
+};
+
+template <int BITS, int CB, int BM>
+__device__ __forceinline__ void gu_tile(const _Float16* A, int K, int rows, const void* tr, int N, int cg,
+                                        MfmaSmem& sm, hx_f4 (&acc)[BM / 32][4])
+{
+    mfma_tile<BITS, CB, BM>(A, K, rows, static_cast<const uint32_t*>(tr), K, N, cg * 8, sm, acc);
+}
+
+template <int CB, int BM>
+__device__ __forceinline__ void gu_tile_bits(int bits, const _Float16* A, int K, int rows, const void* tr, int N,
+                                             int cg, MfmaSmem& sm, hx_f4 (&acc)[BM / 32][4])
+{
+    switch (bits) {
+        case 1: gu_tile<1, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
+        case 2: gu_tile<2, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
+        case 3: gu_tile<3, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
+        case 4: gu_tile<4, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
+        case 5: gu_tile<5, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
+        case 6: gu_tile<6, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
+        case 7: gu_tile<7, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
+        default: gu_tile<8, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
+    }
+}
+
+// Gate and up tiles of one (job, 128-column block), then the SiLU-gate and the down-projection input
+// transform on the matrix cores (hadamard_inner.cuh:284-413 op order: G, U rounded to fp16, H,
+// fp16, times svh in fp16, fp16 SiLU chain, clamps, times suh_d in fp16, H, fp16).
+template <int CB, int BM>
+__device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg, MfmaSmem& sm)
+{
+    constexpr int WM = BM / 2, MB = WM / 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int e = job.expert;
+    const int bg = a.bits_tab[0] ? a.bits_tab[0][e] : a.bits_uniform[0];
+    const int bu = a.bits_tab[1] ? a.bits_tab[1][e] : a.bits_uniform[1];
+    _Float16* H = sm.ab[0];
+    _Float16* X = sm.ab[0] + 128 * MF_LDA2;
+    auto mapped = [&](int row, float v) -> float {
+        if constexpr (CB == 2) return fmaf(v, CB2_SCALE, CB2_BIAS * sm.rowsum[row]);
+        else return v;
+    };
+
+    hx_f4 acc[MB][4];
+    // The fp16 tiles G and then u wait in global scratch (this workgroup's rows and columns only; they
+    // stay in L2) instead of registers, which would halve the waves per SIMD of the main loops.
+    _Float16* gs = a.g_scratch + (size_t)job.row0 * a.N + cg * 128;
+    _Float16* us = a.u_scratch + (size_t)job.row0 * a.N + cg * 128;
+    auto frag_store = [&](_Float16* dst, auto f) {  // fragment (row, col) -> dst[row][col], rows < job.rows
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = WM * wm + 16 * mb + 4 * (lane >> 4) + r, col = 64 * wn + 16 * nb + (lane & 15);
+                    if (row < job.rows) dst[(size_t)row * a.N + col] = f(row, col, acc[mb][nb][r]);
+                }
+    };
+    // gate: G = fp16(mapped sum)
+    gu_tile_bits<CB, BM>(bg, a.xg + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[0][e], a.N, cg, sm, acc);
+    frag_store(gs, [&](int row, int, float v) { return (_Float16)mapped(row, v); });
+    __syncthreads();  // rowsum is reused by the up tile
+    gu_tile_bits<CB, BM>(bu, a.xu + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[1][e], a.N, cg, sm, acc);
+
+    // u = fp16(H(U)) * svh_u
+    h128_to_lds(H);
+    acc_to_lds_f16<BM>(acc, X, [&](int row, int, float v) { return mapped(row, v); });
+    __syncthreads();
+    hadamard_mfma<BM>(X, H, acc);
+    const _Float16* svg = static_cast<const _Float16*>(a.svh[0][e]) + cg * 128;
+    const _Float16* svu = static_cast<const _Float16*>(a.svh[1][e]) + cg * 128;
+    const _Float16* sud = static_cast<const _Float16*>(a.suh_d[e]) + cg * 128;
+    frag_store(us, [&](int, int col, float v) { return (_Float16)((_Float16)v * svu[col]); });
+    __syncthreads();  // G and u stores done (workgroup scope), X free
+    // g = fp16(H(G)) * svh_g
+    for (int i = threadIdx.x; i < BM * 16; i += MF_THREADS) {
+        const int row = i >> 4, c8 = (i & 15) * 8;
+        hx_u4v v = {0u, 0u, 0u, 0u};
+        if (row < job.rows) v = *reinterpret_cast<const hx_u4v*>(gs + (size_t)row * a.N + c8);
+        *reinterpret_cast<hx_u4v*>(&X[row * MF_LDA2 + c8]) = v;
+    }
+    __syncthreads();
+    hadamard_mfma<BM>(X, H, acc);
+    const float L = a.act_limit;
+    const _Float16 Lh = (_Float16)L, nLh = (_Float16)(-L);
+    __syncthreads();
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+        const int col = 64 * wn + 16 * nb + (lane & 15);
+        const _Float16 sg = svg[col], sd = sud[col];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = WM * wm + 16 * mb + 4 * (lane >> 4) + r;
+                _Float16 g = (_Float16)acc[mb][nb][r] * sg;
+                _Float16 uu = row < job.rows ? us[(size_t)row * a.N + col] : (_Float16)0.0f;
+                g = hx_silu_h(g);
+                if (L != 0.0f) {
+                    uu = uu < nLh ? nLh : (uu > Lh ? Lh : uu);
+                    g = g > Lh ? Lh : g;
+                }
+                X[row * MF_LDA2 + col] = (g * uu) * sd;
+            }
+    }
+    __syncthreads();
+    // act = fp16(H(p)), staged back to LDS for row-wise stores
+    hadamard_mfma<BM>(X, H, acc);
+    __syncthreads();
+    acc_to_lds_f16<BM>(acc, X, [](int, int, float v) { return v; });
+    __syncthreads();
+    _Float16* out = a.act + (size_t)job.row0 * a.N + cg * 128;
+    for (int i = threadIdx.x; i < BM * 16; i += MF_THREADS) {
+        const int row = i >> 4, c8 = (i & 15) * 8;
+        if (row < job.rows)
+            *reinterpret_cast<hx_u4v*>(out + (size_t)row * a.N + c8) = *reinterpret_cast<const hx_u4v*>(&X[row * MF_LDA2 + c8]);
+    }
+}
+
+template <int CB>
+__global__ __launch_bounds__(MF_THREADS) void grouped_gu_kernel(GuArgs a)
+{
+    __shared__ MfmaSmem sm;
+    const int job_i = blockIdx.y;
+    if (job_i >= *a.njobs) return;
+    const Job job = a.jobs[job_i];
+    if (job.bm == 64) gu_fused<CB, 64>(a, job, blockIdx.x, sm);
+    else gu_fused<CB, MF_BM>(a, job, blockIdx.x, sm);
+}
+
 // ------------------------------------------------------------------ guad
 
 __global__ __launch_bounds__(256) void prefill_guad_kernel(const _Float16* G, const _Float16* U, const int* row_expert,
@@ -307,29 +456,29 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     hipLaunchKernelGGL(prefill_gather_kernel, dim3((unsigned)((gblocks + 3) / 4)), dim3(256), 0, st, p.x,
                        p.token_sorted, row_expert, p.suh[0], p.suh[1], xg, xu, gblocks, p.hidden);
 
-    GroupedGemmArgs g{};
-    g.jobs = jobs;
-    g.njobs = njobs;
-    g.A[0] = xg;
-    g.A[1] = xu;
-    g.out[0] = G;
-    g.out[1] = U;
-    g.tr[0] = p.tr[0];
-    g.tr[1] = p.tr[1];
-    g.bits_tab[0] = p.bits_tab[0];
-    g.bits_tab[1] = p.bits_tab[1];
-    g.bits_uniform[0] = p.bits_uniform[0];
-    g.bits_uniform[1] = p.bits_uniform[1];
-    g.K = p.hidden;
-    g.N = p.inter;
-    g.nproj = 2;
-    dim3 grid_gu(2 * (p.inter / 128), L.max_jobs);
-    if (p.cb == 1) hipLaunchKernelGGL(grouped_gemm_kernel<1>, grid_gu, dim3(MF_THREADS), 0, st, g);
-    else hipLaunchKernelGGL(grouped_gemm_kernel<2>, grid_gu, dim3(MF_THREADS), 0, st, g);
-
-    const long ublocks = (long)p.R * (p.inter / 128);
-    hipLaunchKernelGGL(prefill_guad_kernel, dim3((unsigned)((ublocks + 3) / 4)), dim3(256), 0, st, G, U, row_expert,
-                       p.svh[0], p.svh[1], p.suh[2], A, ublocks, p.inter, p.act_limit);
+    GuArgs gu{};
+    gu.jobs = jobs;
+    gu.njobs = njobs;
+    gu.xg = xg;
+    gu.xu = xu;
+    gu.tr[0] = p.tr[0];
+    gu.tr[1] = p.tr[1];
+    gu.svh[0] = p.svh[0];
+    gu.svh[1] = p.svh[1];
+    gu.suh_d = p.suh[2];
+    gu.bits_tab[0] = p.bits_tab[0];
+    gu.bits_tab[1] = p.bits_tab[1];
+    gu.bits_uniform[0] = p.bits_uniform[0];
+    gu.bits_uniform[1] = p.bits_uniform[1];
+    gu.K = p.hidden;
+    gu.N = p.inter;
+    gu.act_limit = p.act_limit;
+    gu.act = A;
+    gu.g_scratch = G;
+    gu.u_scratch = U;
+    dim3 grid_gu(p.inter / 128, L.max_jobs);
+    if (p.cb == 1) hipLaunchKernelGGL(grouped_gu_kernel<1>, grid_gu, dim3(MF_THREADS), 0, st, gu);
+    else hipLaunchKernelGGL(grouped_gu_kernel<2>, grid_gu, dim3(MF_THREADS), 0, st, gu);
 
     GroupedGemmArgs d{};
     d.jobs = jobs;
