@@ -4,8 +4,9 @@
 // Flow (all stream-ordered, no host synchronisation):
 //   plan       expert_count -> per-row expert id and 128-row tile jobs per expert
 //   gather     xg[r] = fp16(H(x[token_sorted[r]] . suh_g[e])), xu[r] likewise  (one wave per 128 block)
-//   gemm g/u   G = xg . W_g[e], U = xu . W_u[e]   (decode-to-LDS + MFMA, fp16 outputs, one launch)
-//   guad       act[r] = fp16(H((silu(g) * u) . suh_d)), g = fp16(H(G)) . svh_g ...  (fp16 chain)
+//   gate/up    G = xg . W_g[e], U = xu . W_u[e] (decode-to-LDS + MFMA), then in the same workgroup
+//              act[r] = fp16(H((silu(g) * u) . suh_d)), g = fp16(H(G)) . svh_g ... (fp16 chain,
+//              transforms on the matrix cores)
 //   gemm d     D = act . W_d[e]                    (fp16 output)
 //   combine    y[t] = fp16(sum_j H(D[r_j]) * w_j / sqrt(128) . svh_d[e_j]  + shared[t])
 // Reference semantics: src/cuda/quant/exl3_moe_kernel.cuh:57-262, hadamard_inner.cuh:284-481,
@@ -325,45 +326,6 @@ __global__ __launch_bounds__(MF_THREADS) void grouped_gu_kernel(GuArgs a)
     const Job job = a.jobs[job_i];
     if (job.bm == 64) gu_fused<CB, 64>(a, job, blockIdx.x, sm);
     else gu_fused<CB, MF_BM>(a, job, blockIdx.x, sm);
-}
-
-// ------------------------------------------------------------------ guad
-
-__global__ __launch_bounds__(256) void prefill_guad_kernel(const _Float16* G, const _Float16* U, const int* row_expert,
-                                                          const void* const* svh_g, const void* const* svh_u,
-                                                          const void* const* suh_d, _Float16* act, long blocks,
-                                                          int inter, float L)
-{
-    const int lane = threadIdx.x & 63;
-    const long b = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (b >= blocks) return;
-    const int per = inter / 128;
-    const long r = b / per;
-    const int c = (int)(b % per) * 128 + 2 * lane;
-    const int e = row_expert[r];
-    const hx_h2 sg = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(svh_g[e]) + c);
-    const hx_h2 su = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(svh_u[e]) + c);
-    const hx_h2 sd = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(suh_d[e]) + c);
-    const hx_h2 Gv = *reinterpret_cast<const hx_h2*>(G + r * inter + c);
-    const hx_h2 Uv = *reinterpret_cast<const hx_h2*>(U + r * inter + c);
-    float g0 = (float)Gv.x, g1 = (float)Gv.y, u0 = (float)Uv.x, u1 = (float)Uv.y;
-    hx_had128_wave(g0, g1);
-    hx_had128_wave(u0, u1);
-    hx_h2 g = hx_h2{(_Float16)g0, (_Float16)g1} * sg;
-    hx_h2 u = hx_h2{(_Float16)u0, (_Float16)u1} * su;
-    g.x = hx_silu_h(g.x);
-    g.y = hx_silu_h(g.y);
-    if (L != 0.0f) {
-        const _Float16 Lh = (_Float16)L, nLh = (_Float16)(-L);
-        u.x = u.x < nLh ? nLh : (u.x > Lh ? Lh : u.x);
-        u.y = u.y < nLh ? nLh : (u.y > Lh ? Lh : u.y);
-        g.x = g.x > Lh ? Lh : g.x;
-        g.y = g.y > Lh ? Lh : g.y;
-    }
-    hx_h2 p = (g * u) * sd;
-    float p0 = (float)p.x, p1 = (float)p.y;
-    hx_had128_wave(p0, p1);
-    *reinterpret_cast<hx_h2*>(act + r * inter + c) = hx_h2{(_Float16)p0, (_Float16)p1};
 }
 
 // ------------------------------------------------------------------ combine

@@ -3,7 +3,7 @@
   python -m helios_glm53flash_amd.profiling stats <kernel-trace.db>
       per-kernel dispatch count and average / min / max duration (us)
   python -m helios_glm53flash_amd.profiling traffic <fetch.db> <write.db> [--cmd "..."]
-      HBM bytes per launch of the MoE decode kernels from FETCH_SIZE and WRITE_SIZE passes, each
+      HBM bytes per launch of the MoE decode layer kernel from FETCH_SIZE and WRITE_SIZE passes, each
       scaled by what the same counter reads for the calibration copy (256 MiB read + 256 MiB write)
       of bench.py --profile-only
 """
@@ -57,7 +57,7 @@ def traffic(fetch_db: str, write_db: str, cmd: str = "") -> dict:
     out = {"command": cmd, "copy_calibration": {"bytes": COPY_BYTES, "FETCH_SIZE_KiB": copy_f,
                                                 "WRITE_SIZE_KiB": copy_w, "read_scale": kf, "write_scale": kw},
            "kernels": {}}
-    for phase, key in (("experts_gate_up", "moe_decode_gu_kernel"), ("experts_down", "moe_decode_d_kernel")):
+    for phase, key in (("moe_decode", "moe_decode_kernel"),):
         fk, wk = _pick(f, key), _pick(w, key)
         out["kernels"][phase] = {"FETCH_SIZE_KiB": fk, "WRITE_SIZE_KiB": wk,
                                  "read_bytes": fk * 1024 * kf, "write_bytes": wk * 1024 * kw,
