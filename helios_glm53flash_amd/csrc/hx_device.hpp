@@ -44,6 +44,10 @@ static __device__ uint64_t hx_dbg_ts[4096][32];
 
 static constexpr float HX_RSQRT128 = 0.088388347648f;
 
+// Workgroup size in threads / waves (kernels here run 256 or 1024 threads).
+HX_INLINE int hx_nthreads() { return (int)blockDim.x; }
+HX_INLINE int hx_nwaves() { return (int)blockDim.x >> 6; }
+
 HX_INLINE hx_h2 u32_as_h2(uint32_t u) { return __builtin_bit_cast(hx_h2, u); }
 HX_INLINE uint32_t h2_as_u32(hx_h2 h) { return __builtin_bit_cast(uint32_t, h); }
 HX_INLINE _Float16 u16_as_h(uint16_t u) { return __builtin_bit_cast(_Float16, u); }

@@ -306,7 +306,7 @@ HX_INLINE void input_issue(InputRegs& r, const _Float16* x, const int* rows, con
     const int blocks = kc >> 7;
 #pragma unroll
     for (int i = 0; i < IN_PRE; ++i) {
-        const int job = wave + GEMV_WAVES * i;
+        const int job = wave + hx_nwaves() * i;
         r.xv[i] = 0;
         r.sv[i] = 0;
         if (job < M * blocks) {
@@ -335,13 +335,13 @@ HX_INLINE void input_finish(uint32_t* a_lds, const InputRegs& r, const _Float16*
     const int blocks = kc >> 7;
 #pragma unroll
     for (int i = 0; i < IN_PRE; ++i) {
-        const int job = wave + GEMV_WAVES * i;
+        const int job = wave + hx_nwaves() * i;
         if (job < M * blocks) {
             const int m = job / blocks, b = job % blocks;
             a_lds[(m * kc + b * 128) / 2 + lane] = input_transform(r.xv[i], r.sv[i], pre_transformed);
         }
     }
-    for (int job = wave + GEMV_WAVES * IN_PRE; job < M * blocks; job += GEMV_WAVES) {
+    for (int job = wave + hx_nwaves() * IN_PRE; job < M * blocks; job += hx_nwaves()) {
         const int m = job / blocks, b = job % blocks;
         const uint32_t xv = input_word(x, rows, M, K, k0, blocks, job, lane, pre_transformed);
         const uint32_t sv =
@@ -367,27 +367,49 @@ struct GemvArgs {
     bool pre_transformed;
 };
 
+// LDS scratch of gemv_range: one array per (N, KS), shared by every instantiation of a kernel (a
+// __shared__ array inside gemv_range would be allocated once per bit width in mixed-width kernels).
+template <int N, int KS>
+__device__ __forceinline__ float* gemv_lds()
+{
+    __shared__ float buf[N * KS];
+    return buf;
+}
+
 // This workgroup's partial sum of the GEMV over k in [k0, k0 + kc) (kc a multiple of 128): on
 // return colsum[m][c] (LDS fp32, MT x 128) holds sum over that range of a[m][k] * W[k][cg*128 + c].
 // a_lds must hold MT * kc fp16.  MT <= 16.
 //
+// KS = 1: 4 waves, wave w owns tile columns 2w, 2w+1 over the whole range.  KS = 4: 16 waves, wave w
+// owns tile columns 2(w%4), 2(w%4)+1 over the 128-k blocks j = w/4, w/4 + 4, ... of the range, and
+// the four partial sums of a column pair are added in block-subset order through LDS.
+//
 // before_input() runs after the tile prefetch is issued and before a pre-transformed input is read
 // (a consumer waits there for its producer); after_input() runs once the input is in LDS.
-template <int BITS, int CB, int MT, class Before = NoHook, class After = NoHook>
+template <int BITS, int CB, int MT, int KS = 1, class Before = NoHook, class After = NoHook>
 __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, int kc, uint32_t* a_lds, float* colsum,
                                            Before before_input = Before(), After after_input = After())
 {
     static_assert(MT <= 16, "one MFMA holds 16 rows");
+    static_assert(KS == 1 || KS == 2 || KS == 4, "k subsets");
     constexpr bool AFFINE = CB == 2;
-    __shared__ float asum[MT];  // sum of the transformed input over the range, per row (affine cb2)
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* asum = gemv_lds<MT, 1>();  // sum of the transformed input over the range, per row (cb2)
+    float* kpart = gemv_lds<MT * 128, KS>();
+    // wave index as a uniform (scalar) value: the step offsets below stay in SGPRs
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int pair = KS == 1 ? wave : (wave & 3);  // tile-column pair of this wave
+    const int ks = KS == 1 ? 0 : (wave >> 2);      // block subset of this wave
     const int gq = lane >> 4;             // tile row within the 4-row step (MFMA k-group)
     const int t = (lane >> 3) & 1;        // tile column of the wave's pair
     const int q = lane & 7;               // quarter
     const int tiles_n = g.N >> 4;
     constexpr int NW = 8 * BITS;
     const uint32_t* tw = reinterpret_cast<const uint32_t*>(g.trellis);
-    const int tn = cg * 8 + 2 * wave + t;
+    const int tn = cg * 8 + 2 * pair + t;
+    const int nblk = kc >> 7;
+    // this wave's steps: step s covers k = k0 + 128 * (ks + KS * (s / 2)) + 64 * (s % 2)
+    const int steps = KS == 1 ? (kc >> 6) : 2 * max(0, (nblk - ks + KS - 1) / KS);
+    auto step_k = [&](int st) { return 128 * (ks + KS * (st >> 1)) + 64 * (st & 1); };  // relative to k0
 
     // software pipeline: PF steps of tile words in flight.  The first PF are issued before the input
     // transform (after the input loads themselves) so their HBM latency overlaps it; every step then
@@ -395,13 +417,12 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     // last tile row, so the number of loads in flight is the same at every step and each wait is a
     // static count).
     constexpr int PF = BITS <= 4 ? 8 : 4;
-    const int steps = kc >> 6;
     uint32_t buf[PF][BITS + 1];
     // byte offsets: lane part (tile row gq of the step, tile column tn, quarter q) and step part
-    // (tile rows k0/16 + 4*st); the tensor is (K/16) x (N/16) tiles
+    // (tile rows (k0 + step_k) / 16); the tensor is (K/16) x (N/16) tiles
     // the base is uniform: state it, or every buffer load gets a loop over the lanes' descriptors
-    const uint64_t twu = reinterpret_cast<uint64_t>(tw);
     // (readfirstlane returns int: each half goes through uint32_t so the low half is not sign-extended)
+    const uint64_t twu = reinterpret_cast<uint64_t>(tw);
     const uint64_t twb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(twu >> 32)) << 32) |
                          (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)twu);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -410,11 +431,13 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     const int lane_off = ((gq * tiles_n + tn) * NW) * 4;
     const int voff0 = lane_off + ((q * BITS + NW - 1) % NW) * 4, voff1 = lane_off + q * BITS * 4;
     const int row_bytes = tiles_n * NW * 4;
-    const int soff0 = (k0 >> 4) * row_bytes, step_bytes = 4 * row_bytes;
+    auto soff = [&](int st) { return ((k0 + step_k(min(st, steps - 1))) >> 4) * row_bytes; };
     InputRegs in;
     if (!g.pre_transformed) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, false);
+    if (steps > 0) {
 #pragma unroll
-    for (int j = 0; j < PF; ++j) load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff0 + min(j, steps - 1) * step_bytes);
+        for (int j = 0; j < PF; ++j) load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff(j));
+    }
 
     before_input();
     if (g.pre_transformed) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, true);
@@ -423,7 +446,7 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     after_input();
     HX_TS(2);
     if constexpr (AFFINE) {
-        for (int m = wave; m < g.M && m < MT; m += GEMV_WAVES) {
+        for (int m = wave; m < g.M && m < MT; m += hx_nwaves()) {
             const _Float16* row = reinterpret_cast<const _Float16*>(a_lds) + (size_t)m * kc;
             float v = 0.0f;
             for (int k = lane; k < kc; k += 64) v += (float)row[k];
@@ -451,9 +474,9 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
             uint32_t d[16];
             if constexpr (AFFINE) quarter_affine<BITS>(buf[j], d);
             else quarter_decode<BITS, CB>(buf[j], d);
-            load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff0 + min(st + PF, steps - 1) * step_bytes);
+            load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff(st + PF));
             if (st < steps) {
-                const int kl = 64 * st + 16 * gq;
+                const int kl = step_k(st) + 16 * gq;
                 const hx_h8 a0 = *reinterpret_cast<const hx_h8*>(arow + kl);
                 const hx_h8 a1 = *reinterpret_cast<const hx_h8*>(arow + kl + 8);
                 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, quarter_operand<0, 0>(d), acc0, 0, 0, 0);
@@ -465,22 +488,43 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     }
 
     HX_SETPRIO(3);  // the split-K handoff and epilogues are on the critical path
-    if constexpr (AFFINE) hx_lds_barrier();  // asum of every row is in LDS
-
     // C: lane holds rows 4*(lane/16) + i of column label lane%16 = 8t + q; label -> column
-    // 16*(2*wave + t) + 8*nh + q of the group
+    // 16*(2*pair + t) + 8*nh + q of the group
+    if constexpr (KS > 1) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = 4 * gq + i;
-        if (m < MT && m < g.M) {
-            float c0 = acc0[i], c1 = acc1[i];
-            if constexpr (AFFINE) {
-                const float b = CB2_BIAS * asum[m];
-                c0 = fmaf(c0, CB2_SCALE, b);
-                c1 = fmaf(c1, CB2_SCALE, b);
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * gq + i;
+            if (m < MT && m < g.M) {
+                kpart[(ks * MT + m) * 128 + 16 * (2 * pair + t) + q] = acc0[i];
+                kpart[(ks * MT + m) * 128 + 16 * (2 * pair + t) + 8 + q] = acc1[i];
             }
-            colsum[m * 128 + 16 * (2 * wave + t) + q] = c0;
-            colsum[m * 128 + 16 * (2 * wave + t) + 8 + q] = c1;
+        }
+        hx_lds_barrier();
+        for (int i = threadIdx.x; i < MT * 128; i += hx_nthreads()) {
+            const int m = i >> 7;
+            if (m < g.M) {
+                float v = kpart[i];
+#pragma unroll
+                for (int sub = 1; sub < KS; ++sub) v += kpart[sub * MT * 128 + i];
+                if constexpr (AFFINE) v = fmaf(v, CB2_SCALE, CB2_BIAS * asum[m]);
+                colsum[i] = v;
+            }
+        }
+    } else {
+        if constexpr (AFFINE) hx_lds_barrier();  // asum of every row is in LDS
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * gq + i;
+            if (m < MT && m < g.M) {
+                float c0 = acc0[i], c1 = acc1[i];
+                if constexpr (AFFINE) {
+                    const float b = CB2_BIAS * asum[m];
+                    c0 = fmaf(c0, CB2_SCALE, b);
+                    c1 = fmaf(c1, CB2_SCALE, b);
+                }
+                colsum[m * 128 + 16 * (2 * pair + t) + q] = c0;
+                colsum[m * 128 + 16 * (2 * pair + t) + 8 + q] = c1;
+            }
         }
     }
     __syncthreads();
@@ -506,7 +550,7 @@ __device__ __forceinline__ void gemv_split_sum(const GemvArgs& g, int cg, int s,
 template <int MT>
 HX_INLINE void publish_partial(float* partial, int M, int N, int cg, int s, const float* colsum)
 {
-    for (int i = threadIdx.x; i < MT * 128; i += GEMV_THREADS) {
+    for (int i = threadIdx.x; i < MT * 128; i += hx_nthreads()) {
         const int m = i >> 7, c = i & 127;
         if (m < M)
             __hip_atomic_store(&partial[((size_t)s * M + m) * N + cg * 128 + c], colsum[i], __ATOMIC_RELAXED,
@@ -536,7 +580,7 @@ HX_INLINE void gather_partials(const float* partial, int M, int N, int splits, i
 {
     // the loads of 8 splits are issued together, then added in split order
     constexpr int B = 8;
-    for (int i = threadIdx.x; i < MT * 128; i += GEMV_THREADS) {
+    for (int i = threadIdx.x; i < MT * 128; i += hx_nthreads()) {
         const int m = i >> 7, c = i & 127;
         float v = 0.0f;
         if (m < M) {

@@ -18,7 +18,7 @@ __device__ void linear_epilogue(const float* colsum, const _Float16* svh, void* 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = cg * 128 + 2 * lane;
     hx_h2 sv = *reinterpret_cast<const hx_h2*>(svh + c);
-    for (int m = wave; m < M && m < MT; m += GEMV_WAVES) {
+    for (int m = wave; m < M && m < MT; m += hx_nwaves()) {
         float v0 = colsum[m * 128 + 2 * lane], v1 = colsum[m * 128 + 2 * lane + 1];
         hx_had128_wave(v0, v1);
         if (y_fp32) {

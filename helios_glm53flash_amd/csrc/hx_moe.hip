@@ -16,9 +16,9 @@ hipError_t launch_moe_decode_m1(const MoeDecodeArgs& a, int cb, int bits, hipStr
 hipError_t launch_moe_decode_m4(const MoeDecodeArgs& a, int cb, int bits, hipStream_t st);
 hipError_t launch_moe_decode_m8(const MoeDecodeArgs& a, int cb, int bits, hipStream_t st);
 
-// Workgroups of `kernel` (256 threads, `lds` dynamic LDS bytes) that fit on the current device at
+// Workgroups of `kernel` (`threads` threads, `lds` dynamic LDS bytes) that fit on the current device at
 // once: CU count times blocks per CU, cached per (device, kernel, lds).
-int resident_blocks(const void* kernel, size_t lds)
+int resident_blocks(const void* kernel, int threads, size_t lds)
 {
     struct Key {
         int dev;
@@ -35,7 +35,7 @@ int resident_blocks(const void* kernel, size_t lds)
         if (c.dev == dev && c.k == kernel && c.lds == lds) return c.n;
     int cus = 0, per = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, GEMV_THREADS, lds) != hipSuccess || per <= 0)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, lds) != hipSuccess || per <= 0)
         per = 1;
     cache.push_back({dev, kernel, lds, cus * per});
     return cus * per;

@@ -216,7 +216,7 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int R = a.T * a.topk;
     if (a.scores) {
-        for (int t = wave; t < a.T; t += GEMV_WAVES) {
+        for (int t = wave; t < a.T; t += hx_nwaves()) {
             int e;
             float w;
             wave_topk(a.scores + (size_t)t * a.E, a.bias, a.E, a.topk, a.routed_scale, e, w);
@@ -366,7 +366,7 @@ __device__ __forceinline__ void guad_epilogue(const MoeDecodeArgs& a, const Slot
     const hx_h2 su = *reinterpret_cast<const hx_h2*>(svu + c);
     const hx_h2 sd = *reinterpret_cast<const hx_h2*>(sud + c);
     const float L = a.act_limit;
-    for (int m = wave; m < si.count && m < MT; m += GEMV_WAVES) {
+    for (int m = wave; m < si.count && m < MT; m += hx_nwaves()) {
         hx_h2 p;
         if (!shared) {
             // G, U as fp16 (the reference GEMM writes fp16), transform, fp16, times svh (fp16)
@@ -421,7 +421,7 @@ __device__ __forceinline__ void down_epilogue(const MoeDecodeArgs& a, const Deco
     const _Float16* svd = static_cast<const _Float16*>(shared ? a.sh_svh[2] : a.svh[2][si.expert]);
     const hx_h2 sd = *reinterpret_cast<const hx_h2*>(svd + c);
     const int R = a.T * a.topk;
-    for (int m = wave; m < si.count && m < MT; m += GEMV_WAVES) {
+    for (int m = wave; m < si.count && m < MT; m += hx_nwaves()) {
         float d0, d1, wgt;
         size_t row;
         if (!shared) {
@@ -449,7 +449,7 @@ __device__ __forceinline__ void down_epilogue(const MoeDecodeArgs& a, const Deco
 __device__ __forceinline__ void combine_columns(const MoeDecodeArgs& a, const DecodePlan& p, int cg, bool has_shared)
 {
     const int R = a.T * a.topk;
-    for (int i = threadIdx.x; i < a.T * 128; i += GEMV_THREADS) {
+    for (int i = threadIdx.x; i < a.T * 128; i += hx_nthreads()) {
         const int t = i >> 7;
         const int c = cg * 128 + (i & 127);
         // the loads of 8 contributions (and the shared row) are issued together, then added in
@@ -488,6 +488,17 @@ __device__ __forceinline__ void combine_columns(const MoeDecodeArgs& a, const De
 // finishes its gate/up share requests the tile words of its down share first and only then waits
 // for the activations it needs (per slot and 128-column block), so the down projection's HBM
 // latency overlaps the end of the gate/up phase.
+
+// Workgroup shape: 4 * DEC_KS waves.  With DEC_KS > 1 the DEC_KS wave groups split each
+// segment's 128-k blocks (block j of the segment goes to group j % DEC_KS) and add their sums in
+// group order through LDS.  Measured on MI355X (config-3 layer, 1 token): 4 waves x 4 workgroups
+// per CU 73 us, 8 x 2 76 us, 16 x 1 83 us -- fewer, larger workgroups wait longer at their
+// barriers than they save in segment handoffs.
+#ifndef HX_DEC_KS
+#define HX_DEC_KS 1
+#endif
+constexpr int DEC_KS = HX_DEC_KS;
+constexpr int DEC_THREADS = 256 * DEC_KS;
 
 // Bounded wait of thread 0 for *flag >= target (the producers are resident workgroups that do not
 // wait for anything themselves, so the wait ends; the bound only turns a bug into a flagged wrong
@@ -566,7 +577,7 @@ __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodeP
     g.K = a.hidden;
     g.N = a.inter;
     g.pre_transformed = false;
-    gemv_range<BITS, CB, MT>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
+    gemv_range<BITS, CB, MT, DEC_KS>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
 
     // partial of segment i of (slot, proj, cg): partial_{g,u}[((slot*gg + cg) * (KB + 1) + i) * 8 + m][128]
     float* pbase = (proj == 0 ? a.partial_g : a.partial_u) + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
@@ -610,7 +621,7 @@ __device__ __forceinline__ void d_segment(const MoeDecodeArgs& a, const DecodePl
             for (int kb = kb0; kb < kb1; ++kb) wait_flag(&a.ready[slot * gg + kb], 1, a.status);
         hx_lds_barrier();
     };
-    gemv_range<BITS, CB, MT>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs, wait_inputs);
+    gemv_range<BITS, CB, MT, DEC_KS>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs, wait_inputs);
 
     const int count = sp.count(c, KB);
     float* pbase = a.partial_d + (size_t)(slot * gd + cg) * (KB + 1) * 8 * 128;
@@ -702,7 +713,7 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
     HX_TS_BASE(8);
     if (blockIdx.x == 0 && a.out_idx) {
         const int R = a.T * a.topk;
-        for (int i = threadIdx.x; i < R; i += GEMV_THREADS) {
+        for (int i = threadIdx.x; i < R; i += hx_nthreads()) {
             const int pos = plan.r2s[i];
             int e = 0;
             for (int qq = 0; qq < plan.n; ++qq)
@@ -733,7 +744,7 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
         last = __hip_atomic_fetch_add(a.exit_count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
     __syncthreads();
     if (last) {
-        for (int i = threadIdx.x; i < (a.routed_slots + 1) * gg; i += GEMV_THREADS)
+        for (int i = threadIdx.x; i < (a.routed_slots + 1) * gg; i += hx_nthreads())
             __hip_atomic_store(&a.ready[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (threadIdx.x == 0) {
             __hip_atomic_store(a.queue_gu, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -743,16 +754,16 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
     }
 }
 
-// Fixed bit width: at most 128 VGPRs so that four workgroups share a CU.
+// Fixed bit width: at most 128 VGPRs so that 16 waves (4 / DEC_KS workgroups) share a CU.
 template <int BITS, int CB, int MT>
-__global__ __launch_bounds__(GEMV_THREADS, 4) void moe_decode_kernel(MoeDecodeArgs a)
+__global__ __launch_bounds__(DEC_THREADS, 4 / DEC_KS) void moe_decode_kernel(MoeDecodeArgs a)
 {
     moe_decode_body<BITS, CB, MT>(a);
 }
 
 // Mixed bit widths (per-segment dispatch); the larger code keeps the default register budget.
 template <int CB, int MT>
-__global__ __launch_bounds__(GEMV_THREADS) void moe_decode_mixed_kernel(MoeDecodeArgs a)
+__global__ __launch_bounds__(DEC_THREADS) void moe_decode_mixed_kernel(MoeDecodeArgs a)
 {
     moe_decode_body<0, CB, MT>(a);
 }

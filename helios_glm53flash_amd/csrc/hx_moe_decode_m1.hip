@@ -26,7 +26,7 @@ static hipError_t launch_k(Kernel kernel, const MoeDecodeArgs& a, hipStream_t st
     size_t lds = (size_t)1 * 128 * sizeof(_Float16);
     int grid = 1;
     for (int it = 0; it < 3; ++it) {
-        grid = resident_blocks(reinterpret_cast<const void*>(kernel), lds);
+        grid = resident_blocks(reinterpret_cast<const void*>(kernel), DEC_THREADS, lds);
         if (grid < 1) grid = 1;
         if (const char* v = getenv("HX_MOE_WG_PER_CU")) {  // tuning: fewer workgroups per CU
             int cus = 0;
@@ -40,7 +40,7 @@ static hipError_t launch_k(Kernel kernel, const MoeDecodeArgs& a, hipStream_t st
         if (need <= lds) break;
         lds = need;
     }
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(GEMV_THREADS), lds, st, a);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(DEC_THREADS), lds, st, a);
     return hipGetLastError();
 }
 
