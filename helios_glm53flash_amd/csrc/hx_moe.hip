@@ -7,39 +7,13 @@
 
 #include <stdlib.h>
 
-#include <mutex>
-#include <vector>
+
 
 namespace hx {
 
 hipError_t launch_moe_decode_m1(const MoeDecodeArgs& a, int cb, int bits, hipStream_t st);
 hipError_t launch_moe_decode_m4(const MoeDecodeArgs& a, int cb, int bits, hipStream_t st);
 hipError_t launch_moe_decode_m8(const MoeDecodeArgs& a, int cb, int bits, hipStream_t st);
-
-// Workgroups of `kernel` (`threads` threads, `lds` dynamic LDS bytes) that fit on the current device at
-// once: CU count times blocks per CU, cached per (device, kernel, lds).
-int resident_blocks(const void* kernel, int threads, size_t lds)
-{
-    struct Key {
-        int dev;
-        const void* k;
-        size_t lds;
-        int n;
-    };
-    static std::mutex mu;
-    static std::vector<Key> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 256;
-    std::lock_guard<std::mutex> lock(mu);
-    for (const Key& c : cache)
-        if (c.dev == dev && c.k == kernel && c.lds == lds) return c.n;
-    int cus = 0, per = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, lds) != hipSuccess || per <= 0)
-        per = 1;
-    cache.push_back({dev, kernel, lds, cus * per});
-    return cus * per;
-}
 
 static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -93,8 +67,6 @@ MoeDecodeArgs MoeWs::decode_args(char* base) const
     a.counter_d = ctr + 4096;
     a.counter_y = ctr + 8192;
     a.exit_count = ctr + 10240;
-    a.queue_gu = ctr + 10241;
-    a.queue_d = ctr + 10242;
     a.ready = ctr + 10304;
     a.status = reinterpret_cast<int*>(base + off_plan);
     a.contrib = reinterpret_cast<float*>(base + off_contrib);
@@ -105,11 +77,29 @@ MoeDecodeArgs MoeWs::decode_args(char* base) const
     return a;
 }
 
+// Units of the decode layer: gate/up per (slot, projection, column group, k-split of kc_gu), down
+// per (slot, column group, k-split of kc_d), kc = the largest multiple-of-128 divisor of K up to
+// 1024 (HX_MOE_KC overrides the cap, for tuning), so that every unit is one segment of one column
+// group: 1152 + 576 workgroups for 9 slots at hidden 4096, intermediate 2048, i.e. a little under
+// two rounds of resident workgroups (1024 on MI355X).  Measured (config-3 layer): cap 512 81 us,
+// 1024 62-64 us, 2048 65 us, 4096 72 us; unaligned units sized to whole rounds of resident
+// workgroups 61-68 us.  Returns the longest unit's k extent.
+int decode_units(MoeDecodeArgs& a)
+{
+    int cap = 1024;
+    if (const char* v = getenv("HX_MOE_KC")) cap = atoi(v) > 0 ? atoi(v) : cap;
+    const int kg = gemv_kc_for(a.hidden, cap), kd = gemv_kc_for(a.inter, cap);
+    const int slots = a.routed_slots + 1;
+    a.units_gu = slots * 2 * (a.inter / 128) * (a.hidden / kg);
+    a.units_d = slots * (a.hidden / 128) * (a.inter / kd);
+    return kg > kd ? kg : kd;
+}
+
 hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t bits_mask, hipStream_t st)
 {
     if (a.T > 8 || a.T * a.topk > DEC_MAX_R) return hipErrorInvalidValue;
     // counter area (ints): counter_gu [0, 4096), counter_d [4096, 8192), counter_y [8192, 10240),
-    // exit 10240, queue_gu 10241, queue_d 10242, prefill permutation arrival 10250, ready [10304, 16384)
+    // exit 10240, prefill permutation arrival 10250, ready [10304, 16384)
     const int slots = a.routed_slots + 1;
     if (slots * (a.inter / 128) > 4096 || slots * (a.hidden / 128) > 4096 || a.hidden / 128 > 2048 ||
         slots * (a.inter / 128) > 6080)
@@ -120,6 +110,5 @@ hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t bits_mask, hipStrea
     if (a.T <= 4) return launch_moe_decode_m4(a, cb, bits, st);
     return launch_moe_decode_m8(a, cb, bits, st);
 }
-
 
 }  // namespace hx

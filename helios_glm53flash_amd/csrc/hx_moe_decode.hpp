@@ -66,8 +66,7 @@ struct MoeDecodeArgs {
     float* partial_d;              // [slots][hidden/128][inter/128 + 1 segments][8][128]
     _Float16* act;                 // [slots][8][inter]  (down-projection input, already transformed)
     int* exit_count;               // workgroups that finished (zero between calls)
-    int* queue_gu;                 // next dynamic chunk of the gate/up and down phases
-    int* queue_d;
+    int units_gu, units_d;         // workgroups of the gate/up and down phases (grid = their sum)
     int* ready;                    // [slots][inter/128] 1 once the guad epilogue stored that block
     int* status;                   // set to 1 when a bounded wait gave up (never expected)
     // outputs
@@ -479,15 +478,21 @@ __device__ __forceinline__ void combine_columns(const MoeDecodeArgs& a, const De
 
 // ------------------------------------------------------------------ the layer kernel
 //
-// One launch per layer call, every workgroup resident at once (the grid never exceeds what fits).
-// Work is split in 128-k blocks, balanced exactly: the gate/up blocks of all active slots
-// (ordered slot, projection, column group, k) are cut into gridDim.x equal contiguous shares, then
-// the down blocks likewise.  A share covers at most a few (slot, projection, column group) segments;
-// each segment's partial sum goes to its own workspace slot and the last of the segments of a column
-// group adds them in segment order (deterministic), then runs the epilogue.  A workgroup that
-// finishes its gate/up share requests the tile words of its down share first and only then waits
-// for the activations it needs (per slot and 128-column block), so the down projection's HBM
-// latency overlaps the end of the gate/up phase.
+// One launch per layer call.  Work is cut in 128-k blocks: the gate/up blocks of every possible
+// slot (ordered slot, projection, column group, k) in units_gu equal contiguous units, then the
+// down blocks (slot, column group, k) in units_d units; workgroup w < units_gu runs gate/up unit w,
+// the others down unit w - units_gu.  The grid is larger than what fits at once, and the hardware
+// dispatches workgroups in increasing index order as earlier ones finish, so faster CUs take more
+// units (no work queue, no atomics).  Every gate/up workgroup has a lower index than every down
+// workgroup and never waits; the dispatcher of each XCD takes its own workgroups in index order,
+// so it dispatches a down workgroup only after all of its gate/up workgroups, which then hold no
+// slot that a producer would need: every producer a down workgroup waits for gets dispatched and
+// finishes, and the waits end.  A unit's partial sum
+// goes to its own workspace slot; the last of the units of a column group adds them in unit order
+// (deterministic) and runs the epilogue.  A down workgroup requests its tile words first and only
+// then waits for the activations it needs (per slot and 128-column block), so the down
+// projection's HBM latency overlaps the end of the gate/up phase.  Units of slots beyond the
+// active ones (fewer distinct experts than routed rows) return at once.
 
 // Workgroup shape: 4 * DEC_KS waves.  With DEC_KS > 1 the DEC_KS wave groups split each
 // segment's 128-k blocks (block j of the segment goes to group j % DEC_KS) and add their sums in
@@ -508,52 +513,25 @@ HX_INLINE void wait_flag(const int* flag, int target, int* status)
     int spins = 0;
     while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
         __builtin_amdgcn_s_sleep(8);
-        if (++spins > (1 << 22)) {
+        if ((++spins & 1023) == 0 && __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+            break;  // another wait already gave up: do not add its bound to every later wait
+        if (spins > (1 << 22)) {
             __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
     }
 }
 
-// Work split of n blocks: the first ns are cut into g equal contiguous static shares (share w is
-// [sstart(w), sstart(w+1))), the rest into chunks of `chunk` blocks that finished workgroups take
-// from a counter, so that workgroups that run slower (later dispatch, a busier XCD) take fewer.  A
-// column group c (blocks [c*kb, c*kb + kb)) is covered by static segments, then chunk segments;
-// segment indices count in k order, so the partial sums are always added in the same order.
+// Split of n blocks into g equal contiguous units (unit w is [sstart(w), sstart(w+1))); column
+// group c covers blocks [c*kb, c*kb + kb), its segments are numbered in k order.
 struct Split {
-    long n, ns;
-    int g, chunk;
-    HX_INLINE long sstart(int w) const { return (long)w * ns / g; }
-    HX_INLINE int sowner(long x) const { return (int)(((x + 1) * g - 1) / ns); }
-    HX_INLINE long nchunks() const { return (n - ns + chunk - 1) / chunk; }
-    HX_INLINE int count(long c, int kb) const
-    {
-        const long lo = c * kb, hi = lo + kb;
-        int cnt = 0;
-        if (lo < ns) cnt += sowner(min(hi, ns) - 1) - sowner(lo) + 1;
-        if (hi > ns) cnt += (int)((hi - 1 - ns) / chunk - (max(lo, ns) - ns) / chunk + 1);
-        return cnt;
-    }
-    HX_INLINE int index(long c, int kb, long b) const  // b: first block of the segment
-    {
-        const long lo = c * kb;
-        if (b < ns) return sowner(b) - sowner(lo);
-        const int cs = lo < ns ? sowner(min(lo + kb, ns) - 1) - sowner(lo) + 1 : 0;
-        return cs + (int)((b - ns) / chunk - (max(lo, ns) - ns) / chunk);
-    }
+    long n;
+    int g;
+    HX_INLINE long sstart(int w) const { return (long)w * n / g; }
+    HX_INLINE int sowner(long x) const { return (int)(((x + 1) * g - 1) / n); }
+    HX_INLINE int count(long c, int kb) const { return sowner(c * kb + kb - 1) - sowner(c * kb) + 1; }
+    HX_INLINE int index(long c, int kb, long b) const { return sowner(b) - sowner(c * kb); }  // b: first block
 };
-
-// Three quarters static, the rest in chunks of 2 blocks; every static share holds at least one
-// block.
-HX_INLINE Split make_split(long n, int G)
-{
-    Split sp;
-    sp.n = n;
-    sp.g = (int)min((long)G, n);
-    sp.ns = n;  // all static (a dynamic tail costs a ramp per chunk, more than it balances)
-    sp.chunk = 2;
-    return sp;
-}
 
 template <int BITS, int CB, int MT>
 __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, long c,
@@ -645,14 +623,15 @@ HX_INLINE int slot_bits(const MoeDecodeArgs& a, const DecodePlan& p, int slot, i
 // Runs the blocks [b, e) of a phase as segments of single column groups.
 template <int BITS, int CB, int MT>
 __device__ __forceinline__ void run_blocks(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, int KB,
-                                           bool gu, long b, long e, uint32_t* a_lds, float* cs_g, float* cs_u,
-                                           int* rows)
+                                           bool gu, int nact, long b, long e, uint32_t* a_lds, float* cs_g,
+                                           float* cs_u, int* rows)
 {
     const int gg = a.inter >> 7, gd = a.hidden >> 7;
     while (b < e) {
         const long c = b / KB;
         const int kb0 = (int)(b % KB);
         const int kb1 = (int)min((long)KB, kb0 + (e - b));
+        if ((gu ? c / (2 * gg) : c / gd) >= nact) return;  // slots in order: the rest is inactive too
         int bits = BITS;
         if constexpr (BITS == 0) {
             const int aslot = (int)(gu ? c / (2 * gg) : c / gd);
@@ -672,27 +651,6 @@ __device__ __forceinline__ void run_blocks(const MoeDecodeArgs& a, const DecodeP
             default: break;
         }
         b += kb1 - kb0;
-    }
-}
-
-// One phase: the static share, then chunks from the phase's counter until none is left.
-template <int BITS, int CB, int MT>
-__device__ __forceinline__ void run_phase(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, int KB,
-                                          bool gu, int* queue, uint32_t* a_lds, float* cs_g, float* cs_u, int* rows)
-{
-    __shared__ int chunk_id;
-    const int w = blockIdx.x;
-    if (w < sp.g) run_blocks<BITS, CB, MT>(a, plan, sp, KB, gu, sp.sstart(w), sp.sstart(w + 1), a_lds, cs_g, cs_u, rows);
-    const long nch = sp.nchunks();
-    for (;;) {
-        __syncthreads();
-        if (threadIdx.x == 0)
-            chunk_id = nch > 0 ? __hip_atomic_fetch_add(queue, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-        __syncthreads();
-        const long j = __builtin_amdgcn_readfirstlane(chunk_id);  // uniform: keeps the unit math scalar
-        if (j >= nch) break;
-        const long b = sp.ns + j * sp.chunk;
-        run_blocks<BITS, CB, MT>(a, plan, sp, KB, gu, b, min(sp.n, b + sp.chunk), a_lds, cs_g, cs_u, rows);
     }
 }
 
@@ -726,16 +684,20 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
     const int nact = plan.n + (has_shared ? 1 : 0);
     const int gg = a.inter >> 7, gd = a.hidden >> 7;
     const int w = blockIdx.x, G = gridDim.x;
+    const int nslots = a.routed_slots + 1;  // units exist for every possible slot
 
-    // gate/up: blocks (aslot, proj, cg, kb) with kb < hidden/128; then down: (aslot, cg, kb), kb < inter/128
-    run_phase<BITS, CB, MT>(a, plan, make_split((long)nact * 2 * gg * (a.hidden >> 7), G), a.hidden >> 7, true,
-                            a.queue_gu, a_lds, cs_g, cs_u, rows);
-    HX_TS_BASE(0);
-    HX_TS(3);
-    HX_TS_BASE(16);
-    run_phase<BITS, CB, MT>(a, plan, make_split((long)nact * gd * (a.inter >> 7), G), a.inter >> 7, false,
-                            a.queue_d, a_lds, cs_g, cs_u, rows);
-
+    if (w < a.units_gu) {
+        const int KB = a.hidden >> 7;
+        const Split sp{(long)nslots * 2 * gg * KB, a.units_gu};
+        run_blocks<BITS, CB, MT>(a, plan, sp, KB, true, nact, sp.sstart(w), sp.sstart(w + 1), a_lds, cs_g, cs_u,
+                                 rows);
+    } else {
+        HX_TS_BASE(16);
+        const int KB = a.inter >> 7, u = w - a.units_gu;
+        const Split sp{(long)nslots * gd * KB, a.units_d};
+        run_blocks<BITS, CB, MT>(a, plan, sp, KB, false, nact, sp.sstart(u), sp.sstart(u + 1), a_lds, cs_g, cs_u,
+                                 rows);
+    }
     HX_TS_BASE(0);
     HX_TS(4);
     // the last workgroup to finish clears the activation flags for the next call
@@ -746,11 +708,7 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
     if (last) {
         for (int i = threadIdx.x; i < (a.routed_slots + 1) * gg; i += hx_nthreads())
             __hip_atomic_store(&a.ready[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (threadIdx.x == 0) {
-            __hip_atomic_store(a.queue_gu, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(a.queue_d, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(a.exit_count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        if (threadIdx.x == 0) __hip_atomic_store(a.exit_count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 

@@ -7,33 +7,14 @@
 
 namespace hx {
 
-// Grid = every workgroup that fits at once; LDS = the input rows of the longest segment, i.e. one
-// share of 128-k blocks (capped at K / 128), with the share sized for all slots active.
+// Grid = the gate/up units then the down units; LDS = the input rows of the longest unit.
 template <class Kernel>
-static hipError_t launch_k(Kernel kernel, const MoeDecodeArgs& a, hipStream_t st)
+static hipError_t launch_k(Kernel kernel, const MoeDecodeArgs& a0, hipStream_t st)
 {
-    const long slots = a.routed_slots + 1;
-    const long gg = a.inter / 128, gd = a.hidden / 128;
-    const long nmax = 2 * slots * gg * gd > slots * gd * gg ? 2 * slots * gg * gd : slots * gd * gg;
-    const long kbmax = gg > gd ? gg : gd;
-    size_t lds = (size_t)4 * 128 * sizeof(_Float16);
-    int grid = 1;
-    for (int it = 0; it < 3; ++it) {
-        grid = resident_blocks(reinterpret_cast<const void*>(kernel), DEC_THREADS, lds);
-        if (grid < 1) grid = 1;
-        if (const char* v = getenv("HX_MOE_WG_PER_CU")) {  // tuning: fewer workgroups per CU
-            int cus = 0;
-            (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
-            const int cap = cus * atoi(v);
-            if (cap > 0 && cap < grid) grid = cap;
-        }
-        long share = (nmax + grid - 1) / grid;
-        if (share > kbmax) share = kbmax;
-        const size_t need = (size_t)4 * share * 128 * sizeof(_Float16);
-        if (need <= lds) break;
-        lds = need;
-    }
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(DEC_THREADS), lds, st, a);
+    MoeDecodeArgs a = a0;
+    const int kc = decode_units(a);
+    const size_t lds = (size_t)4 * kc * sizeof(_Float16);
+    hipLaunchKernelGGL(kernel, dim3(a.units_gu + a.units_d), dim3(DEC_THREADS), lds, st, a);
     return hipGetLastError();
 }
 
