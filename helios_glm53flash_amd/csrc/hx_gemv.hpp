@@ -432,6 +432,7 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     const int voff0 = lane_off + ((q * BITS + NW - 1) % NW) * 4, voff1 = lane_off + q * BITS * 4;
     const int row_bytes = tiles_n * NW * 4;
     auto soff = [&](int st) { return ((k0 + step_k(min(st, steps - 1))) >> 4) * row_bytes; };
+    HX_TS(0);
     InputRegs in;
     if (!g.pre_transformed) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, false);
     if (steps > 0) {
@@ -439,7 +440,9 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
         for (int j = 0; j < PF; ++j) load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff(j));
     }
 
+    HX_TS(1);
     before_input();
+    HX_TS(3);
     if (g.pre_transformed) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, true);
     input_finish(a_lds, in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, g.pre_transformed);
     hx_lds_barrier();

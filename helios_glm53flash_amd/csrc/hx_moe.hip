@@ -5,7 +5,11 @@
 #include "hx_kernels.hpp"
 #include "hx_moe.hpp"
 
+#include <stdio.h>
 #include <stdlib.h>
+
+#include <mutex>
+#include <vector>
 
 
 
@@ -77,22 +81,52 @@ MoeDecodeArgs MoeWs::decode_args(char* base) const
     return a;
 }
 
-// Units of the decode layer: gate/up per (slot, projection, column group, k-split of kc_gu), down
-// per (slot, column group, k-split of kc_d), kc = the largest multiple-of-128 divisor of K up to
-// 1024 (HX_MOE_KC overrides the cap, for tuning), so that every unit is one segment of one column
-// group: 1152 + 576 workgroups for 9 slots at hidden 4096, intermediate 2048, i.e. a little under
-// two rounds of resident workgroups (1024 on MI355X).  Measured (config-3 layer): cap 512 81 us,
-// 1024 62-64 us, 2048 65 us, 4096 72 us; unaligned units sized to whole rounds of resident
-// workgroups 61-68 us.  Returns the longest unit's k extent.
-int decode_units(MoeDecodeArgs& a)
+// Workgroups of `kernel` that fit on the current device at once (CU count x blocks per CU), cached
+// per (device, kernel, threads, lds).
+int resident_blocks(const void* kernel, int threads, size_t lds)
 {
-    int cap = 1024;
-    if (const char* v = getenv("HX_MOE_KC")) cap = atoi(v) > 0 ? atoi(v) : cap;
-    const int kg = gemv_kc_for(a.hidden, cap), kd = gemv_kc_for(a.inter, cap);
-    const int slots = a.routed_slots + 1;
-    a.units_gu = slots * 2 * (a.inter / 128) * (a.hidden / kg);
-    a.units_d = slots * (a.hidden / 128) * (a.inter / kd);
-    return kg > kd ? kg : kd;
+    struct Key {
+        int dev;
+        const void* k;
+        int threads;
+        size_t lds;
+        int n;
+    };
+    static std::mutex mu;
+    static std::vector<Key> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Key& c : cache)
+        if (c.dev == dev && c.k == kernel && c.threads == threads && c.lds == lds) return c.n;
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, lds) != hipSuccess || per <= 0) per = 1;
+    cache.push_back({dev, kernel, threads, lds, cus * per});
+    return cus * per;
+}
+
+// Units of the decode layer (the grid): gate/up units = one round of resident workgroups, down
+// units likewise (a second round, dispatched as the first one's workgroups finish), each clamped
+// to [column groups, blocks] of its phase; a column group gets U / C or U / C + 1 units (equal k
+// ranges, one segment each).  Measured (config-3 layer, 1024 resident): 1024 + 1024 units 53 us;
+// 1024 + 512 58-60 us; 576 + 576 (all resident at once) 57 us; 1152 + 576 (every column group in 4
+// / 2 units, some gate/up in the second round) 61 us; a fused variant (workgroup w runs gate/up
+// unit w then down unit w, reusing its plan) 60 us.  HX_MOE_UNITS="g,d" scales the two counts
+// (tuning).  Returns the longest unit's k extent.
+int decode_units(MoeDecodeArgs& a, int resident)
+{
+    const long slots = a.routed_slots + 1;
+    const long cg_gu = slots * 2 * (a.inter / 128), kb_gu = a.hidden / 128;
+    const long cg_d = slots * (a.hidden / 128), kb_d = a.inter / 128;
+    double fg = 1.0, fd = 1.0;
+    if (const char* v = getenv("HX_MOE_UNITS")) sscanf(v, "%lf,%lf", &fg, &fd);
+    auto clampu = [](long u, long c, long kb) { return u < c ? c : (u > c * kb ? c * kb : u); };
+    const long ug = clampu((long)(resident * fg), cg_gu, kb_gu), ud = clampu((long)(resident * fd), cg_d, kb_d);
+    a.units_gu = (int)ug;
+    a.units_d = (int)ud;
+    const long bg = (kb_gu + ug / cg_gu - 1) / (ug / cg_gu), bd = (kb_d + ud / cg_d - 1) / (ud / cg_d);
+    return (int)(128 * (bg > bd ? bg : bd));
 }
 
 hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t bits_mask, hipStream_t st)

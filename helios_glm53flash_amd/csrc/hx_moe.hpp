@@ -49,8 +49,10 @@ struct PrefillArgs {
 
 // Few-token layer (one persistent launch); bits_mask has bit b set for every bit width b in use.
 hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t bits_mask, hipStream_t st);
-// Sets a.units_gu / a.units_d (the decode layer's grid) and returns the longest unit's k extent.
-int decode_units(MoeDecodeArgs& a);
+// Sets a.units_gu / a.units_d (the decode layer's grid; `resident` = workgroups that fit at once)
+// and returns the longest unit's k extent.
+int decode_units(MoeDecodeArgs& a, int resident);
+int resident_blocks(const void* kernel, int threads, size_t lds);
 // Routed experts for T > 8 tokens: writes per-row fp32 contributions (sorted order) when contrib is
 // non-null, y = fp16(routed + shared_rows) when y is non-null, and the fp32 routed sum into
 // y_routed (added to its contents when accumulate) when y_routed is non-null.

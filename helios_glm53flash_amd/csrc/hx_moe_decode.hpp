@@ -22,6 +22,13 @@ namespace hx {
 constexpr int DEC_MAX_R = 64;  // T * topk rows handled by the few-token path
 
 // Routing plan of one call: sorted rows and active-expert slots.
+// Trellis, suh, svh of gate, up, down of one slot's expert (or of the shared expert).
+struct SlotTables {
+    const void* tr[3];
+    const void* suh[3];
+    const void* svh[3];
+};
+
 struct DecodePlan {
     int n;                     // active routed experts
     int expert[DEC_MAX_R];
@@ -30,6 +37,7 @@ struct DecodePlan {
     int token[DEC_MAX_R];      // token of sorted row r
     float weight[DEC_MAX_R];   // routing weight of sorted row r
     int r2s[DEC_MAX_R];        // flat routing index -> sorted row
+    SlotTables tab;            // tables of the workgroup's own slot
 };
 
 struct MoeDecodeArgs {
@@ -205,55 +213,79 @@ HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, in
     w_out = (float)(_Float16)(w_out * scale / sum);
 }
 
-// Build the plan in LDS (every workgroup computes the same plan).  Layer mode routes the tokens;
-// grouped mode reads the caller's expert_count / token_sorted / weight_sorted.
-__device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p)
+// Tables of expert e (e < 0: the shared expert).
+HX_INLINE void load_slot_tables(const MoeDecodeArgs& a, SlotTables& t, int e)
+{
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        t.tr[j] = e < 0 ? a.sh_tr[j] : a.tr[j][e];
+        t.suh[j] = e < 0 ? a.sh_suh[j] : a.suh[j][e];
+        t.svh[j] = e < 0 ? a.sh_svh[j] : a.svh[j][e];
+    }
+}
+
+// Build the plan in LDS (every workgroup computes the same plan), and the tables of the
+// workgroup's own slot `my_slot` if it is active (slots in plan order, the shared expert after the
+// routed ones).  Layer mode routes the tokens; grouped mode reads the caller's expert_count /
+// token_sorted / weight_sorted.
+__device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p, int my_slot)
 {
     __shared__ int sel_e[DEC_MAX_R];
     __shared__ float sel_w[DEC_MAX_R];
-    __shared__ int first[DEC_MAX_R];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int R = a.T * a.topk;
     if (a.scores) {
+        // one token: wave 0 selects and sorts in registers; more: one wave per token, then LDS
+        int e1 = 0;
+        float w1 = 0.0f;
         for (int t = wave; t < a.T; t += hx_nwaves()) {
             int e;
             float w;
             wave_topk(a.scores + (size_t)t * a.E, a.bias, a.E, a.topk, a.routed_scale, e, w);
-            if (lane < a.topk) {
+            HX_TS(5);
+            if (a.T == 1) {
+                e1 = e;
+                w1 = w;
+            } else if (lane < a.topk) {
                 sel_e[t * a.topk + lane] = e;
                 sel_w[t * a.topk + lane] = w;
             }
         }
-        __syncthreads();
+        if (a.T > 1) __syncthreads();
         if (wave == 0) {
             // stable counting sort of the R <= 64 selections by expert (ascending flat index within an
-            // expert, glue2.cu:244-293 with a deterministic cursor)
+            // expert, glue2.cu:244-293 with a deterministic cursor); selection j is read from lane j
             const int i = lane;
-            const int ei = i < R ? sel_e[i] : 0x7fffffff;
+            const int ei = i < R ? (a.T == 1 ? e1 : sel_e[i]) : 0x7fffffff;
+            const float wi = a.T == 1 ? w1 : (i < R ? sel_w[i] : 0.0f);
             int less = 0, eqb = 0, cnt = 0;
             for (int j = 0; j < R; ++j) {
-                const int ej = sel_e[j];
+                const int ej = __builtin_amdgcn_readlane(ei, j);
                 less += ej < ei;
                 eqb += (ej == ei) && (j < i);
                 cnt += ej == ei;
             }
-            if (i < R) first[i] = eqb == 0;
-            __builtin_amdgcn_wave_barrier();
-            int dless = 0;
-            for (int j = 0; j < R; ++j) dless += first[j] && sel_e[j] < ei;
+            const uint64_t fm = __ballot(i < R && eqb == 0);  // first selection of each expert
+            int dless = 0;                                     // distinct experts below ei
+            for (int j = 0; j < R; ++j)
+                if ((fm >> j) & 1) dless += __builtin_amdgcn_readlane(ei, j) < ei;
+            const int n = __popcll(fm);
             if (i < R) {
                 const int pos = less + eqb;
                 p.token[pos] = i / a.topk;
-                p.weight[pos] = sel_w[i];
+                p.weight[pos] = wi;
                 p.r2s[i] = pos;
                 if (eqb == 0) {
                     p.expert[dless] = ei;
                     p.start[dless] = less;
                     p.count[dless] = cnt;
+                    if (dless == my_slot) load_slot_tables(a, p.tab, ei);
                 }
             }
-            const uint64_t fm = __ballot(i < R && eqb == 0);
-            if (lane == 0) p.n = __popcll(fm);
+            if (lane == 0) {
+                p.n = n;
+                if (my_slot == n) load_slot_tables(a, p.tab, -1);
+            }
         }
     } else {
         if (wave == 0) {
@@ -286,7 +318,12 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
                 seen += __popcll(act);
                 base += __shfl(cs, 63, 64);
             }
-            if (lane == 0) p.n = min(seen, DEC_MAX_R);
+            if (lane == 0) {
+                p.n = min(seen, DEC_MAX_R);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                if (my_slot < p.n) load_slot_tables(a, p.tab, p.expert[my_slot]);
+                else if (my_slot == p.n) load_slot_tables(a, p.tab, -1);
+            }
             if (lane < R) {
                 p.token[lane] = min(max((int)a.token_sorted[lane], 0), a.T - 1);
                 p.weight[lane] = (float)a.weight_sorted[lane];
@@ -352,15 +389,15 @@ HX_INLINE int proj_bits(const MoeDecodeArgs& a, int proj, int expert)
 // guad epilogue for rows m < count of one 128-column group (hadamard_inner.cuh:284-413 for routed
 // experts; swiglu_clamp + down-input transform for the shared expert, runner.cpp:723-738).
 template <int MT>
-__device__ __forceinline__ void guad_epilogue(const MoeDecodeArgs& a, const SlotInfo& si, int slot, int cg, const float* cs_g,
-                              const float* cs_u)
+__device__ __forceinline__ void guad_epilogue(const MoeDecodeArgs& a, const DecodePlan& p, const SlotInfo& si, int slot,
+                                              int cg, const float* cs_g, const float* cs_u)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = cg * 128 + 2 * lane;
     const bool shared = si.expert < 0;
-    const _Float16* svg = static_cast<const _Float16*>(shared ? a.sh_svh[0] : a.svh[0][si.expert]);
-    const _Float16* svu = static_cast<const _Float16*>(shared ? a.sh_svh[1] : a.svh[1][si.expert]);
-    const _Float16* sud = static_cast<const _Float16*>(shared ? a.sh_suh[2] : a.suh[2][si.expert]);
+    const _Float16* svg = static_cast<const _Float16*>(p.tab.svh[0]);
+    const _Float16* svu = static_cast<const _Float16*>(p.tab.svh[1]);
+    const _Float16* sud = static_cast<const _Float16*>(p.tab.suh[2]);
     const hx_h2 sg = *reinterpret_cast<const hx_h2*>(svg + c);
     const hx_h2 su = *reinterpret_cast<const hx_h2*>(svu + c);
     const hx_h2 sd = *reinterpret_cast<const hx_h2*>(sud + c);
@@ -417,7 +454,7 @@ __device__ __forceinline__ void down_epilogue(const MoeDecodeArgs& a, const Deco
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = cg * 128 + 2 * lane;
     const bool shared = si.expert < 0;
-    const _Float16* svd = static_cast<const _Float16*>(shared ? a.sh_svh[2] : a.svh[2][si.expert]);
+    const _Float16* svd = static_cast<const _Float16*>(p.tab.svh[2]);
     const hx_h2 sd = *reinterpret_cast<const hx_h2*>(svd + c);
     const int R = a.T * a.topk;
     for (int m = wave; m < si.count && m < MT; m += hx_nwaves()) {
@@ -522,21 +559,37 @@ HX_INLINE void wait_flag(const int* flag, int target, int* status)
     }
 }
 
-// Split of n blocks into g equal contiguous units (unit w is [sstart(w), sstart(w+1))); column
-// group c covers blocks [c*kb, c*kb + kb), its segments are numbered in k order.
+// Units of a phase: C column groups of KB 128-k blocks in U units, C <= U <= C * KB.  The first
+// r = U % C column groups get q + 1 = U / C + 1 units, the others q; the units of a column group
+// are equal contiguous k ranges, numbered in k order (the order their partial sums are added in).
 struct Split {
-    long n;
-    int g;
-    HX_INLINE long sstart(int w) const { return (long)w * n / g; }
-    HX_INLINE int sowner(long x) const { return (int)(((x + 1) * g - 1) / n); }
-    HX_INLINE int count(long c, int kb) const { return sowner(c * kb + kb - 1) - sowner(c * kb) + 1; }
-    HX_INLINE int index(long c, int kb, long b) const { return sowner(b) - sowner(c * kb); }  // b: first block
+    int C, KB, q, r;
+    HX_INLINE static Split make(int C, int KB, int U)
+    {
+        U = max(C, min(U, C * KB));
+        return Split{C, KB, U / C, U % C};
+    }
+    HX_INLINE int count(long c) const { return q + (c < r ? 1 : 0); }
+    // unit w -> column group of the unit
+    HX_INLINE int ucg(int w) const
+    {
+        const int big = r * (q + 1);
+        return w < big ? w / (q + 1) : r + (w - big) / q;
+    }
+    // unit w -> index of the unit within its column group
+    HX_INLINE int uidx(int w) const
+    {
+        const int big = r * (q + 1);
+        return w < big ? w % (q + 1) : (w - big) % q;
+    }
+    HX_INLINE int kb_begin(long c, int j) const { return j * KB / count(c); }
 };
 
 template <int BITS, int CB, int MT>
 __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, long c,
-                                           int kb0, int kb1, uint32_t* a_lds, float* cs_g, float* cs_u, int* rows)
+                                           int j, uint32_t* a_lds, float* cs_g, float* cs_u, int* rows)
 {
+    const int kb0 = sp.kb_begin(c, j), kb1 = sp.kb_begin(c, j + 1);
     const int gg = a.inter >> 7, KB = a.hidden >> 7;
     const int aslot = (int)(c / (2 * gg)), proj = (int)((c / gg) & 1), cg = (int)(c % gg);
     const int slot = aslot < plan.n ? aslot : a.routed_slots;
@@ -549,8 +602,8 @@ __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodeP
     GemvArgs g;
     g.x = a.x;
     g.rows = rows;
-    g.trellis = static_cast<const uint16_t*>(shared ? pick3(a.sh_tr, proj) : pick3(a.tr, proj)[si.expert]);
-    g.suh = static_cast<const _Float16*>(shared ? pick3(a.sh_suh, proj) : pick3(a.suh, proj)[si.expert]);
+    g.trellis = static_cast<const uint16_t*>(plan.tab.tr[proj]);
+    g.suh = static_cast<const _Float16*>(plan.tab.suh[proj]);
     g.M = si.count;
     g.K = a.hidden;
     g.N = a.inter;
@@ -559,15 +612,15 @@ __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodeP
 
     // partial of segment i of (slot, proj, cg): partial_{g,u}[((slot*gg + cg) * (KB + 1) + i) * 8 + m][128]
     float* pbase = (proj == 0 ? a.partial_g : a.partial_u) + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
-    publish_partial<MT>(pbase, si.count, 128, 0, sp.index(c, KB, c * KB + kb0), cs_g);
+    publish_partial<MT>(pbase, si.count, 128, 0, j, cs_g);
     const long cgate = c - proj * gg, cup = cgate + gg;
-    const int ng = sp.count(cgate, KB), nu = sp.count(cup, KB);
+    const int ng = sp.count(cgate), nu = sp.count(cup);
     if (!arrive_last(&a.counter_gu[slot * gg + cg], ng + nu)) return;
     float* pg = a.partial_g + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
     float* pu = a.partial_u + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
     gather_partials<MT>(pg, si.count, 128, ng, 0, cs_g);
     gather_partials<MT>(pu, si.count, 128, nu, 0, cs_u);
-    guad_epilogue<MT>(a, si, slot, cg, cs_g, cs_u);
+    guad_epilogue<MT>(a, plan, si, slot, cg, cs_g, cs_u);
     // the activations of this block are stored (device-coherent): flag them for the down phase
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -576,8 +629,9 @@ __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodeP
 
 template <int BITS, int CB, int MT>
 __device__ __forceinline__ void d_segment(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, long c,
-                                          int kb0, int kb1, uint32_t* a_lds, float* cs)
+                                          int j, uint32_t* a_lds, float* cs)
 {
+    const int kb0 = sp.kb_begin(c, j), kb1 = sp.kb_begin(c, j + 1);
     const int gd = a.hidden >> 7, gg = a.inter >> 7, KB = a.inter >> 7;
     const int aslot = (int)(c / gd), cg = (int)(c % gd);
     const int slot = aslot < plan.n ? aslot : a.routed_slots;
@@ -587,7 +641,7 @@ __device__ __forceinline__ void d_segment(const MoeDecodeArgs& a, const DecodePl
     GemvArgs g;
     g.x = a.act + (size_t)slot * 8 * a.inter;
     g.rows = nullptr;
-    g.trellis = static_cast<const uint16_t*>(shared ? a.sh_tr[2] : a.tr[2][si.expert]);
+    g.trellis = static_cast<const uint16_t*>(plan.tab.tr[2]);
     g.suh = nullptr;
     g.M = si.count;
     g.K = a.inter;
@@ -601,9 +655,9 @@ __device__ __forceinline__ void d_segment(const MoeDecodeArgs& a, const DecodePl
     };
     gemv_range<BITS, CB, MT, DEC_KS>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs, wait_inputs);
 
-    const int count = sp.count(c, KB);
+    const int count = sp.count(c);
     float* pbase = a.partial_d + (size_t)(slot * gd + cg) * (KB + 1) * 8 * 128;
-    publish_partial<MT>(pbase, si.count, 128, 0, sp.index(c, KB, c * KB + kb0), cs);
+    publish_partial<MT>(pbase, si.count, 128, 0, j, cs);
     if (!arrive_last(&a.counter_d[slot * gd + cg], count)) return;
     gather_partials<MT>(pbase, si.count, 128, count, 0, cs);
     down_epilogue<MT>(a, plan, si, cg, cs);
@@ -620,37 +674,30 @@ HX_INLINE int slot_bits(const MoeDecodeArgs& a, const DecodePlan& p, int slot, i
     return proj_bits(a, proj, si.valid ? si.expert : 0);
 }
 
-// Runs the blocks [b, e) of a phase as segments of single column groups.
+// Runs unit (c, j) of a phase (one segment of one column group); units of inactive slots return.
 template <int BITS, int CB, int MT>
-__device__ __forceinline__ void run_blocks(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, int KB,
-                                           bool gu, int nact, long b, long e, uint32_t* a_lds, float* cs_g,
-                                           float* cs_u, int* rows)
+__device__ __forceinline__ void run_unit(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, bool gu,
+                                         int nact, long c, int j, uint32_t* a_lds, float* cs_g, float* cs_u,
+                                         int* rows)
 {
     const int gg = a.inter >> 7, gd = a.hidden >> 7;
-    while (b < e) {
-        const long c = b / KB;
-        const int kb0 = (int)(b % KB);
-        const int kb1 = (int)min((long)KB, kb0 + (e - b));
-        if ((gu ? c / (2 * gg) : c / gd) >= nact) return;  // slots in order: the rest is inactive too
-        int bits = BITS;
-        if constexpr (BITS == 0) {
-            const int aslot = (int)(gu ? c / (2 * gg) : c / gd);
-            bits = slot_bits(a, plan, aslot < plan.n ? aslot : a.routed_slots, gu ? (int)((c / gg) & 1) : 2);
-        }
-        switch (bits) {
+    const int aslot = (int)(gu ? c / (2 * gg) : c / gd);
+    if (aslot >= nact) return;
+    int bits = BITS;
+    if constexpr (BITS == 0)
+        bits = slot_bits(a, plan, aslot < plan.n ? aslot : a.routed_slots, gu ? (int)((c / gg) & 1) : 2);
+    switch (bits) {
 #define HX_SEG_CASE(B)                                                                             \
     case B:                                                                                        \
         if constexpr (BITS == 0 || BITS == B) {                                                    \
-            if (gu) gu_segment<B, CB, MT>(a, plan, sp, c, kb0, kb1, a_lds, cs_g, cs_u, rows);        \
-            else d_segment<B, CB, MT>(a, plan, sp, c, kb0, kb1, a_lds, cs_g);                        \
+            if (gu) gu_segment<B, CB, MT>(a, plan, sp, c, j, a_lds, cs_g, cs_u, rows);               \
+            else d_segment<B, CB, MT>(a, plan, sp, c, j, a_lds, cs_g);                               \
         }                                                                                          \
         break;
-            HX_SEG_CASE(1) HX_SEG_CASE(2) HX_SEG_CASE(3) HX_SEG_CASE(4)
-            HX_SEG_CASE(5) HX_SEG_CASE(6) HX_SEG_CASE(7) HX_SEG_CASE(8)
+        HX_SEG_CASE(1) HX_SEG_CASE(2) HX_SEG_CASE(3) HX_SEG_CASE(4)
+        HX_SEG_CASE(5) HX_SEG_CASE(6) HX_SEG_CASE(7) HX_SEG_CASE(8)
 #undef HX_SEG_CASE
-            default: break;
-        }
-        b += kb1 - kb0;
+        default: break;
     }
 }
 
@@ -666,7 +713,15 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
     HX_SETPRIO(3);  // the routing plan gates every workgroup
     HX_TS_BASE(0);
     HX_TS(0);
-    build_plan(a, plan);
+    const int gg = a.inter >> 7, gd = a.hidden >> 7;
+    const int w = blockIdx.x, G = gridDim.x;
+    const int nslots = a.routed_slots + 1;  // units exist for every possible slot
+    const bool gu = w < a.units_gu;
+    const Split sp = gu ? Split::make(nslots * 2 * gg, a.hidden >> 7, a.units_gu)
+                        : Split::make(nslots * gd, a.inter >> 7, a.units_d);
+    const int u = gu ? w : w - a.units_gu;
+    const int c = sp.ucg(u), j = sp.uidx(u);
+    build_plan(a, plan, gu ? c / (2 * gg) : c / gd);
     HX_TS(1);
     HX_TS_BASE(8);
     if (blockIdx.x == 0 && a.out_idx) {
@@ -682,22 +737,8 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
     }
     const bool has_shared = a.sh_tr[0] != nullptr;
     const int nact = plan.n + (has_shared ? 1 : 0);
-    const int gg = a.inter >> 7, gd = a.hidden >> 7;
-    const int w = blockIdx.x, G = gridDim.x;
-    const int nslots = a.routed_slots + 1;  // units exist for every possible slot
-
-    if (w < a.units_gu) {
-        const int KB = a.hidden >> 7;
-        const Split sp{(long)nslots * 2 * gg * KB, a.units_gu};
-        run_blocks<BITS, CB, MT>(a, plan, sp, KB, true, nact, sp.sstart(w), sp.sstart(w + 1), a_lds, cs_g, cs_u,
-                                 rows);
-    } else {
-        HX_TS_BASE(16);
-        const int KB = a.inter >> 7, u = w - a.units_gu;
-        const Split sp{(long)nslots * gd * KB, a.units_d};
-        run_blocks<BITS, CB, MT>(a, plan, sp, KB, false, nact, sp.sstart(u), sp.sstart(u + 1), a_lds, cs_g, cs_u,
-                                 rows);
-    }
+    if (!gu) HX_TS_BASE(16);
+    run_unit<BITS, CB, MT>(a, plan, sp, gu, nact, c, j, a_lds, cs_g, cs_u, rows);
     HX_TS_BASE(0);
     HX_TS(4);
     // the last workgroup to finish clears the activation flags for the next call

@@ -7,13 +7,19 @@
 
 namespace hx {
 
-// Grid = the gate/up units then the down units; LDS = the input rows of the longest unit.
+// Grid = the gate/up units then the down units (decode_units); LDS = the input rows of the longest unit (the
+// unit count depends on the occupancy, which depends on the LDS: iterated to a fixed point).
 template <class Kernel>
 static hipError_t launch_k(Kernel kernel, const MoeDecodeArgs& a0, hipStream_t st)
 {
     MoeDecodeArgs a = a0;
-    const int kc = decode_units(a);
-    const size_t lds = (size_t)8 * kc * sizeof(_Float16);
+    size_t lds = (size_t)8 * 1024 * sizeof(_Float16);
+    for (int it = 0; it < 4; ++it) {
+        const int res = resident_blocks(reinterpret_cast<const void*>(kernel), DEC_THREADS, lds);
+        const size_t need = (size_t)8 * decode_units(a, res) * sizeof(_Float16);
+        if (need == lds) break;
+        lds = need;
+    }
     hipLaunchKernelGGL(kernel, dim3(a.units_gu + a.units_d), dim3(DEC_THREADS), lds, st, a);
     return hipGetLastError();
 }
