@@ -1,13 +1,14 @@
-// hx_moe_decode.hpp -- fused MoE layer for few tokens (T <= 8, T*topk <= 64) on gfx950 in two
-// launches, without host synchronisation:
+// hx_moe_decode.hpp -- fused MoE layer for few tokens (T <= 8, T*topk <= 64) on gfx950 in ONE
+// launch, without host synchronisation.  Every workgroup computes the router top-k and the
+// token-by-expert permutation from the fp16 scores (a few hundred bytes), then runs one unit:
 //
-//   kernel A  router top-k + token-by-expert permutation (recomputed by every workgroup from the
-//             fp16 scores, a few hundred bytes), then one split-K slice of one expert's gate or up
-//             GEMV with the trellis decode fused; the last-arriving slice of a (slot, column group)
-//             runs the SiLU-gate epilogue and stores the down-projection input.
-//   kernel B  one split-K slice of one expert's down GEMV; the last slice of a (slot, column group)
-//             writes the weighted contribution rows; the last of all slots of a column group then
-//             reduces the contributions in routing-rank order, adds the shared expert and writes y.
+//   gate/up unit  one k range of one expert's gate or up GEMV with the trellis decode fused; the
+//                 last-arriving unit of a (slot, column group) adds the partial sums, runs the
+//                 SiLU-gate epilogue, stores the down-projection input and raises its ready flag.
+//   down unit     requests its tile words, waits for the ready flags of its k range, then one k
+//                 range of one expert's down GEMV; the last unit of a (slot, column group) writes
+//                 the weighted contribution rows; the last of all slots of a column group reduces
+//                 the contributions in routing-rank order, adds the shared expert and writes y.
 //
 // Reference semantics: src/cuda/aux/routing.cu:211-329 (router), src/engine/glue2.cu:244-311
 // (permutation, ordered reduction), src/cuda/quant/exl3_moe_kernel.cuh:57-262 and
