@@ -550,7 +550,11 @@ HX_INLINE void wait_flag(const int* flag, int target, int* status)
 {
     int spins = 0;
     while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-        __builtin_amdgcn_s_sleep(8);
+        // back off: device-coherent loads of a few flags from a thousand workgroups all go to the
+        // memory channels of those flags, which the weight streams go through too
+        if (spins < 4) __builtin_amdgcn_s_sleep(4);
+        else if (spins < 16) __builtin_amdgcn_s_sleep(16);
+        else __builtin_amdgcn_s_sleep(64);
         if ((++spins & 1023) == 0 && __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
             break;  // another wait already gave up: do not add its bound to every later wait
         if (spins > (1 << 22)) {
@@ -722,6 +726,10 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
                         : Split::make(nslots * gd, a.inter >> 7, a.units_d);
     const int u = gu ? w : w - a.units_gu;
     const int c = sp.ucg(u), j = sp.uidx(u);
+    // every workgroup routes for itself: the scores are a few plain (cached) loads, whereas a plan
+    // published by one workgroup would be read by all with device-coherent loads of the same few
+    // lines (measured: 54 -> 97 us for the config-3 layer, the weight streams through those
+    // lines' memory channel stall)
     build_plan(a, plan, gu ? c / (2 * gg) : c / gd);
     HX_TS(1);
     HX_TS_BASE(8);
