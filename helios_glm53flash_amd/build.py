@@ -33,12 +33,22 @@ HIP_FLAGS = [
 ]
 
 
+# Per-file flags.  The MFMA-tile kernels keep their accumulators in VGPRs: with the default
+# selection the accumulators live in AGPRs while the MFMAs are selected in their VGPR form, and every
+# k step copies them back and forth (3 extra VALU moves per MFMA on gfx950, measured in the
+# generated code).
+FILE_FLAGS = {
+    "hx_moe_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "hx_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = OUT_DIR / (src.stem + ".o")
-    deps = [src] + sorted(CSRC.glob("*.hpp")) + [ROOT / "include" / "hx" / "exl3.h"]
+    deps = [src] + sorted(CSRC.glob("*.hpp")) + [ROOT / "include" / "hx" / "exl3.h", Path(__file__)]
     if obj.exists() and obj.stat().st_mtime > max(d.stat().st_mtime for d in deps):
         return obj
-    cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

@@ -24,6 +24,7 @@ constexpr int MF_THREADS = 256;
 constexpr int MF_BM = 128;  // largest row tile
 constexpr int MF_BN = 128;
 constexpr int MF_BK = 64;
+constexpr int MF_PF = 3;  // chunks of global loads in flight
 constexpr int MF_LDA = MF_BK + 8;  // halves per LDS row (pad against bank conflicts)
 constexpr int MF_LDC = MF_BN + 4;  // floats per LDS row in the epilogue
 constexpr int MF_AB = (MF_BM + MF_BN) * MF_LDA;  // halves of one A + B buffer
@@ -81,37 +82,39 @@ __device__ __forceinline__ void mfma_tile(const _Float16* A, long lda, int rows,
     const int voff0 = t_off + ((q * BITS + NW - 1) % NW) * 4, voff1 = t_off + q * BITS * 4;
     const int row_bytes = tiles_n * NW * 4;
 
-    hx_u4v av[NA];
-    uint32_t wv[BITS + 1];
+    // global loads run MF_PF chunks ahead of the LDS stores (one chunk of matrix-core work covers
+    // far less than an HBM round trip); slot s of the register ring holds chunk c with c % MF_PF == s
+    hx_u4v av[MF_PF][NA];
+    uint32_t wv[MF_PF][BITS + 1];
     float rs[NA];
 #pragma unroll
     for (int i = 0; i < NA; ++i) rs[i] = 0.0f;
 
-    auto load_chunk = [&](int k0) {
+    auto load_chunk = [&](int slot, int k0) {
 #pragma unroll
-        for (int i = 0; i < NA; ++i) av[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[i], k0 * 2, 0);
-        load_quarter_buf<BITS>(wv, rt, voff0, voff1, (k0 >> 4) * row_bytes);
+        for (int i = 0; i < NA; ++i) av[slot][i] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[i], k0 * 2, 0);
+        load_quarter_buf<BITS>(wv[slot], rt, voff0, voff1, (k0 >> 4) * row_bytes);
     };
-    auto store_chunk = [&](int buf, bool count) {
+    auto store_chunk = [&](int slot, int buf, bool count) {
         _Float16* as = sm.ab[buf];
         _Float16* bs = sm.ab[buf] + MF_BM * MF_LDA;
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
             const int idx = t + MF_THREADS * i;
-            *reinterpret_cast<hx_u4v*>(&as[(idx >> 3) * MF_LDA + 8 * (idx & 7)]) = av[i];
+            *reinterpret_cast<hx_u4v*>(&as[(idx >> 3) * MF_LDA + 8 * (idx & 7)]) = av[slot][i];
             if (CB == 2 && count) {
                 const hx_h2 one = {(_Float16)1.0f, (_Float16)1.0f};
                 float s = rs[i];
-                s = __builtin_amdgcn_fdot2(u32_as_h2(av[i].x), one, s, false);
-                s = __builtin_amdgcn_fdot2(u32_as_h2(av[i].y), one, s, false);
-                s = __builtin_amdgcn_fdot2(u32_as_h2(av[i].z), one, s, false);
-                s = __builtin_amdgcn_fdot2(u32_as_h2(av[i].w), one, s, false);
+                s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].x), one, s, false);
+                s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].y), one, s, false);
+                s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].z), one, s, false);
+                s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].w), one, s, false);
                 rs[i] = s;
             }
         }
         uint32_t d[16];
-        if constexpr (CB == 2) quarter_affine<BITS>(wv, d);
-        else quarter_decode<BITS, CB>(wv, d);
+        if constexpr (CB == 2) quarter_affine<BITS>(wv[slot], d);
+        else quarter_decode<BITS, CB>(wv[slot], d);
         _Float16* bcol = bs + (16 * tc + q) * MF_LDA + 16 * tr;
         *reinterpret_cast<hx_h8*>(bcol) = quarter_operand<0, 0>(d);
         *reinterpret_cast<hx_h8*>(bcol + 8) = quarter_operand<0, 1>(d);
@@ -120,33 +123,40 @@ __device__ __forceinline__ void mfma_tile(const _Float16* A, long lda, int rows,
     };
 
     const int nk = K / MF_BK;
-    load_chunk(0);
-    store_chunk(0, true);
+    // prologue: chunks 0 .. MF_PF-1 requested (past the end: the last chunk again, never stored)
+#pragma unroll
+    for (int s = 0; s < MF_PF; ++s) load_chunk(s, min(s, nk - 1) * MF_BK);
+    store_chunk(0, 0, true);
     __syncthreads();
-    for (int c = 0; c < nk; ++c) {
-        const int cur = c & 1;
-        // next chunk's loads (the last iteration repeats the last chunk; its decode is not used)
-        const bool more = c + 1 < nk;
-        load_chunk(min(c + 1, nk - 1) * MF_BK);
-        const _Float16* as = sm.ab[cur];
-        const _Float16* bs = sm.ab[cur] + MF_BM * MF_LDA;
+    for (int c0 = 0; c0 < nk; c0 += MF_PF) {
 #pragma unroll
-        for (int kk = 0; kk < MF_BK; kk += 32) {
-            hx_h8 af[MB], bf[4];
+        for (int u = 0; u < MF_PF; ++u) {
+            const int c = c0 + u;  // chunk in LDS buffer c & 1, its registers (slot u) are free
+            if (c >= nk) break;
+            load_chunk(u, min(c + MF_PF, nk - 1) * MF_BK);
+            const _Float16* as = sm.ab[c & 1];
+            const _Float16* bs = sm.ab[c & 1] + MF_BM * MF_LDA;
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-                af[mb] = *reinterpret_cast<const hx_h8*>(&as[(WM * wm + 16 * mb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
+            for (int kk = 0; kk < MF_BK; kk += 32) {
+                hx_h8 af[MB], bf[4];
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-                bf[nb] = *reinterpret_cast<const hx_h8*>(&bs[(64 * wn + 16 * nb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
+                for (int mb = 0; mb < MB; ++mb)
+                    af[mb] = *reinterpret_cast<const hx_h8*>(
+                        &as[(WM * wm + 16 * mb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
 #pragma unroll
                 for (int nb = 0; nb < 4; ++nb)
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mb], bf[nb], acc[mb][nb], 0, 0, 0);
+                    bf[nb] = *reinterpret_cast<const hx_h8*>(
+                        &bs[(64 * wn + 16 * nb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                    for (int nb = 0; nb < 4; ++nb)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mb], bf[nb], acc[mb][nb], 0, 0, 0);
+            }
+            // the next chunk (slot (u + 1) % MF_PF, requested MF_PF - 1 chunks ago) into the other buffer
+            store_chunk((u + 1) % MF_PF, (c + 1) & 1, c + 1 < nk);
+            __syncthreads();
         }
-        store_chunk(cur ^ 1, more);
-        __syncthreads();
     }
     if constexpr (CB == 2) {
         // the 8 threads of a row are consecutive lanes
