@@ -24,7 +24,7 @@ constexpr int MF_THREADS = 256;
 constexpr int MF_BM = 128;  // largest row tile
 constexpr int MF_BN = 128;
 constexpr int MF_BK = 64;
-constexpr int MF_PF = 3;  // chunks of global loads in flight
+constexpr int MF_PF = 4;  // chunks of global loads in flight
 constexpr int MF_LDA = MF_BK + 8;  // halves per LDS row (pad against bank conflicts)
 constexpr int MF_LDC = MF_BN + 4;  // floats per LDS row in the epilogue
 constexpr int MF_AB = (MF_BM + MF_BN) * MF_LDA;  // halves of one A + B buffer
