@@ -54,7 +54,7 @@ __device__ void linear_tile_epilogue(const MfmaSmem& sm, int half, int rows, con
 }
 
 template <int BITS, int CB>
-__global__ __launch_bounds__(MF_THREADS) void linear_mfma_kernel(const _Float16* a, const uint32_t* trellis,
+__global__ __launch_bounds__(MF_THREADS, 2) void linear_mfma_kernel(const _Float16* a, const uint32_t* trellis,
                                                                 const _Float16* svh, void* y, int M, int K, int N,
                                                                 bool y_fp32)
 {

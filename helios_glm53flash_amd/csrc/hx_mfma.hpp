@@ -24,7 +24,7 @@ constexpr int MF_THREADS = 256;
 constexpr int MF_BM = 128;  // largest row tile
 constexpr int MF_BN = 128;
 constexpr int MF_BK = 64;
-constexpr int MF_PF = 4;  // chunks of global loads in flight
+constexpr int MF_PF = 3;  // chunks of global loads in flight
 constexpr int MF_LDA = MF_BK + 8;  // halves per LDS row (pad against bank conflicts)
 constexpr int MF_LDC = MF_BN + 4;  // floats per LDS row in the epilogue
 constexpr int MF_AB = (MF_BM + MF_BN) * MF_LDA;  // halves of one A + B buffer
@@ -127,37 +127,46 @@ __device__ __forceinline__ void mfma_tile(const _Float16* A, long lda, int rows,
 #pragma unroll
     for (int s = 0; s < MF_PF; ++s) load_chunk(s, min(s, nk - 1) * MF_BK);
     store_chunk(0, 0, true);
-    __syncthreads();
-    for (int c0 = 0; c0 < nk; c0 += MF_PF) {
+    // LDS-only barriers: __syncthreads() would also wait for every global load in flight, i.e.
+    // drain the prefetch ring at each chunk
+    hx_lds_barrier();
+    // one chunk: c in LDS buffer c & 1, its registers (slot u = c % MF_PF) are free for chunk
+    // c + MF_PF; then chunk c + 1 (slot (u + 1) % MF_PF, requested MF_PF - 1 chunks ago) is stored
+    // into the other buffer
+    auto step = [&](int c, int u) {
+        load_chunk(u, min(c + MF_PF, nk - 1) * MF_BK);
+        const _Float16* as = sm.ab[c & 1];
+        const _Float16* bs = sm.ab[c & 1] + MF_BM * MF_LDA;
 #pragma unroll
-        for (int u = 0; u < MF_PF; ++u) {
-            const int c = c0 + u;  // chunk in LDS buffer c & 1, its registers (slot u) are free
-            if (c >= nk) break;
-            load_chunk(u, min(c + MF_PF, nk - 1) * MF_BK);
-            const _Float16* as = sm.ab[c & 1];
-            const _Float16* bs = sm.ab[c & 1] + MF_BM * MF_LDA;
+        for (int kk = 0; kk < MF_BK; kk += 32) {
+            hx_h8 af[MB], bf[4];
 #pragma unroll
-            for (int kk = 0; kk < MF_BK; kk += 32) {
-                hx_h8 af[MB], bf[4];
+            for (int mb = 0; mb < MB; ++mb)
+                af[mb] = *reinterpret_cast<const hx_h8*>(
+                    &as[(WM * wm + 16 * mb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
 #pragma unroll
-                for (int mb = 0; mb < MB; ++mb)
-                    af[mb] = *reinterpret_cast<const hx_h8*>(
-                        &as[(WM * wm + 16 * mb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
+            for (int nb = 0; nb < 4; ++nb)
+                bf[nb] = *reinterpret_cast<const hx_h8*>(
+                    &bs[(64 * wn + 16 * nb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
                 for (int nb = 0; nb < 4; ++nb)
-                    bf[nb] = *reinterpret_cast<const hx_h8*>(
-                        &bs[(64 * wn + 16 * nb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-                    for (int nb = 0; nb < 4; ++nb)
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mb], bf[nb], acc[mb][nb], 0, 0, 0);
-            }
-            // the next chunk (slot (u + 1) % MF_PF, requested MF_PF - 1 chunks ago) into the other buffer
-            store_chunk((u + 1) % MF_PF, (c + 1) & 1, c + 1 < nk);
-            __syncthreads();
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mb], bf[nb], acc[mb][nb], 0, 0, 0);
         }
+        store_chunk((u + 1) % MF_PF, (c + 1) & 1, c + 1 < nk);
+        hx_lds_barrier();
+    };
+    // whole groups of MF_PF chunks without exits (an exit inside the group makes the compiler wait
+    // for every load in flight where the paths join), then the remaining chunks
+    const int nmain = nk - nk % MF_PF;
+    for (int c0 = 0; c0 < nmain; c0 += MF_PF) {
+#pragma unroll
+        for (int u = 0; u < MF_PF; ++u) step(c0 + u, u);
     }
+#pragma unroll
+    for (int u = 0; u < MF_PF - 1; ++u)
+        if (nmain + u < nk) step(nmain + u, u);
     if constexpr (CB == 2) {
         // the 8 threads of a row are consecutive lanes
 #pragma unroll

@@ -156,7 +156,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job
 }
 
 template <int CB>
-__global__ __launch_bounds__(MF_THREADS) void grouped_gemm_kernel(GroupedGemmArgs g)
+__global__ __launch_bounds__(MF_THREADS, 2) void grouped_gemm_kernel(GroupedGemmArgs g)
 {
     __shared__ MfmaSmem sm;
     const int job_i = blockIdx.y;
@@ -318,7 +318,7 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
 }
 
 template <int CB>
-__global__ __launch_bounds__(MF_THREADS) void grouped_gu_kernel(GuArgs a)
+__global__ __launch_bounds__(MF_THREADS, 2) void grouped_gu_kernel(GuArgs a)
 {
     __shared__ MfmaSmem sm;
     const int job_i = blockIdx.y;
