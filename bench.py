@@ -308,6 +308,48 @@ def profile_only(torch, moe):
     print("profile workload done: copy 256 MiB x3, 10 decode-layer steps")
 
 
+def bench_checkpoint(torch):
+    """Checkpoint load rate: one config-3 layer (288 routed experts, 2-bit, 1.82 GB) written as two
+    safetensors shards to a temporary directory, then validated and loaded into one HBM slab
+    (helios_glm53flash_amd.checkpoint).  The file was just written, so it sits in the page cache:
+    the rate is host memory -> pinned staging -> HBM plus validation, not disk."""
+    import tempfile
+    import time
+
+    from safetensors.numpy import save_file
+
+    from helios_glm53flash_amd import checkpoint as ck
+    E, hidden, inter, bits = 288, 4096, 2048, 2
+    r = np.random.default_rng(5)
+    blk = r.integers(-32768, 32768, size=hidden * inter * bits // 16 + 4096, dtype=np.int16)
+    sgn = r.choice([-1.0, 1.0], hidden).astype(np.float16)
+    mul = np.array(0x83DCD12D - (1 << 32), dtype=np.int32)
+    with tempfile.TemporaryDirectory() as d:
+        for part in range(2):
+            tensors = {}
+            for e in range(part * E // 2, (part + 1) * E // 2):
+                for p, (pn, (K, N)) in enumerate(zip(ck.PROJ_NAMES, ((hidden, inter), (hidden, inter),
+                                                                      (inter, hidden)))):
+                    base = f"model.language_model.layers.0.mlp.experts.{e}.{pn}"
+                    o = (e * 3 + p) % 4096
+                    tensors[base + ".trellis"] = blk[o:o + K * N * bits // 16].reshape(K // 16, N // 16, 16 * bits)
+                    tensors[base + ".suh"] = sgn[:K]
+                    tensors[base + ".svh"] = sgn[:N]
+                    tensors[base + ".mul1"] = mul
+            save_file(tensors, f"{d}/model-{part:05d}-of-00002.safetensors")
+            del tensors
+        t0 = time.perf_counter()
+        ss = ck.ShardSet(d)
+        ex = ck.load_experts(ss, 0, E, hidden, inter)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        nbytes = sum(t.numel() * t.element_size() for p in range(3) for arr in (ex.trellis[p], ex.suh[p], ex.svh[p])
+                     for t in arr)
+        del ex
+    return {"workload": "checkpoint load: 288 experts x (gate, up, down) 2-bit, 2 shards, page-cache resident",
+            "bytes": nbytes, "seconds": round(dt, 3), "gbs": round(nbytes / dt / 1e9, 2)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -340,6 +382,7 @@ def main():
     pre = None if args.skip_prefill else bench_prefill(args, torch, moe)
     lin = None if args.skip_extra else bench_linears(torch, moe, exl3)
     sweep = None if args.skip_extra else bench_sweep(torch, moe)
+    ckpt = None if args.skip_extra else bench_checkpoint(torch)
     cpu = None if args.skip_cpu else cpu_baseline(dec["layers"], args.cpu_budget)
 
     out = {
@@ -383,6 +426,7 @@ def main():
                              "host call per step" % dec["graph_steps"],
             "linears": lin,
             "sweep_42_layers": sweep,
+            "checkpoint_load": ckpt,
             "prefill": None if pre is None else {
                 "workload": "moe_prefill: 4096 tokens, top-8 of 288 with Zipf(1.1) popularity, experts 0-143 "
                             "2-bit / 144-287 3-bit, hidden 4096, intermediate 2048 (BASELINE config 4), routed "

@@ -1,0 +1,157 @@
+"""Checkpoint loader: safetensors shards -> expert slab / GroupWords (names, shapes, dtypes, mul1 checks
+of src/core/expert_layout.cpp:6-55 and model.cpp:74-90), bit-exact placement, and a layer loaded from
+a file against the CPU oracle."""
+import numpy as np
+import pytest
+
+from helpers import assert_close
+
+safetensors_numpy = pytest.importorskip("safetensors.numpy")
+
+MUL1_I32 = np.int32(0x83DCD12D - (1 << 32))
+PREFIX = "model.language_model.layers"
+
+
+def _linear(r, K, N, bits):
+    tr = r.integers(-32768, 32768, size=(K // 16, N // 16, 16 * bits), dtype=np.int16)
+    suh = r.choice([-1.0, 1.0], K).astype(np.float16)
+    svh = (r.choice([-1.0, 1.0], N) * r.uniform(0.5, 1.5, N)).astype(np.float16)
+    return tr, suh, svh
+
+
+def make_checkpoint(path, E=3, hidden=256, inter=128, bits=((2, 2, 2), (3, 2, 4), (2, 3, 2)), shared=(2, 2, 2),
+                    layer=0, seed=0, shards=2):
+    """A synthetic checkpoint of one MoE layer (routed experts + shared expert) split over shards;
+    returns the arrays written, keyed by tensor name."""
+    r = np.random.default_rng(seed)
+    tensors = {}
+    shapes = [(hidden, inter), (hidden, inter), (inter, hidden)]
+    groups = [(f"{PREFIX}.{layer}.mlp.experts.{e}", bits[e]) for e in range(E)]
+    if shared:
+        groups.append((f"{PREFIX}.{layer}.mlp.shared_experts", shared))
+    for base, bb in groups:
+        for pn, (K, N), b in zip(("gate_proj", "up_proj", "down_proj"), shapes, bb):
+            tr, suh, svh = _linear(r, K, N, b)
+            tensors[f"{base}.{pn}.trellis"] = tr
+            tensors[f"{base}.{pn}.suh"] = suh
+            tensors[f"{base}.{pn}.svh"] = svh
+            tensors[f"{base}.{pn}.mul1"] = np.array(MUL1_I32, dtype=np.int32)
+    names = sorted(tensors)
+    for s in range(shards):
+        part = {n: tensors[n] for n in names[s::shards]}
+        safetensors_numpy.save_file(part, str(path / f"model-{s:05d}-of-{shards:05d}.safetensors"))
+    return tensors
+
+
+def test_shardset_reads_every_tensor(tmp_path):
+    from helios_glm53flash_amd import checkpoint as ck
+    tensors = make_checkpoint(tmp_path)
+    ss = ck.ShardSet(tmp_path)
+    assert len(ss.paths) == 2 and set(ss.tensors) == set(tensors)
+    for name, arr in tensors.items():
+        got = ss.read(ss.find(name))
+        assert got.dtype == arr.dtype and got.shape == arr.shape and np.array_equal(got, arr), name
+    assert ss.find("nope") is None
+
+
+def test_expert_slab_layout_and_bytes(tmp_path):
+    from helios_glm53flash_amd import checkpoint as ck
+    tensors = make_checkpoint(tmp_path)
+    ss = ck.ShardSet(tmp_path)
+    lay, _ = ck.expert_layout(ss, 0, 3, 256, 128)
+    starts = [o for e in lay.off for p in e for o in p]
+    assert all(o % ck.PIECE_ALIGN == 0 for o in starts) and len(set(starts)) == len(starts)
+    assert lay.bits == [[2, 2, 2], [3, 2, 4], [2, 3, 2]]
+    ex = ck.load_experts(ss, 0, 3, 256, 128, device="cpu")
+    assert ex.bits == [[2, 3, 2], [2, 2, 3], [2, 4, 2]]  # [projection][expert]
+    for e in range(3):
+        for p, pn in enumerate(("gate_proj", "up_proj", "down_proj")):
+            base = f"{PREFIX}.0.mlp.experts.{e}.{pn}"
+            assert np.array_equal(ex.trellis[p][e].numpy(), tensors[base + ".trellis"])
+            assert np.array_equal(ex.suh[p][e].numpy(), tensors[base + ".suh"])
+            assert np.array_equal(ex.svh[p][e].numpy(), tensors[base + ".svh"])
+    sh = ck.load_shared_mlp(ss, 0, 256, 128, device="cpu")
+    assert [g.bits for g in sh] == [2, 2, 2] and sh[0].mul1 == 0x83DCD12D
+    assert ck.load_shared_mlp(ss, 1, 256, 128, device="cpu") is None
+
+
+@pytest.mark.parametrize("defect", ["missing", "mul1", "shape", "dtype", "suh_len"])
+def test_expert_validation_names_the_tensor(tmp_path, defect):
+    from helios_glm53flash_amd import checkpoint as ck
+    tensors = make_checkpoint(tmp_path, shards=1)
+    bad = f"{PREFIX}.0.mlp.experts.1.up_proj"
+    if defect == "missing":
+        del tensors[bad + ".svh"]
+    elif defect == "mul1":
+        tensors[bad + ".mul1"] = np.array(12345, dtype=np.int32)
+    elif defect == "shape":
+        tensors[bad + ".trellis"] = tensors[bad + ".trellis"][:, :4].copy()
+    elif defect == "dtype":
+        tensors[bad + ".suh"] = tensors[bad + ".suh"].astype(np.float32)
+    else:
+        tensors[bad + ".suh"] = tensors[bad + ".suh"][:128].copy()
+    for f in tmp_path.glob("*.safetensors"):
+        f.unlink()
+    safetensors_numpy.save_file(tensors, str(tmp_path / "model.safetensors"))
+    ss = ck.ShardSet(tmp_path)
+    with pytest.raises(ck.CheckpointError, match="experts.1.up_proj"):
+        ck.expert_layout(ss, 0, 3, 256, 128)
+
+
+def test_truncated_shard_is_rejected(tmp_path):
+    from helios_glm53flash_amd import checkpoint as ck
+    make_checkpoint(tmp_path, shards=1)
+    f = next(tmp_path.glob("*.safetensors"))
+    data = f.read_bytes()
+    f.write_bytes(data[:-100])
+    with pytest.raises(ck.CheckpointError):
+        ck.ShardSet(tmp_path)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [1, 24])
+def test_layer_from_checkpoint_matches_oracle(tmp_path, T):
+    """Routed + shared experts loaded from safetensors into HBM; decode (T=1) and prefill (T=24) layer
+    outputs against the oracle on the arrays that were written."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from helios_glm53flash_amd import checkpoint as ck, moe
+    from oracle import oracle as O
+    E, hidden, inter, topk = 6, 256, 128, 2
+    bits = [(2, 2, 2), (3, 2, 4), (2, 3, 2), (2, 2, 2), (4, 4, 3), (2, 2, 2)]
+    tensors = make_checkpoint(tmp_path, E=E, hidden=hidden, inter=inter, bits=bits, seed=7)
+    ss = ck.ShardSet(tmp_path)
+    ex = ck.load_experts(ss, 0, E, hidden, inter)
+    sh = ck.load_shared_mlp(ss, 0, hidden, inter)
+    layer = moe.MoeLayer(ex, sh, topk=topk)
+    r = np.random.default_rng(T)
+    x = r.standard_normal((T, hidden)).astype(np.float16)
+    scores = r.standard_normal((T, E)).astype(np.float16)
+    y_routed = torch.empty((T, hidden), dtype=torch.float32, device="cuda")
+    y = layer(torch.from_numpy(x).cuda(), torch.from_numpy(scores).cuda(), y_routed=y_routed)
+    torch.cuda.synchronize()
+
+    def g(base, p):
+        pn = ("gate_proj", "up_proj", "down_proj")[p]
+        return [tensors[f"{base}.{pn}.{s}"] for s in ("trellis", "suh", "svh")]
+
+    exp = {"trellis": [], "suh": [], "svh": [], "bits": []}
+    for p in range(3):
+        gs = [g(f"{PREFIX}.0.mlp.experts.{e}", p) for e in range(E)]
+        exp["trellis"].append([a[0].view(np.uint16) for a in gs])
+        exp["suh"].append([a[1].view(np.uint16) for a in gs])
+        exp["svh"].append([a[2].view(np.uint16) for a in gs])
+        exp["bits"].append(np.array([b[p] for b in bits], np.int32))
+    shd = {"trellis": [], "suh": [], "svh": [], "bits": []}
+    for p in range(3):
+        a = g(f"{PREFIX}.0.mlp.shared_experts", p)
+        shd["trellis"].append(a[0].view(np.uint16))
+        shd["suh"].append(a[1].view(np.uint16))
+        shd["svh"].append(a[2].view(np.uint16))
+        shd["bits"].append(a[0].shape[2] // 16)
+    idx, w = O.routing(scores, topk, 2.5)
+    rows = np.arange(T)
+    yr_ref, yo_ref = O.moe_rows(x, hidden, inter, idx, w, rows, exp, shd, 10.0)
+    assert_close(y_routed.cpu().numpy(), yr_ref, what=f"routed from checkpoint T={T}")
+    assert_close(y.float().cpu().numpy(), yo_ref.view(np.float16).astype(np.float64), what=f"y from checkpoint T={T}")
