@@ -144,14 +144,17 @@ def bench_prefill(args, torch, moe):
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops}
 
 
-def graph_time_us(torch, fn, reps: int = 20) -> float:
-    """Average microseconds of fn() replayed from a HIP graph (fn must be capture-safe)."""
+def graph_time_us(torch, fn, reps: int = 20, inner: int = 20) -> float:
+    """Average microseconds of one fn() call: `inner` calls captured back to back in one HIP graph,
+    replayed `reps` times (one call per graph would add the replay's own launch cost, tens of us, to
+    every µs-scale kernel).  fn must be capture-safe."""
     fn()
     torch.cuda.synchronize()
     stream = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
-        fn()
+        for _ in range(inner):
+            fn()
     graph.replay()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -160,7 +163,7 @@ def graph_time_us(torch, fn, reps: int = 20) -> float:
         graph.replay()
     b.record()
     torch.cuda.synchronize()
-    return a.elapsed_time(b) / reps * 1e3
+    return a.elapsed_time(b) / (reps * inner) * 1e3
 
 
 def bench_linears(torch, moe, exl3):
@@ -209,7 +212,7 @@ def bench_sweep(torch, moe, layers_n: int = 42):
     def run():
         for i in range(layers_n):
             layers[i](x, scores[i], y=ys[i], ws=ws)
-    us = graph_time_us(torch, run, reps=10)
+    us = graph_time_us(torch, run, reps=10, inner=2)
     step_bytes = layers_n * 8 * layers[0].experts.weight_bytes([0])
     del layers
     return {"layers": layers_n, "us_per_step": round(us, 1), "us_per_layer": round(us / layers_n, 2),
@@ -308,6 +311,24 @@ def profile_only(torch, moe):
     print("profile workload done: copy 256 MiB x3, 10 decode-layer steps")
 
 
+def bench_router(torch):
+    """Router logits (gemm_nt_f16, glue2.cu:9-65): fp16 scores [M][288] = x [M][4096] . W^T, W the
+    router gate [288][4096] fp16 (2.36 MB); M = 1 (decode, HIP graph) and M = 4096 (prefill)."""
+    from helios_glm53flash_amd import exl3
+    E, H = 288, 4096
+    r = np.random.default_rng(9)
+    w = torch.from_numpy((r.standard_normal((E, H)) * 0.02).astype(np.float16)).cuda()
+    out = {}
+    for M in (1, 4096):
+        x = torch.from_numpy(r.standard_normal((M, H)).astype(np.float16)).cuda()
+        y = torch.empty((M, E), dtype=torch.float16, device="cuda")
+        us = graph_time_us(torch, lambda: exl3.gemm_nt_f16(y, x, w, M, E, H))
+        flops = 2.0 * M * E * H
+        out[f"M{M}"] = {"us": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 2),
+                        "weight_gbs": round(E * H * 2 / (us * 1e-6) / 1e9, 1)}
+    return out
+
+
 def bench_checkpoint(torch):
     """Checkpoint load rate: one config-3 layer (288 routed experts, 2-bit, 1.82 GB) written as two
     safetensors shards to a temporary directory, then validated and loaded into one HBM slab
@@ -383,6 +404,7 @@ def main():
     lin = None if args.skip_extra else bench_linears(torch, moe, exl3)
     sweep = None if args.skip_extra else bench_sweep(torch, moe)
     ckpt = None if args.skip_extra else bench_checkpoint(torch)
+    router = None if args.skip_extra else bench_router(torch)
     cpu = None if args.skip_cpu else cpu_baseline(dec["layers"], args.cpu_budget)
 
     out = {
@@ -427,6 +449,7 @@ def main():
             "linears": lin,
             "sweep_42_layers": sweep,
             "checkpoint_load": ckpt,
+            "router_logits": router,
             "prefill": None if pre is None else {
                 "workload": "moe_prefill: 4096 tokens, top-8 of 288 with Zipf(1.1) popularity, experts 0-143 "
                             "2-bit / 144-287 3-bit, hidden 4096, intermediate 2048 (BASELINE config 4), routed "

@@ -218,3 +218,40 @@ def load_shared_mlp(shards: ShardSet, layer: int, hidden: int, inter: int, devic
         return None
     return [load_group(shards, f"{base}.{pn}", K, N, device)
             for pn, (K, N) in zip(PROJ_NAMES, ((hidden, inter), (hidden, inter), (inter, hidden)))]
+
+
+def _to_f16(shards: ShardSet, t: TensorInfo) -> np.ndarray:
+    a = shards.read(t)
+    if t.dtype == "F16":
+        return a
+    if t.dtype == "BF16":  # bf16 bits -> fp32 (exact) -> fp16 (round to nearest even)
+        return (a.astype(np.uint32) << 16).view(np.float32).astype(np.float16)
+    if t.dtype in ("F32", "F64"):
+        return a.astype(np.float16)
+    raise CheckpointError(f"{t.name}: expected a floating-point tensor, got {t.dtype}")
+
+
+def load_router(shards: ShardSet, layer: int, experts: int, hidden: int, device="cuda",
+                prefix: str = "model.language_model.layers") -> tuple:
+    """Router gate fp16 [E][hidden] and score-correction bias (model.cpp:185-196), or (None, None).
+
+    The bias is stored centred, as the reference's loader does (model.cpp:524-535): read as fp32, minus
+    its mean (fp64 sum, rounded to fp32), then rounded to fp16; top-k selection is unchanged by the
+    shift and the fp16 values keep more precision."""
+    base = f"{prefix}.{layer}.mlp.gate"
+    tw = shards.find(base + ".weight")
+    if tw is None:
+        return None, None
+    if tw.shape != (experts, hidden):
+        raise CheckpointError(f"invalid router gate shape {tw.shape}: {base}.weight")
+    w = torch.from_numpy(_to_f16(shards, tw).copy()).to(device)
+    tb = shards.find(base + ".e_score_correction_bias")
+    if tb is None:
+        return w, None
+    if tb.shape != (experts,):
+        raise CheckpointError(f"invalid router bias shape {tb.shape}: {base}.e_score_correction_bias")
+    f = shards.read(tb).astype(np.float32) if tb.dtype != "BF16" else \
+        (shards.read(tb).astype(np.uint32) << 16).view(np.float32)
+    mean = np.float32(f.astype(np.float64).sum() / f.size)
+    b = (f - mean).astype(np.float16)
+    return w, torch.from_numpy(b).to(device)

@@ -230,6 +230,15 @@ int hx_swiglu_clamp(const float* gate, const float* up, void* out, size_t n, flo
                       "hx_swiglu_clamp");
 }
 
+int hx_gemm_nt_f16(void* y, const void* x, const void* w, int M, int N, int K, int y_fp32, int add,
+                   hx_stream_t stream)
+{
+    if (!y || !x || !w || M < 0 || N < 0 || K <= 0 || K % 32)
+        return fail(HX_ERR_INVALID, "hx_gemm_nt_f16: bad arguments (K must be a positive multiple of 32)");
+    return hip_status(hx::launch_gemm_nt_f16(static_cast<const _Float16*>(x), static_cast<const _Float16*>(w), y, M,
+                                             N, K, y_fp32 != 0, add != 0, (hipStream_t)stream),
+                      "hx_gemm_nt_f16");
+}
 
 // ------------------------------------------------------------------ MoE
 

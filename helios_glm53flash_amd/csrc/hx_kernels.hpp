@@ -43,5 +43,7 @@ hipError_t launch_permute_chunked(const int64_t* ids, const _Float16* w, int M, 
 hipError_t launch_reduce_sorted(float* y, const float* contrib, const int64_t* route_to_sorted, int M, int topk,
                                 int hidden, hipStream_t st);
 hipError_t launch_swiglu_clamp(const float* g, const float* u, _Float16* out, size_t n, float limit, hipStream_t st);
+hipError_t launch_gemm_nt_f16(const _Float16* x, const _Float16* w, void* y, int M, int N, int K, bool y_fp32,
+                              bool add, hipStream_t st);
 
 }  // namespace hx

@@ -182,6 +182,17 @@ def swiglu_clamp(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor, n: int
           "hx_swiglu_clamp")
 
 
-__all__ = ["GroupWords", "gemm", "gemv", "reconstruct", "reconstruct_slice", "had_r_128", "routing_ds3_nogroup",
+def gemm_nt_f16(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor, M: int, N: int, K: int, y_fp32: bool = False,
+                add: bool = False, stream=None) -> None:
+    """y[m][n] = sum_k x[m][k] * w[n][k] (glue2.cu:9-65,165-182): the MoE router logits with w the
+    router gate [E][hidden]; fp16 y rounded once from the fp32 sum, or fp32 y (added to when add)."""
+    _need(x, "x", (torch.float16,))
+    _need(w, "w", (torch.float16,))
+    _need(y, "y", (torch.float32,) if y_fp32 else (torch.float16,))
+    check(lib.hx_gemm_nt_f16(y.data_ptr(), x.data_ptr(), w.data_ptr(), M, N, K, int(y_fp32), int(add),
+                             _stream(stream)), "hx_gemm_nt_f16")
+
+
+__all__ = ["GroupWords", "gemm", "gemm_nt_f16", "gemv", "reconstruct", "reconstruct_slice", "had_r_128", "routing_ds3_nogroup",
            "moe_permute", "moe_reduce_sorted", "swiglu_clamp", "workspace", "MUL1", "HxError",
            "HX_GEMM_PATH_GEMV", "HX_GEMM_PATH_MFMA"]

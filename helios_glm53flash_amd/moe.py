@@ -11,7 +11,7 @@ from typing import Optional, Sequence
 import torch
 
 from ._lib import ExpertTablesC, GroupWordsC, check, lib
-from .exl3 import MUL1, GroupWords, _need, _ptr, _stream, workspace
+from .exl3 import MUL1, GroupWords, _need, _ptr, _stream, gemm_nt_f16, workspace
 
 PROJ = ("gate", "up", "down")
 
@@ -142,7 +142,10 @@ class MoeLayer:
     """One MoE FFN layer (routed experts + optional shared expert), resident in HBM."""
 
     def __init__(self, experts: ExpertSet, shared: Optional[list] = None, topk: int = 8,
-                 routed_scale: float = 2.5, act_limit: float = 10.0):
+                 routed_scale: float = 2.5, act_limit: float = 10.0, router_weight: Optional[torch.Tensor] = None):
+        """router_weight: optional router gate fp16 [E][hidden]; with it the layer may be called with
+        scores=None and computes the logits itself (gemm_nt_f16, stream-ordered, no host sync)."""
+        self.router_weight = router_weight
         self.experts = experts
         self.shared = shared
         self.topk = topk
@@ -157,13 +160,18 @@ class MoeLayer:
     def workspace_bytes(self, tokens: int) -> int:
         return moe_workspace_bytes(tokens, self.experts.hidden, self.experts.inter, self.experts.num_experts, self.topk)
 
-    def __call__(self, x: torch.Tensor, scores: torch.Tensor, y: Optional[torch.Tensor] = None,
+    def __call__(self, x: torch.Tensor, scores: Optional[torch.Tensor] = None, y: Optional[torch.Tensor] = None,
                  y_routed: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None, stream=None,
                  ws: Optional[torch.Tensor] = None) -> torch.Tensor:
         _need(x, "x", (torch.float16,))
-        _need(scores, "scores", (torch.float16,))
         T = x.shape[0]
         ex = self.experts
+        if scores is None:
+            if self.router_weight is None:
+                raise ValueError("MoeLayer: scores=None needs router_weight")
+            scores = torch.empty((T, ex.num_experts), dtype=torch.float16, device=x.device)
+            gemm_nt_f16(scores, x, self.router_weight, T, ex.num_experts, ex.hidden, stream=stream)
+        _need(scores, "scores", (torch.float16,))
         if y is None:
             y = torch.empty((T, ex.hidden), dtype=torch.float16, device=x.device)
         if ws is None:

@@ -132,6 +132,13 @@ int hx_moe_reduce_sorted(float* y, const float* contributions, const int64_t* ro
  * Replaces helios::glue::swiglu_clamp (src/engine/glue2.cuh:64, glue2.cu:406-414). */
 int hx_swiglu_clamp(const float* gate, const float* up, void* out, size_t n, float limit, hx_stream_t stream);
 
+/* Dense fp16 NT GEMM y[m][n] = sum_k x[m][k] * w[n][k] (x [M][K], w [N][K] row-major, fp32
+ * accumulate): fp16 output rounded once (y_fp32 = 0) or fp32 output, added to y when add != 0.  The
+ * MoE router logits (w = the router gate [E][hidden]) are its main use.  K % 32 == 0.
+ * Replaces helios::glue::gemm_nt_f16 (src/engine/glue2.cuh:9-10, glue2.cu:9-65,165-182). */
+int hx_gemm_nt_f16(void* y, const void* x, const void* w, int M, int N, int K, int y_fp32, int add,
+                   hx_stream_t stream);
+
 /* ---- MoE layer ---------------------------------------------------------------------------- */
 
 /* Workspace bytes for hx_moe_grouped / hx_moe_layer with these extents. */

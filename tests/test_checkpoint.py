@@ -155,3 +155,29 @@ def test_layer_from_checkpoint_matches_oracle(tmp_path, T):
     yr_ref, yo_ref = O.moe_rows(x, hidden, inter, idx, w, rows, exp, shd, 10.0)
     assert_close(y_routed.cpu().numpy(), yr_ref, what=f"routed from checkpoint T={T}")
     assert_close(y.float().cpu().numpy(), yo_ref.view(np.float16).astype(np.float64), what=f"y from checkpoint T={T}")
+
+
+def test_router_bias_is_centred_and_gate_converted(tmp_path):
+    """model.cpp:185-196,524-535: gate weight to fp16; bias fp32 minus its mean (fp64 sum), to fp16."""
+    from helios_glm53flash_amd import checkpoint as ck
+    r = np.random.default_rng(3)
+    E, H = 12, 64
+    gate = r.standard_normal((E, H)).astype(np.float32)
+    bias = (r.standard_normal(E) * 3 + 7).astype(np.float32)
+    bf16 = (gate.view(np.uint32) >> 16).astype(np.uint16)  # truncated bf16 bits of the gate
+    safetensors_numpy.save_file({f"{PREFIX}.2.mlp.gate.weight": gate,
+                                 f"{PREFIX}.2.mlp.gate.e_score_correction_bias": bias}, str(tmp_path / "a.safetensors"))
+    w, b = ck.load_router(ck.ShardSet(tmp_path), 2, E, H, device="cpu")
+    assert np.array_equal(w.numpy(), gate.astype(np.float16))
+    mean = np.float32(bias.astype(np.float64).sum() / E)
+    assert np.array_equal(b.numpy(), (bias - mean).astype(np.float16))
+    assert abs(float(b.float().mean())) < 1e-2
+    (tmp_path / "a.safetensors").unlink()
+    import json, struct
+    hdr = json.dumps({f"{PREFIX}.2.mlp.gate.weight": {"dtype": "BF16", "shape": [E, H],
+                                                      "data_offsets": [0, E * H * 2]}}).encode()
+    (tmp_path / "b.safetensors").write_bytes(struct.pack("<Q", len(hdr)) + hdr + bf16.tobytes())
+    w, b = ck.load_router(ck.ShardSet(tmp_path), 2, E, H, device="cpu")
+    assert b is None
+    assert np.array_equal(w.numpy(), (bf16.astype(np.uint32) << 16).view(np.float32).astype(np.float16))
+    assert ck.load_router(ck.ShardSet(tmp_path), 3, E, H, device="cpu") == (None, None)
