@@ -218,6 +218,13 @@ inline void swiglu_clamp(const float* gate, const float* up, void* out, size_t n
 {
     exl3::check(hx_swiglu_clamp(gate, up, out, n, limit, (hx_stream_t)s), "helios::glue::swiglu_clamp");
 }
+// reference: src/engine/glue2.cuh:9-10 (router logits and other dense fp16 NT products)
+inline void gemm_nt_f16(void* y, const void* x, const void* w, int M, int N, int K, bool y_fp32, bool add,
+                        Stream s = 0)
+{
+    exl3::check(hx_gemm_nt_f16(y, x, w, M, N, K, y_fp32 ? 1 : 0, add ? 1 : 0, (hx_stream_t)s),
+                "helios::glue::gemm_nt_f16");
+}
 }  // namespace glue
 
 }  // namespace helios
