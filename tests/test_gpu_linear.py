@@ -104,3 +104,35 @@ def test_config1_single_linear(hx):
     """K=4096, N=2048, 2-bit, M=1 vs fp64 decode+matmul."""
     _, got, ref = _run_linear(hx, 1, 4096, 2048, 2, 2, True, seed=1)
     assert_close(got, ref, what="config 1")
+
+
+@pytest.mark.parametrize("M", [1, 64])
+def test_dense_3bit_real_shape(hx, M):
+    """3-bit dense linear at a projection's real shape (K=4096 -> N=12288), GEMV and MFMA paths."""
+    path, got, ref = _run_linear(hx, M, 4096, 12288, 3, 2, True, seed=300 + M)
+    assert path == (hx.HX_GEMM_PATH_GEMV if M <= 16 else hx.HX_GEMM_PATH_MFMA)
+    assert_close(got, ref, what=f"3-bit 4096x12288 M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 512])
+def test_lm_head_6bit_sampled_columns(hx, M):
+    """6-bit lm_head at its real shape (K=4096 -> N=151552), GEMV (M=1) and MFMA (M=512) paths; the
+    oracle checks sampled 128-column groups (each group's output transform is independent of the
+    others, so a tile-column slice of the weight is an exact sub-problem)."""
+    import torch
+    from oracle import oracle as O
+    K, N, bits = 4096, 151552, 6
+    tr, suh, svh = make_linear(600 + M, K, N, bits)
+    x = make_x(601 + M, M, K)
+    w = hx.GroupWords(_dev(tr, torch.int16), _dev(suh), _dev(svh), hx.MUL1)
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    a_had = torch.empty((M, K), dtype=torch.float16, device="cuda") if M > hx.GEMV_MAX_M else None
+    hx.gemm(y, _dev(x), w, M, N, K, bits, True, a_had=a_had)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    rows = np.arange(M) if M <= 16 else np.array([0, 1, 255, 256, 511])
+    for g in (0, 517, N // 128 - 1):
+        sl = slice(128 * g, 128 * g + 128)
+        sub = np.ascontiguousarray(tr[:, 8 * g:8 * g + 8, :])
+        ref = O.linear(x[rows], sub, suh, np.ascontiguousarray(svh[sl]), K, 128, bits, 2, out_f16=False)
+        assert_close(got[rows, sl], ref, what=f"lm_head 6-bit M={M} group {g}")
