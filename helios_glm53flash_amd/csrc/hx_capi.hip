@@ -177,6 +177,40 @@ int hx_exl3_reconstruct_slice(void* unpacked, const void* packed, int packed_row
                       "hx_exl3_reconstruct_slice");
 }
 
+int hx_exl3_reconstruct_had_slice(void* unpacked, const void* packed, const void* suh, const void* svh,
+                                  int packed_rows, int packed_cols, int unpacked_rows, int unpacked_cols, int bits,
+                                  int mcg, int mul1, int64_t n_offset, hx_stream_t stream)
+{
+    if (!unpacked || !packed || !suh || !svh) return fail(HX_ERR_INVALID, "hx_exl3_reconstruct_had_slice: null pointer");
+    if (bits < 1 || bits > 8) return fail(HX_ERR_INVALID, "hx_exl3_reconstruct_had_slice: bits must be in [1, 8]");
+    if (unpacked_rows % 128 || unpacked_cols % 128 || n_offset % 128 || n_offset < 0 || unpacked_rows < 0 ||
+        unpacked_cols < 0 || n_offset + unpacked_cols > (int64_t)packed_cols * 16 || unpacked_rows > packed_rows * 16)
+        return fail(HX_ERR_INVALID, "hx_exl3_reconstruct_had_slice: dimensions must be 128-aligned and inside the tensor");
+    return hip_status(hx::launch_reconstruct_had(static_cast<_Float16*>(unpacked), static_cast<const uint16_t*>(packed),
+                                                 static_cast<const _Float16*>(suh), static_cast<const _Float16*>(svh),
+                                                 packed_rows, packed_cols, unpacked_rows, unpacked_cols, bits,
+                                                 codebook(mcg, mul1), (long)n_offset, (hipStream_t)stream),
+                      "hx_exl3_reconstruct_had_slice");
+}
+
+int hx_exl3_pack_trellis(void* packed, const void* unpacked, int rows, int cols, int K, hx_stream_t stream)
+{
+    if (!packed || !unpacked || rows < 0 || cols < 0 || K < 1 || K > 8)
+        return fail(HX_ERR_INVALID, "hx_exl3_pack_trellis: bad arguments");
+    return hip_status(hx::launch_pack_trellis(static_cast<uint16_t*>(packed), static_cast<const uint16_t*>(unpacked),
+                                              (long)rows * cols, K, (hipStream_t)stream),
+                      "hx_exl3_pack_trellis");
+}
+
+int hx_exl3_unpack_trellis(void* unpacked, const void* packed, int rows, int cols, int K, hx_stream_t stream)
+{
+    if (!packed || !unpacked || rows < 0 || cols < 0 || K < 1 || K > 8)
+        return fail(HX_ERR_INVALID, "hx_exl3_unpack_trellis: bad arguments");
+    return hip_status(hx::launch_unpack_trellis(static_cast<uint16_t*>(unpacked), static_cast<const uint16_t*>(packed),
+                                                (long)rows * cols, K, (hipStream_t)stream),
+                      "hx_exl3_unpack_trellis");
+}
+
 int hx_had_r_128(const void* input, void* output, const void* pre_scale, const void* post_scale, int64_t rows,
                  int cols, float r_scale, hx_stream_t stream)
 {

@@ -184,6 +184,20 @@ HX_INLINE int hx_kn_to_pos(int k, int n)
     return 8 * l + j;
 }
 
+// Window p (16 stream bits ending at stream bit (p+1)*bits, cyclic over the tile) of a tile held as
+// 8*bits uint32 words, with a run-time bit width (reconstruct paths).
+HX_INLINE uint32_t window_rt(const uint32_t* w, int bits, int p)
+{
+    const int total = 256 * bits, nw = 8 * bits;
+    int s = (p + 1) * bits - 16;
+    if (s < 0) s += total;
+    const int wi = s >> 5, off = s & 31;
+    if (off <= 16) return (w[wi] >> (16 - off)) & 0xffffu;
+    int wj = wi + 1;
+    if (wj == nw) wj = 0;
+    return __builtin_amdgcn_alignbit(w[wi], w[wj], 48 - off) & 0xffffu;
+}
+
 // ------------------------------------------------------------------ wave-level Hadamard-128
 
 // 128-point Sylvester transform of one vector held as 2 values per lane (elements 2*lane,

@@ -43,6 +43,11 @@ hipError_t launch_permute_chunked(const int64_t* ids, const _Float16* w, int M, 
 hipError_t launch_reduce_sorted(float* y, const float* contrib, const int64_t* route_to_sorted, int M, int topk,
                                 int hidden, hipStream_t st);
 hipError_t launch_swiglu_clamp(const float* g, const float* u, _Float16* out, size_t n, float limit, hipStream_t st);
+hipError_t launch_pack_trellis(uint16_t* packed, const uint16_t* unpacked, long blocks, int K, hipStream_t st);
+hipError_t launch_unpack_trellis(uint16_t* unpacked, const uint16_t* packed, long blocks, int K, hipStream_t st);
+hipError_t launch_reconstruct_had(_Float16* out, const uint16_t* packed, const _Float16* suh, const _Float16* svh,
+                                  int packed_rows, int packed_cols, int unpacked_rows, int unpacked_cols, int bits,
+                                  int cb, long n_offset, hipStream_t st);
 hipError_t launch_gemm_nt_f16(const _Float16* x, const _Float16* w, void* y, int M, int N, int K, bool y_fp32,
                               bool add, hipStream_t st);
 

@@ -7,18 +7,6 @@ namespace hx {
 
 // ------------------------------------------------------------------ reconstruct
 
-HX_INLINE uint32_t window_rt(const uint32_t* w, int bits, int p)
-{
-    const int total = 256 * bits, nw = 8 * bits;
-    int s = (p + 1) * bits - 16;
-    if (s < 0) s += total;
-    const int wi = s >> 5, off = s & 31;
-    if (off <= 16) return (w[wi] >> (16 - off)) & 0xffffu;
-    int wj = wi + 1;
-    if (wj == nw) wj = 0;
-    return __builtin_amdgcn_alignbit(w[wi], w[wj], 48 - off) & 0xffffu;
-}
-
 // One workgroup per (tile row tk, 8 consecutive tile columns): thread t writes 8 consecutive
 // fp16 of row 16*tk + t/16.  Reference: reconstruct.cu:8-81 (same W_hat [K][N] row-major output).
 template <int CB>

@@ -130,6 +130,37 @@ def reconstruct(unpacked, packed, packed_rows, packed_cols, unpacked_cols, K, mc
     reconstruct_slice(unpacked, packed, packed_rows, packed_cols, unpacked_cols, K, mcg, mul1, 0, stream)
 
 
+def reconstruct_had_slice(unpacked: torch.Tensor, packed: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+                          packed_rows: int, packed_cols: int, unpacked_rows: int, unpacked_cols: int, K: int,
+                          mcg: bool, mul1: bool, n_offset: int, stream=None) -> None:
+    """Original-basis weights diag(suh) H W_hat H diag(svh) / 128 per 128 x 128 tile (reference
+    reconstruct_had_slice, reconstruct.cuh:37-63); svh already offset by n_offset."""
+    _need(unpacked, "unpacked", (torch.float16,))
+    _need(packed, "packed", (torch.int16, torch.uint16))
+    _need(suh, "suh", (torch.float16,))
+    _need(svh, "svh", (torch.float16,))
+    check(lib.hx_exl3_reconstruct_had_slice(unpacked.data_ptr(), packed.data_ptr(), suh.data_ptr(), svh.data_ptr(),
+                                            packed_rows, packed_cols, unpacked_rows, unpacked_cols, K, int(mcg),
+                                            int(bool(mul1)), n_offset, _stream(stream)),
+          "hx_exl3_reconstruct_had_slice")
+
+
+def pack_trellis(packed: torch.Tensor, unpacked: torch.Tensor, rows: int, cols: int, K: int, stream=None) -> None:
+    """rows*cols blocks of 256 K-bit symbols -> 16*K trellis words each (reference pack.cuh:9-20)."""
+    _need(packed, "packed", (torch.int16, torch.uint16))
+    _need(unpacked, "unpacked", (torch.int16, torch.uint16))
+    check(lib.hx_exl3_pack_trellis(packed.data_ptr(), unpacked.data_ptr(), rows, cols, K, _stream(stream)),
+          "hx_exl3_pack_trellis")
+
+
+def unpack_trellis(unpacked: torch.Tensor, packed: torch.Tensor, rows: int, cols: int, K: int, stream=None) -> None:
+    """Inverse of pack_trellis: symbols with the bits above K zero (reference pack.cuh:22-33)."""
+    _need(packed, "packed", (torch.int16, torch.uint16))
+    _need(unpacked, "unpacked", (torch.int16, torch.uint16))
+    check(lib.hx_exl3_unpack_trellis(unpacked.data_ptr(), packed.data_ptr(), rows, cols, K, _stream(stream)),
+          "hx_exl3_unpack_trellis")
+
+
 def had_r_128(input: torch.Tensor, output: torch.Tensor, pre_scale: Optional[torch.Tensor],
               post_scale: Optional[torch.Tensor], rows: int, cols: int, r_scale: float = 0.088388347648,
               stream=None) -> None:
@@ -193,6 +224,6 @@ def gemm_nt_f16(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor, M: int, N: in
                              _stream(stream)), "hx_gemm_nt_f16")
 
 
-__all__ = ["GroupWords", "gemm", "gemm_nt_f16", "gemv", "reconstruct", "reconstruct_slice", "had_r_128", "routing_ds3_nogroup",
+__all__ = ["GroupWords", "gemm", "gemm_nt_f16", "reconstruct_had_slice", "pack_trellis", "unpack_trellis", "gemv", "reconstruct", "reconstruct_slice", "had_r_128", "routing_ds3_nogroup",
            "moe_permute", "moe_reduce_sorted", "swiglu_clamp", "workspace", "MUL1", "HxError",
            "HX_GEMM_PATH_GEMV", "HX_GEMM_PATH_MFMA"]

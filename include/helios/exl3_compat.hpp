@@ -131,6 +131,24 @@ inline void reconstruct(void* unpacked, const void* packed, int packed_rows, int
 {
     reconstruct_slice(unpacked, packed, packed_rows, packed_cols, unpacked_cols, K, mcg, mul1, 0, s);
 }
+// reference: src/cuda/quant/reconstruct.cuh:37-63
+inline void reconstruct_had_slice(void* unpacked, const void* packed, const void* suh, const void* svh, int packed_rows,
+                                  int packed_cols, int unpacked_rows, int unpacked_cols, int K, bool mcg, bool mul1,
+                                  int64_t n_offset, Stream s = 0)
+{
+    check(hx_exl3_reconstruct_had_slice(unpacked, packed, suh, svh, packed_rows, packed_cols, unpacked_rows,
+                                        unpacked_cols, K, mcg, mul1, n_offset, (hx_stream_t)s),
+          "helios::exl3::reconstruct_had_slice");
+}
+// reference: src/cuda/quant/pack.cuh:9-33
+inline void pack_trellis(void* packed, const void* unpacked, int rows, int cols, int K, Stream s = 0)
+{
+    check(hx_exl3_pack_trellis(packed, unpacked, rows, cols, K, (hx_stream_t)s), "helios::exl3::pack_trellis");
+}
+inline void unpack_trellis(void* unpacked, const void* packed, int rows, int cols, int K, Stream s = 0)
+{
+    check(hx_exl3_unpack_trellis(unpacked, packed, rows, cols, K, (hx_stream_t)s), "helios::exl3::unpack_trellis");
+}
 
 // reference: src/cuda/quant/exl3_moe.cuh:20-31
 struct ExpertTables {

@@ -100,6 +100,21 @@ int hx_exl3_gemm(void* y, const void* x, const hx_group_words* w, int M, int N, 
 int hx_exl3_reconstruct_slice(void* unpacked, const void* packed, int packed_rows, int packed_cols,
                               int unpacked_cols, int bits, int mcg, int mul1, int64_t n_offset, hx_stream_t stream);
 
+/* Original-basis weights W = diag(suh) . H128 . W_hat . H128 . diag(svh) / 128 per 128 x 128 tile,
+ * fp16 [unpacked_rows][unpacked_cols]; unpacked_rows, unpacked_cols and n_offset multiples of 128;
+ * suh holds >= unpacked_rows entries, svh >= unpacked_cols (already offset by n_offset).
+ * Replaces helios::exl3::reconstruct_had_slice (src/cuda/quant/reconstruct.cuh:37-63,
+ * reconstruct.cu:320-374). */
+int hx_exl3_reconstruct_had_slice(void* unpacked, const void* packed, const void* suh, const void* svh,
+                                  int packed_rows, int packed_cols, int unpacked_rows, int unpacked_cols, int bits,
+                                  int mcg, int mul1, int64_t n_offset, hx_stream_t stream);
+
+/* rows*cols blocks of 256 K-bit symbols (uint16 each, low K bits used) <-> 16*K uint16 trellis
+ * words per block.  Replace helios::exl3::pack_trellis / unpack_trellis (src/cuda/quant/pack.cuh:9-33,
+ * pack.cu:7-176); unpack writes symbols with the bits above K zero. */
+int hx_exl3_pack_trellis(void* packed, const void* unpacked, int rows, int cols, int K, hx_stream_t stream);
+int hx_exl3_unpack_trellis(void* unpacked, const void* packed, int rows, int cols, int K, hx_stream_t stream);
+
 /* Row-wise Hadamard-128 with optional fp16 pre/post scales, fp16 in/out.
  * Replaces helios::exl3::had_r_128 (src/cuda/quant/hadamard.cuh:14-43) for DType::Half. */
 int hx_had_r_128(const void* input, void* output, const void* pre_scale, const void* post_scale, int64_t rows,

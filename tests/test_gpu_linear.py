@@ -136,3 +136,53 @@ def test_lm_head_6bit_sampled_columns(hx, M):
         sub = np.ascontiguousarray(tr[:, 8 * g:8 * g + 8, :])
         ref = O.linear(x[rows], sub, suh, np.ascontiguousarray(svh[sl]), K, 128, bits, 2, out_f16=False)
         assert_close(got[rows, sl], ref, what=f"lm_head 6-bit M={M} group {g}")
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+def test_pack_unpack_trellis_bit_exact(hx, K):
+    """pack_trellis / unpack_trellis (pack.cu): GPU packing equals the oracle's packer for every block,
+    and unpacking returns the symbols (low K bits of the oracle's windows)."""
+    import torch
+    from oracle import oracle as O
+    rows, cols = 3, 5
+    r = np.random.default_rng(K)
+    sym = r.integers(0, 65536, size=(rows * cols, 256), dtype=np.uint16)  # bits above K are ignored
+    packed = torch.empty((rows * cols, 16 * K), dtype=torch.int16, device="cuda")
+    hx.pack_trellis(packed, _dev(sym, torch.int16), rows, cols, K)
+    back = torch.empty((rows * cols, 256), dtype=torch.int16, device="cuda")
+    hx.unpack_trellis(back, packed, rows, cols, K)
+    torch.cuda.synchronize()
+    got = packed.cpu().numpy().view(np.uint16)
+    mask = (1 << K) - 1
+    for b in range(rows * cols):
+        want = O.pack_tile(sym[b] & mask, K)
+        assert np.array_equal(got[b], want), b
+        assert np.array_equal(O.unpack_tile(want, K) & mask, sym[b] & mask)
+    assert np.array_equal(back.cpu().numpy().view(np.uint16), sym & mask)
+
+
+@pytest.mark.parametrize("bits,cb", [(2, 2), (3, 0), (4, 1), (6, 2)])
+def test_reconstruct_had_slice(hx, bits, cb):
+    """Original-basis weights diag(suh) H W_hat H diag(svh) / 128 per 128 x 128 tile against fp64 on the
+    bit-exact W_hat; a column slice with its pre-offset svh."""
+    import torch
+    from oracle import oracle as O
+    K, N = 256, 512
+    tr, suh, svh = make_linear(90 + bits, K, N, bits)
+    w_hat = O.reconstruct(tr, K, N, bits, cb).view(np.float16).astype(np.float64)
+    idx = np.arange(128)
+    H = np.where(np.array([[bin(i & j).count("1") & 1 for j in idx] for i in idx]) == 0, 1.0, -1.0)
+    ref = np.empty((K, N))
+    for a in range(0, K, 128):
+        for b in range(0, N, 128):
+            ref[a:a + 128, b:b + 128] = H @ w_hat[a:a + 128, b:b + 128] @ H / 128.0
+    ref *= suh.astype(np.float64)[:, None] * svh.astype(np.float64)[None, :]
+    out = torch.empty((K, N), dtype=torch.float16, device="cuda")
+    hx.reconstruct_had_slice(out, _dev(tr, torch.int16), _dev(suh), _dev(svh), K // 16, N // 16, K, N, bits,
+                             cb == 1, cb == 2, 0)
+    part = torch.empty((K, 256), dtype=torch.float16, device="cuda")
+    hx.reconstruct_had_slice(part, _dev(tr, torch.int16), _dev(suh), _dev(np.ascontiguousarray(svh[128:384])),
+                             K // 16, N // 16, K, 256, bits, cb == 1, cb == 2, 128)
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), ref, what=f"reconstruct_had bits={bits} cb={cb}")
+    assert np.array_equal(part.cpu().numpy(), out.cpu().numpy()[:, 128:384])
