@@ -93,30 +93,44 @@ __global__ __launch_bounds__(512) void prefill_plan_kernel(const int64_t* expert
 
 // ------------------------------------------------------------------ gather + input transform
 
+// One workgroup per sorted row: the row's token, expert and suh pointers are loaded once; wave w
+// transforms the 128-blocks w, w+4, ... with every block's loads issued before the first transform.
 __global__ __launch_bounds__(256) void prefill_gather_kernel(const _Float16* x, const int64_t* token_sorted,
                                                             const int* row_expert, const void* const* suh_g,
                                                             const void* const* suh_u, _Float16* xg, _Float16* xu,
-                                                            long blocks, int hidden)
+                                                            int hidden)
 {
-    const int lane = threadIdx.x & 63;
-    const long b = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (b >= blocks) return;
-    const int per = hidden / 128;
-    const long r = b / per;
-    const int c = (int)(b % per) * 128 + 2 * lane;
+    constexpr int U = 8;  // blocks per wave per round
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const long r = blockIdx.x;
     const int e = row_expert[r];
-    const hx_h2 xv = *reinterpret_cast<const hx_h2*>(x + (size_t)token_sorted[r] * hidden + c);
-    {
-        hx_h2 v = xv * *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(suh_g[e]) + c);
-        float v0 = (float)v.x, v1 = (float)v.y;
-        hx_had128_wave(v0, v1);
-        *reinterpret_cast<hx_h2*>(xg + r * hidden + c) = hx_h2{(_Float16)v0, (_Float16)v1};
-    }
-    {
-        hx_h2 v = xv * *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(suh_u[e]) + c);
-        float v0 = (float)v.x, v1 = (float)v.y;
-        hx_had128_wave(v0, v1);
-        *reinterpret_cast<hx_h2*>(xu + r * hidden + c) = hx_h2{(_Float16)v0, (_Float16)v1};
+    const _Float16* xr = x + (size_t)token_sorted[r] * hidden;
+    const _Float16* sg = static_cast<const _Float16*>(suh_g[e]);
+    const _Float16* su = static_cast<const _Float16*>(suh_u[e]);
+    const int per = hidden / 128;
+    for (int b0 = wave; b0 < per; b0 += 4 * U) {
+        hx_h2 xv[U], gv[U], uv[U];
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            const int c = min(b0 + 4 * i, per - 1) * 128 + 2 * lane;
+            xv[i] = *reinterpret_cast<const hx_h2*>(xr + c);
+            gv[i] = *reinterpret_cast<const hx_h2*>(sg + c);
+            uv[i] = *reinterpret_cast<const hx_h2*>(su + c);
+        }
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            if (b0 + 4 * i >= per) break;
+            const int c = (b0 + 4 * i) * 128 + 2 * lane;
+            hx_h2 v = xv[i] * gv[i];
+            float v0 = (float)v.x, v1 = (float)v.y;
+            hx_had128_wave(v0, v1);
+            *reinterpret_cast<hx_h2*>(xg + r * hidden + c) = hx_h2{(_Float16)v0, (_Float16)v1};
+            v = xv[i] * uv[i];
+            v0 = (float)v.x;
+            v1 = (float)v.y;
+            hx_had128_wave(v0, v1);
+            *reinterpret_cast<hx_h2*>(xu + r * hidden + c) = hx_h2{(_Float16)v0, (_Float16)v1};
+        }
     }
 }
 
@@ -332,45 +346,67 @@ __global__ __launch_bounds__(MF_THREADS, 2) void grouped_gu_kernel(GuArgs a)
 
 // One wave per (token, 128-column block): contributions H(D[r]) * w / sqrt(128) . svh_d[e] in
 // ascending routing rank from +0, then + shared, then fp16.
+// One workgroup per token: the token's routes (sorted row, weight, down svh pointer) are staged in
+// LDS once; wave w handles the 128-blocks w, w+4, ..., loading the routes' D blocks 8 at a time and
+// adding them in routing-rank order (deterministic).
 __global__ __launch_bounds__(256) void prefill_combine_kernel(const _Float16* D, const int64_t* r2s,
                                                              const int* row_expert, const _Float16* w_sorted,
                                                              const void* const* svh_d, int T, int topk, int hidden,
                                                              float* contrib, const float* shared_rows, _Float16* y,
                                                              float* y_routed, bool accumulate)
 {
-    const int lane = threadIdx.x & 63;
-    const long b = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    constexpr int J = 8;  // routes loaded together
+    __shared__ long rs[64];
+    __shared__ float ws[64];
+    __shared__ const _Float16* sv[64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.x;
+    if (threadIdx.x < topk) {
+        const long r = r2s[(size_t)t * topk + threadIdx.x];
+        rs[threadIdx.x] = r;
+        ws[threadIdx.x] = (float)w_sorted[r];
+        sv[threadIdx.x] = static_cast<const _Float16*>(svh_d[row_expert[r]]);
+    }
+    __syncthreads();
     const int per = hidden / 128;
-    if (b >= (long)T * per) return;
-    const int t = (int)(b / per);
-    const int c = (int)(b % per) * 128 + 2 * lane;
-    float a0 = 0.0f, a1 = 0.0f;
-    for (int j = 0; j < topk; ++j) {
-        const int64_t r = r2s[(size_t)t * topk + j];
-        const int e = row_expert[r];
-        const hx_h2 dv = *reinterpret_cast<const hx_h2*>(D + (size_t)r * hidden + c);
-        float d0 = (float)dv.x, d1 = (float)dv.y;
-        hx_had128_wave(d0, d1);
-        const float w = (float)w_sorted[r];
-        const hx_h2 sd = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(svh_d[e]) + c);
-        d0 = d0 * w * (float)sd.x;
-        d1 = d1 * w * (float)sd.y;
-        if (contrib) *reinterpret_cast<float2*>(contrib + (size_t)r * hidden + c) = make_float2(d0, d1);
-        a0 += d0;
-        a1 += d1;
-    }
-    const size_t o = (size_t)t * hidden + c;
-    if (y_routed) {
-        float2* yr = reinterpret_cast<float2*>(y_routed + o);
-        float2 prev = accumulate ? *yr : make_float2(0.0f, 0.0f);
-        *yr = make_float2(prev.x + a0, prev.y + a1);
-    }
-    if (y) {
-        if (shared_rows) {
-            a0 += shared_rows[o];
-            a1 += shared_rows[o + 1];
+    for (int blk = wave; blk < per; blk += 4) {
+        const int c = blk * 128 + 2 * lane;
+        float a0 = 0.0f, a1 = 0.0f;
+        for (int j0 = 0; j0 < topk; j0 += J) {
+            hx_h2 dv[J], sd[J];
+#pragma unroll
+            for (int i = 0; i < J; ++i) {
+                const int j = min(j0 + i, topk - 1);
+                dv[i] = *reinterpret_cast<const hx_h2*>(D + (size_t)rs[j] * hidden + c);
+                sd[i] = *reinterpret_cast<const hx_h2*>(sv[j] + c);
+            }
+#pragma unroll
+            for (int i = 0; i < J; ++i) {
+                if (j0 + i >= topk) break;
+                float d0 = (float)dv[i].x, d1 = (float)dv[i].y;
+                hx_had128_wave(d0, d1);
+                const float w = ws[j0 + i];
+                d0 = d0 * w * (float)sd[i].x;
+                d1 = d1 * w * (float)sd[i].y;
+                if (contrib)
+                    *reinterpret_cast<float2*>(contrib + (size_t)rs[j0 + i] * hidden + c) = make_float2(d0, d1);
+                a0 += d0;
+                a1 += d1;
+            }
         }
-        *reinterpret_cast<hx_h2*>(y + o) = hx_h2{(_Float16)a0, (_Float16)a1};
+        const size_t o = (size_t)t * hidden + c;
+        if (y_routed) {
+            float2* yr = reinterpret_cast<float2*>(y_routed + o);
+            float2 prev = accumulate ? *yr : make_float2(0.0f, 0.0f);
+            *yr = make_float2(prev.x + a0, prev.y + a1);
+        }
+        if (y) {
+            if (shared_rows) {
+                a0 += shared_rows[o];
+                a1 += shared_rows[o + 1];
+            }
+            *reinterpret_cast<hx_h2*>(y + o) = hx_h2{(_Float16)a0, (_Float16)a1};
+        }
     }
 }
 
@@ -414,9 +450,9 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
 
     hipLaunchKernelGGL(prefill_plan_kernel, dim3((unsigned)((p.R + 511) / 512)), dim3(512), 0, st, p.expert_count,
                        p.E, p.R, jobs, njobs, row_expert);
-    const long gblocks = (long)p.R * (p.hidden / 128);
-    hipLaunchKernelGGL(prefill_gather_kernel, dim3((unsigned)((gblocks + 3) / 4)), dim3(256), 0, st, p.x,
-                       p.token_sorted, row_expert, p.suh[0], p.suh[1], xg, xu, gblocks, p.hidden);
+    if (p.R > 0)
+        hipLaunchKernelGGL(prefill_gather_kernel, dim3((unsigned)p.R), dim3(256), 0, st, p.x, p.token_sorted,
+                           row_expert, p.suh[0], p.suh[1], xg, xu, p.hidden);
 
     GuArgs gu{};
     gu.jobs = jobs;
@@ -466,10 +502,11 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
         return hipGetLastError();
     }
     if (!p.r2s) return hipErrorInvalidValue;
-    const long cblocks = (long)p.T * (p.hidden / 128);
-    hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)((cblocks + 3) / 4)), dim3(256), 0, st, D, p.r2s,
-                       row_expert, p.weight_sorted, p.svh[2], p.T, p.topk, p.hidden, contrib, shared_rows, y,
-                       y_routed, accumulate);
+    if (p.topk > 64) return hipErrorInvalidValue;
+    if (p.T > 0)
+        hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)p.T), dim3(256), 0, st, D, p.r2s, row_expert,
+                           p.weight_sorted, p.svh[2], p.T, p.topk, p.hidden, contrib, shared_rows, y, y_routed,
+                           accumulate);
     return hipGetLastError();
 }
 
