@@ -122,3 +122,11 @@ def test_moe_grouped_reference_api(hx):
         torch.cuda.synchronize()
         # y2 = 1 + sum (accumulate contract): compare up to the fp32 rounding of that addition
         assert float((y2 - (1.0 + y1)).abs().max()) <= float(y1.abs().max()) * 2 ** -22
+
+
+@pytest.mark.parametrize("T", [4, 8])
+def test_moe_decode_config3_several_tokens(hx, T):
+    """Config-3 shape with 4 and 8 tokens (up to 64 routed slots + shared: more units than one round of
+    resident workgroups), 2 sampled tokens against the oracle."""
+    _run_layer(hx, E=288, hidden=4096, inter=2048, topk=8, T=T, bits=2, shared_bits=2, seed=500 + T,
+               rows=[0, T - 1])
