@@ -21,6 +21,7 @@
 namespace hx {
 
 constexpr int DEC_MAX_R = 64;  // T * topk rows handled by the few-token path
+constexpr int DEC_SHARED = -2;  // build_plan: the workgroup's slot is the shared expert
 
 // Routing plan of one call: sorted rows and active-expert slots.
 // Trellis, suh, svh of gate, up, down of one slot's expert (or of the shared expert).
@@ -226,8 +227,8 @@ HX_INLINE void load_slot_tables(const MoeDecodeArgs& a, SlotTables& t, int e)
 }
 
 // Build the plan in LDS (every workgroup computes the same plan), and the tables of the
-// workgroup's own slot `my_slot` if it is active (slots in plan order, the shared expert after the
-// routed ones).  Layer mode routes the tokens; grouped mode reads the caller's expert_count /
+// workgroup's own slot: routed slot my_slot >= 0 if it is active, the shared expert for
+// my_slot == DEC_SHARED, none for -1.  Layer mode routes the tokens; grouped mode reads the caller's expert_count /
 // token_sorted / weight_sorted.
 __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p, int my_slot)
 {
@@ -285,7 +286,7 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
             }
             if (lane == 0) {
                 p.n = n;
-                if (my_slot == n) load_slot_tables(a, p.tab, -1);
+                if (my_slot == DEC_SHARED) load_slot_tables(a, p.tab, -1);
             }
         }
     } else {
@@ -322,8 +323,8 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
             if (lane == 0) {
                 p.n = min(seen, DEC_MAX_R);
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-                if (my_slot < p.n) load_slot_tables(a, p.tab, p.expert[my_slot]);
-                else if (my_slot == p.n) load_slot_tables(a, p.tab, -1);
+                if (my_slot >= 0 && my_slot < p.n) load_slot_tables(a, p.tab, p.expert[my_slot]);
+                else if (my_slot == DEC_SHARED) load_slot_tables(a, p.tab, -1);
             }
             if (lane < R) {
                 p.token[lane] = min(max((int)a.token_sorted[lane], 0), a.T - 1);
@@ -590,14 +591,24 @@ struct Split {
     HX_INLINE int kb_begin(long c, int j) const { return j * KB / count(c); }
 };
 
+// Slot of unit slot position us: with a shared expert, position 0 is the shared expert (its units
+// come first, and need no routing) and position 1 + s routed slot s; -1 for an inactive position.
+HX_INLINE int unit_slot(const MoeDecodeArgs& a, const DecodePlan& p, int us)
+{
+    if (a.sh_tr[0] != nullptr) {
+        if (us == 0) return a.routed_slots;
+        return us - 1 < p.n ? us - 1 : -1;
+    }
+    return us < p.n ? us : -1;
+}
+
 template <int BITS, int CB, int MT>
 __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, long c,
-                                           int j, uint32_t* a_lds, float* cs_g, float* cs_u, int* rows)
+                                           int j, int slot, uint32_t* a_lds, float* cs_g, float* cs_u, int* rows)
 {
     const int kb0 = sp.kb_begin(c, j), kb1 = sp.kb_begin(c, j + 1);
     const int gg = a.inter >> 7, KB = a.hidden >> 7;
-    const int aslot = (int)(c / (2 * gg)), proj = (int)((c / gg) & 1), cg = (int)(c % gg);
-    const int slot = aslot < plan.n ? aslot : a.routed_slots;
+    const int proj = (int)((c / gg) & 1), cg = (int)(c % gg);
     const SlotInfo si = slot_info(a, plan, slot);
     const bool shared = si.expert < 0;
     if (threadIdx.x < 8)
@@ -634,12 +645,11 @@ __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodeP
 
 template <int BITS, int CB, int MT>
 __device__ __forceinline__ void d_segment(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, long c,
-                                          int j, uint32_t* a_lds, float* cs)
+                                          int j, int slot, uint32_t* a_lds, float* cs)
 {
     const int kb0 = sp.kb_begin(c, j), kb1 = sp.kb_begin(c, j + 1);
     const int gd = a.hidden >> 7, gg = a.inter >> 7, KB = a.inter >> 7;
-    const int aslot = (int)(c / gd), cg = (int)(c % gd);
-    const int slot = aslot < plan.n ? aslot : a.routed_slots;
+    const int cg = (int)(c % gd);
     const SlotInfo si = slot_info(a, plan, slot);
     const bool shared = si.expert < 0;
 
@@ -682,21 +692,19 @@ HX_INLINE int slot_bits(const MoeDecodeArgs& a, const DecodePlan& p, int slot, i
 // Runs unit (c, j) of a phase (one segment of one column group); units of inactive slots return.
 template <int BITS, int CB, int MT>
 __device__ __forceinline__ void run_unit(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, bool gu,
-                                         int nact, long c, int j, uint32_t* a_lds, float* cs_g, float* cs_u,
-                                         int* rows)
+                                         long c, int j, uint32_t* a_lds, float* cs_g, float* cs_u, int* rows)
 {
     const int gg = a.inter >> 7, gd = a.hidden >> 7;
-    const int aslot = (int)(gu ? c / (2 * gg) : c / gd);
-    if (aslot >= nact) return;
+    const int slot = unit_slot(a, plan, (int)(gu ? c / (2 * gg) : c / gd));
+    if (slot < 0) return;
     int bits = BITS;
-    if constexpr (BITS == 0)
-        bits = slot_bits(a, plan, aslot < plan.n ? aslot : a.routed_slots, gu ? (int)((c / gg) & 1) : 2);
+    if constexpr (BITS == 0) bits = slot_bits(a, plan, slot, gu ? (int)((c / gg) & 1) : 2);
     switch (bits) {
 #define HX_SEG_CASE(B)                                                                             \
     case B:                                                                                        \
         if constexpr (BITS == 0 || BITS == B) {                                                    \
-            if (gu) gu_segment<B, CB, MT>(a, plan, sp, c, j, a_lds, cs_g, cs_u, rows);               \
-            else d_segment<B, CB, MT>(a, plan, sp, c, j, a_lds, cs_g);                               \
+            if (gu) gu_segment<B, CB, MT>(a, plan, sp, c, j, slot, a_lds, cs_g, cs_u, rows);         \
+            else d_segment<B, CB, MT>(a, plan, sp, c, j, slot, a_lds, cs_g);                         \
         }                                                                                          \
         break;
         HX_SEG_CASE(1) HX_SEG_CASE(2) HX_SEG_CASE(3) HX_SEG_CASE(4)
@@ -726,11 +734,24 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
                         : Split::make(nslots * gd, a.inter >> 7, a.units_d);
     const int u = gu ? w : w - a.units_gu;
     const int c = sp.ucg(u), j = sp.uidx(u);
-    // every workgroup routes for itself: the scores are a few plain (cached) loads, whereas a plan
-    // published by one workgroup would be read by all with device-coherent loads of the same few
-    // lines (measured: 54 -> 97 us for the config-3 layer, the weight streams through those
-    // lines' memory channel stall)
-    build_plan(a, plan, gu ? c / (2 * gg) : c / gd);
+    const bool has_shared = a.sh_tr[0] != nullptr;
+    const int us = gu ? c / (2 * gg) : c / gd;   // unit slot position (0: the shared expert, if any)
+    const bool shared_unit = has_shared && us == 0;
+    if (gu && shared_unit && !(w == 0 && a.out_idx)) {
+        // the shared expert's gate/up needs no routing: its tables are arguments, its rows every token
+        // (all of them: the SiLU-gate epilogue reads svh of gate and up and suh of down)
+        if (threadIdx.x == 0) {
+            plan.n = 0;
+            load_slot_tables(a, plan.tab, -1);
+        }
+        __syncthreads();
+    } else {
+        // every workgroup routes for itself: the scores are a few plain (cached) loads, whereas a
+        // plan published by one workgroup would be read by all with device-coherent loads of the
+        // same few lines (measured: 54 -> 97 us for the config-3 layer, the weight streams through
+        // those lines' memory channel stall)
+        build_plan(a, plan, shared_unit ? DEC_SHARED : (has_shared ? us - 1 : us));
+    }
     HX_TS(1);
     HX_TS_BASE(8);
     if (blockIdx.x == 0 && a.out_idx) {
@@ -744,10 +765,8 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
             a.out_w[i] = (_Float16)plan.weight[pos];
         }
     }
-    const bool has_shared = a.sh_tr[0] != nullptr;
-    const int nact = plan.n + (has_shared ? 1 : 0);
     if (!gu) HX_TS_BASE(16);
-    run_unit<BITS, CB, MT>(a, plan, sp, gu, nact, c, j, a_lds, cs_g, cs_u, rows);
+    run_unit<BITS, CB, MT>(a, plan, sp, gu, c, j, a_lds, cs_g, cs_u, rows);
     HX_TS_BASE(0);
     HX_TS(4);
     // the last workgroup to finish clears the activation flags for the next call
