@@ -220,6 +220,34 @@ HX_INLINE void hx_had128_wave(float& v0, float& v1)
     v1 *= HX_RSQRT128;
 }
 
+// 128-point Sylvester transform held as 8 consecutive values per lane in groups of 16 lanes
+// (element 8 * (lane % 16) + j), four vectors per wave: H128 = H16 (across the 16 lanes) x H8 (in the
+// lane), both natural-order butterflies; scaled by 1/sqrt(128).
+HX_INLINE void hx_had128_x8(float (&v)[8])
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (!(j & h)) {
+                const float a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+        const bool upper = (lane & m) != 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float p = __shfl_xor(v[j], m, 64);
+            v[j] = upper ? p - v[j] : v[j] + p;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] *= HX_RSQRT128;
+}
+
 // Workgroup barrier that waits only for this wave's LDS traffic (s_waitcnt lgkmcnt(0)), so global
 // loads issued before it stay in flight across the barrier.  The waitcnt immediate encodes
 // vmcnt = 63, expcnt = 7, lgkmcnt = 0 (gfx9 field layout).

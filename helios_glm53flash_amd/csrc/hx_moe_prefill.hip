@@ -93,44 +93,41 @@ __global__ __launch_bounds__(512) void prefill_plan_kernel(const int64_t* expert
 
 // ------------------------------------------------------------------ gather + input transform
 
-// One workgroup per sorted row: the row's token, expert and suh pointers are loaded once; wave w
-// transforms the 128-blocks w, w+4, ... with every block's loads issued before the first transform.
+// One workgroup per sorted row: the row's token, expert and suh pointers are loaded once; a lane
+// holds 8 consecutive values of a 128-block (16-byte loads and stores), a wave 4 blocks, the
+// workgroup 16 blocks per round.
 __global__ __launch_bounds__(256) void prefill_gather_kernel(const _Float16* x, const int64_t* token_sorted,
                                                             const int* row_expert, const void* const* suh_g,
                                                             const void* const* suh_u, _Float16* xg, _Float16* xu,
                                                             int hidden)
 {
-    constexpr int U = 8;  // blocks per wave per round
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const long r = blockIdx.x;
     const int e = row_expert[r];
     const _Float16* xr = x + (size_t)token_sorted[r] * hidden;
     const _Float16* sg = static_cast<const _Float16*>(suh_g[e]);
     const _Float16* su = static_cast<const _Float16*>(suh_u[e]);
-    const int per = hidden / 128;
-    for (int b0 = wave; b0 < per; b0 += 4 * U) {
-        hx_h2 xv[U], gv[U], uv[U];
+    _Float16* og = xg + r * hidden;
+    _Float16* ou = xu + r * hidden;
+    for (int c = 8 * threadIdx.x; c < hidden; c += 8 * 256) {
+        const hx_h8 xv = *reinterpret_cast<const hx_h8*>(xr + c);
+        const hx_h8 gv = *reinterpret_cast<const hx_h8*>(sg + c);
+        const hx_h8 uv = *reinterpret_cast<const hx_h8*>(su + c);
+        float a[8], b[8];
 #pragma unroll
-        for (int i = 0; i < U; ++i) {
-            const int c = min(b0 + 4 * i, per - 1) * 128 + 2 * lane;
-            xv[i] = *reinterpret_cast<const hx_h2*>(xr + c);
-            gv[i] = *reinterpret_cast<const hx_h2*>(sg + c);
-            uv[i] = *reinterpret_cast<const hx_h2*>(su + c);
+        for (int j = 0; j < 8; ++j) {
+            a[j] = (float)(_Float16)(xv[j] * gv[j]);
+            b[j] = (float)(_Float16)(xv[j] * uv[j]);
         }
+        hx_had128_x8(a);
+        hx_had128_x8(b);
+        hx_h8 oa, ob;
 #pragma unroll
-        for (int i = 0; i < U; ++i) {
-            if (b0 + 4 * i >= per) break;
-            const int c = (b0 + 4 * i) * 128 + 2 * lane;
-            hx_h2 v = xv[i] * gv[i];
-            float v0 = (float)v.x, v1 = (float)v.y;
-            hx_had128_wave(v0, v1);
-            *reinterpret_cast<hx_h2*>(xg + r * hidden + c) = hx_h2{(_Float16)v0, (_Float16)v1};
-            v = xv[i] * uv[i];
-            v0 = (float)v.x;
-            v1 = (float)v.y;
-            hx_had128_wave(v0, v1);
-            *reinterpret_cast<hx_h2*>(xu + r * hidden + c) = hx_h2{(_Float16)v0, (_Float16)v1};
+        for (int j = 0; j < 8; ++j) {
+            oa[j] = (_Float16)a[j];
+            ob[j] = (_Float16)b[j];
         }
+        *reinterpret_cast<hx_h8*>(og + c) = oa;
+        *reinterpret_cast<hx_h8*>(ou + c) = ob;
     }
 }
 
@@ -347,8 +344,8 @@ __global__ __launch_bounds__(MF_THREADS, 2) void grouped_gu_kernel(GuArgs a)
 // One wave per (token, 128-column block): contributions H(D[r]) * w / sqrt(128) . svh_d[e] in
 // ascending routing rank from +0, then + shared, then fp16.
 // One workgroup per token: the token's routes (sorted row, weight, down svh pointer) are staged in
-// LDS once; wave w handles the 128-blocks w, w+4, ..., loading the routes' D blocks 8 at a time and
-// adding them in routing-rank order (deterministic).
+// LDS once; a lane holds 8 consecutive values of a 128-block (16-byte loads), the routes' D blocks
+// are loaded 8 at a time and added in routing-rank order (deterministic).
 __global__ __launch_bounds__(256) void prefill_combine_kernel(const _Float16* D, const int64_t* r2s,
                                                              const int* row_expert, const _Float16* w_sorted,
                                                              const void* const* svh_d, int T, int topk, int hidden,
@@ -359,7 +356,6 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const _Float16* D,
     __shared__ long rs[64];
     __shared__ float ws[64];
     __shared__ const _Float16* sv[64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t = blockIdx.x;
     if (threadIdx.x < topk) {
         const long r = r2s[(size_t)t * topk + threadIdx.x];
@@ -368,44 +364,46 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const _Float16* D,
         sv[threadIdx.x] = static_cast<const _Float16*>(svh_d[row_expert[r]]);
     }
     __syncthreads();
-    const int per = hidden / 128;
-    for (int blk = wave; blk < per; blk += 4) {
-        const int c = blk * 128 + 2 * lane;
-        float a0 = 0.0f, a1 = 0.0f;
-        for (int j0 = 0; j0 < topk; j0 += J) {
-            hx_h2 dv[J], sd[J];
+    for (int c = 8 * threadIdx.x; c < hidden; c += 8 * 256) {
+        float acc[8];
 #pragma unroll
-            for (int i = 0; i < J; ++i) {
-                const int j = min(j0 + i, topk - 1);
-                dv[i] = *reinterpret_cast<const hx_h2*>(D + (size_t)rs[j] * hidden + c);
-                sd[i] = *reinterpret_cast<const hx_h2*>(sv[j] + c);
-            }
+        for (int k = 0; k < 8; ++k) acc[k] = 0.0f;
+        for (int j0 = 0; j0 < topk; j0 += J) {
+            hx_h8 dv[J];
+#pragma unroll
+            for (int i = 0; i < J; ++i)
+                dv[i] = *reinterpret_cast<const hx_h8*>(D + (size_t)rs[min(j0 + i, topk - 1)] * hidden + c);
 #pragma unroll
             for (int i = 0; i < J; ++i) {
                 if (j0 + i >= topk) break;
-                float d0 = (float)dv[i].x, d1 = (float)dv[i].y;
-                hx_had128_wave(d0, d1);
+                const hx_h8 sd = *reinterpret_cast<const hx_h8*>(sv[j0 + i] + c);
+                float d[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) d[k] = (float)dv[i][k];
+                hx_had128_x8(d);
                 const float w = ws[j0 + i];
-                d0 = d0 * w * (float)sd[i].x;
-                d1 = d1 * w * (float)sd[i].y;
-                if (contrib)
-                    *reinterpret_cast<float2*>(contrib + (size_t)rs[j0 + i] * hidden + c) = make_float2(d0, d1);
-                a0 += d0;
-                a1 += d1;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) d[k] = d[k] * w * (float)sd[k];
+                if (contrib) {
+                    float* cp = contrib + (size_t)rs[j0 + i] * hidden + c;
+                    *reinterpret_cast<float4*>(cp) = make_float4(d[0], d[1], d[2], d[3]);
+                    *reinterpret_cast<float4*>(cp + 4) = make_float4(d[4], d[5], d[6], d[7]);
+                }
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[k] += d[k];
             }
         }
         const size_t o = (size_t)t * hidden + c;
         if (y_routed) {
-            float2* yr = reinterpret_cast<float2*>(y_routed + o);
-            float2 prev = accumulate ? *yr : make_float2(0.0f, 0.0f);
-            *yr = make_float2(prev.x + a0, prev.y + a1);
+            float* yr = y_routed + o;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) yr[k] = accumulate ? yr[k] + acc[k] : acc[k];
         }
         if (y) {
-            if (shared_rows) {
-                a0 += shared_rows[o];
-                a1 += shared_rows[o + 1];
-            }
-            *reinterpret_cast<hx_h2*>(y + o) = hx_h2{(_Float16)a0, (_Float16)a1};
+            hx_h8 out;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) out[k] = (_Float16)(shared_rows ? acc[k] + shared_rows[o + k] : acc[k]);
+            *reinterpret_cast<hx_h8*>(y + o) = out;
         }
     }
 }
