@@ -16,6 +16,7 @@ HX_ERR_INVALID = -1
 HX_ERR_WORKSPACE = -2
 HX_ERR_HIP = -3
 HX_ERR_UNSUPPORTED = -4
+HX_ERR_TIMEOUT = -5
 HX_GEMM_PATH_MFMA = 1
 HX_GEMM_PATH_GEMV = 90
 
@@ -55,6 +56,7 @@ SIGNATURES: dict[str, tuple] = {
                                                 C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int64, C.c_void_p]),
     "hx_exl3_pack_trellis": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "hx_exl3_unpack_trellis": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "hx_moe_check_status": (C.c_int, [C.c_void_p, C.c_void_p]),
     "hx_gemm_nt_f16": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                  C.c_void_p]),
     "hx_moe_workspace_size": (C.c_size_t, [C.c_int] * 5),

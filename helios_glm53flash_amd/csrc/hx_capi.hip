@@ -124,6 +124,24 @@ int hx_workspace_init(void* workspace, size_t bytes, hx_stream_t stream)
     return hip_status(hipMemsetAsync(workspace, 0, bytes, (hipStream_t)stream), "hx_workspace_init");
 }
 
+int hx_moe_check_status(void* workspace, hx_stream_t stream)
+{
+    if (!workspace) return fail(HX_ERR_INVALID, "hx_moe_check_status: null workspace");
+    int* status = static_cast<int*>(workspace) + hx::DEC_STATUS_INT;  // in the counter area
+    int v = 0;
+    int r = hip_status(hipMemcpyAsync(&v, status, sizeof(int), hipMemcpyDeviceToHost, (hipStream_t)stream),
+                       "hx_moe_check_status");
+    if (r == 0) r = hip_status(hipStreamSynchronize((hipStream_t)stream), "hx_moe_check_status");
+    if (r != 0) return r;
+    if (!v) return 0;
+    const int zero = 0;
+    r = hip_status(hipMemcpyAsync(status, &zero, sizeof(int), hipMemcpyHostToDevice, (hipStream_t)stream),
+                   "hx_moe_check_status");
+    if (r == 0) r = hip_status(hipStreamSynchronize((hipStream_t)stream), "hx_moe_check_status");
+    if (r != 0) return r;
+    return fail(HX_ERR_TIMEOUT, "hx_moe_check_status: a bounded wait of the few-token MoE layer gave up");
+}
+
 size_t hx_exl3_gemm_workspace_size(int M, int N, int K)
 {
     if (M <= 0 || N <= 0 || K <= 0) return 0;

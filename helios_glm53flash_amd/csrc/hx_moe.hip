@@ -40,7 +40,6 @@ void MoeWs::plan(int T_, int hidden_, int inter_, int E_, int topk_, bool shared
     off_wsorted = o;  o = al(o + sizeof(_Float16) * R);
     off_r2s = o;      o = al(o + sizeof(int64_t) * R);
     if (T <= 8 && R <= 64) {
-        off_plan = o;     o = al(o + sizeof(DecodePlan));
         // partial sums: one 8 x 128 slot per (slot, column group, segment); a column group has at
         // most K/128 segments (every share holds at least one 128-k block)
         const size_t seg_g = (size_t)slots * (inter / 128) * (hidden / 128 + 1) * 8 * 128;
@@ -72,7 +71,7 @@ MoeDecodeArgs MoeWs::decode_args(char* base) const
     a.counter_y = ctr + 8192;
     a.exit_count = ctr + 10240;
     a.ready = ctr + 10304;
-    a.status = reinterpret_cast<int*>(base + off_plan);
+    a.status = ctr + DEC_STATUS_INT;  // counter area: zero between calls unless a wait gave up
     a.contrib = reinterpret_cast<float*>(base + off_contrib);
     a.partial_g = reinterpret_cast<float*>(base + off_pg);
     a.partial_u = reinterpret_cast<float*>(base + off_pu);
@@ -133,7 +132,7 @@ hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t bits_mask, hipStrea
 {
     if (a.T > 8 || a.T * a.topk > DEC_MAX_R) return hipErrorInvalidValue;
     // counter area (ints): counter_gu [0, 4096), counter_d [4096, 8192), counter_y [8192, 10240),
-    // exit 10240, prefill permutation arrival 10250, ready [10304, 16384)
+    // exit 10240, wait status 10242, prefill permutation arrival 10250, ready [10304, 16384)
     const int slots = a.routed_slots + 1;
     if (slots * (a.inter / 128) > 4096 || slots * (a.hidden / 128) > 4096 || a.hidden / 128 > 2048 ||
         slots * (a.inter / 128) > 6080)

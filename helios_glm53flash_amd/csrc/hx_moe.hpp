@@ -15,7 +15,7 @@ struct MoeWs {
     int routed_slots = 0, slots = 0;
     size_t off_idx = 0, off_w = 0, off_count = 0, off_tsorted = 0, off_wsorted = 0, off_r2s = 0;
     // few-token path
-    size_t off_plan = 0, off_pg = 0, off_pu = 0, off_pd = 0, off_act = 0, off_contrib = 0;
+    size_t off_pg = 0, off_pu = 0, off_pd = 0, off_act = 0, off_contrib = 0;
     // prefill path
     int max_jobs = 0;
     size_t off_perm = 0, off_jobs = 0, off_njobs = 0, off_row_expert = 0, off_xg = 0, off_xu = 0, off_G = 0, off_U = 0,

@@ -22,6 +22,7 @@ namespace hx {
 
 constexpr int DEC_MAX_R = 64;  // T * topk rows handled by the few-token path
 constexpr int DEC_SHARED = -2;  // build_plan: the workgroup's slot is the shared expert
+constexpr int DEC_STATUS_INT = 10242;  // int index of the wait-status word in the counter area
 
 // Routing plan of one call: sorted rows and active-expert slots.
 // Trellis, suh, svh of gate, up, down of one slot's expert (or of the shared expert).
@@ -78,7 +79,8 @@ struct MoeDecodeArgs {
     int* exit_count;               // workgroups that finished (zero between calls)
     int units_gu, units_d;         // workgroups of the gate/up and down phases (grid = their sum)
     int* ready;                    // [slots][inter/128] 1 once the guad epilogue stored that block
-    int* status;                   // set to 1 when a bounded wait gave up (never expected)
+    int* status;                   // set to 1 when a bounded wait gave up (never expected); read and
+                                   // cleared by hx_moe_check_status
     // outputs
     int64_t* out_idx;              // optional router outputs [T][topk]
     _Float16* out_w;

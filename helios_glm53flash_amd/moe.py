@@ -187,4 +187,10 @@ class MoeLayer:
         return y
 
 
-__all__ = ["ExpertSet", "MoeLayer", "moe_grouped", "moe_workspace_bytes", "synthetic_dense_mlp", "synthetic_linear"]
+def check_status(ws: torch.Tensor, stream=None) -> None:
+    """Raise if a bounded in-kernel wait of the few-token layer gave up since the last check (the
+    flag is cleared); synchronizes the stream."""
+    check(lib.hx_moe_check_status(ws.data_ptr(), _stream(stream)), "hx_moe_check_status")
+
+
+__all__ = ["ExpertSet", "MoeLayer", "check_status", "moe_grouped", "moe_workspace_bytes", "synthetic_dense_mlp", "synthetic_linear"]

@@ -10,6 +10,7 @@
  *   HX_ERR_WORKSPACE   workspace missing or smaller than the size query
  *   HX_ERR_HIP         a HIP launch failed (hx_last_error() names it)
  *   HX_ERR_UNSUPPORTED an option the reference has that this build does not implement
+ *   HX_ERR_TIMEOUT     a bounded in-kernel wait of the few-token MoE layer gave up (hx_moe_check_status)
  *
  * Conventions: all data pointers are device pointers on the current HIP device; fp16 data is
  * IEEE binary16; `stream` may be 0 (null stream).  Calls are asynchronous on `stream`.
@@ -34,6 +35,7 @@ typedef struct ihipStream_t* hx_stream_t; /* == hipStream_t */
 #define HX_ERR_WORKSPACE (-2)
 #define HX_ERR_HIP (-3)
 #define HX_ERR_UNSUPPORTED (-4)
+#define HX_ERR_TIMEOUT (-5)
 
 #define HX_GEMM_PATH_MFMA 1
 #define HX_GEMM_PATH_GEMV 90 /* same value the reference returns when its GEMV ran */
@@ -73,6 +75,13 @@ typedef struct hx_expert_tables {
 const char* hx_version(void);
 const char* hx_last_error(void);
 int hx_workspace_init(void* workspace, size_t bytes, hx_stream_t stream);
+
+/* Whether a bounded wait inside the few-token MoE layer (hx_moe_layer / hx_moe_grouped with T <= 8:
+ * a down-projection workgroup waiting for its activations) gave up since the last check: synchronizes
+ * `stream`, clears the flag, returns HX_ERR_TIMEOUT if it was set (the results of those calls are
+ * then not to be trusted), else 0.  No counterpart in the reference, whose kernels cannot wait on
+ * each other. */
+int hx_moe_check_status(void* workspace, hx_stream_t stream);
 
 /* Phase profiler (no reference counterpart; the reference times phases with HELIOS_PROF host/event
  * timers, src/engine/runner.cpp:1006-1058): while enabled, hx_moe_layer records HIP events around
