@@ -25,7 +25,15 @@ constexpr int MF_BM = 128;  // largest row tile
 constexpr int MF_BN = 128;
 constexpr int MF_BK = 64;
 constexpr int MF_PF = 3;  // chunks of global loads in flight
-constexpr int MF_LDA = MF_BK + 8;  // halves per LDS row (pad against bank conflicts)
+#ifndef HX_MF_SWZ
+#define HX_MF_SWZ 1
+#endif
+// Operand rows of a chunk in LDS (A rows, then B columns, 64 halves of k each).  Swizzled layout:
+// 128-byte rows, 16-byte chunk c of row r stored at chunk c ^ f(r), f(r) = ((r >> 1) & 7) ^
+// (((r >> 4) & 1) << 2): with 16 lanes per LDS cycle, the A stores (2 rows x 8 chunks), the B stores
+// (rows 16 t + q of two tile columns) and the fragment reads (16 consecutive rows, one chunk) each
+// touch 16 different bank groups.  Unswizzled: rows padded to 72 halves.
+constexpr int MF_LDA = HX_MF_SWZ ? MF_BK : MF_BK + 8;  // halves per LDS row
 constexpr int MF_LDC = MF_BN + 4;  // floats per LDS row in the epilogue
 constexpr int MF_AB = (MF_BM + MF_BN) * MF_LDA;  // halves of one A + B buffer
 
@@ -33,9 +41,17 @@ struct MfmaSmem {
     union {
         _Float16 ab[2][MF_AB];  // [buffer][A rows (MF_BM x LDA), then B columns (128 x LDA)]
         float c[64 * MF_LDC];   // epilogue staging of 64 rows
+        _Float16 hx[2 * 128 * 136];  // matrix-core Hadamard staging: H128 and one 128 x 128 block
     };
     float rowsum[MF_BM];        // sum_k of each staged A row (codebook-2 map)
 };
+
+// Offset (halves) of 16-byte chunk c (8 halves of k) of LDS row r.
+HX_INLINE int mf_off(int r, int c)
+{
+    if constexpr (HX_MF_SWZ) return r * MF_LDA + 8 * (c ^ (((r >> 1) & 7) ^ (((r >> 4) & 1) << 2)));
+    else return r * MF_LDA + 8 * c;
+}
 
 HX_INLINE __amdgpu_buffer_rsrc_t mf_rsrc(const void* base, size_t bytes)
 {
@@ -101,7 +117,7 @@ __device__ __forceinline__ void mfma_tile(const _Float16* A, long lda, int rows,
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
             const int idx = t + MF_THREADS * i;
-            *reinterpret_cast<hx_u4v*>(&as[(idx >> 3) * MF_LDA + 8 * (idx & 7)]) = av[slot][i];
+            *reinterpret_cast<hx_u4v*>(&as[mf_off(idx >> 3, idx & 7)]) = av[slot][i];
             if (CB == 2 && count) {
                 const hx_h2 one = {(_Float16)1.0f, (_Float16)1.0f};
                 float s = rs[i];
@@ -115,11 +131,11 @@ __device__ __forceinline__ void mfma_tile(const _Float16* A, long lda, int rows,
         uint32_t d[16];
         if constexpr (CB == 2) quarter_affine<BITS>(wv[slot], d);
         else quarter_decode<BITS, CB>(wv[slot], d);
-        _Float16* bcol = bs + (16 * tc + q) * MF_LDA + 16 * tr;
-        *reinterpret_cast<hx_h8*>(bcol) = quarter_operand<0, 0>(d);
-        *reinterpret_cast<hx_h8*>(bcol + 8) = quarter_operand<0, 1>(d);
-        *reinterpret_cast<hx_h8*>(bcol + 8 * MF_LDA) = quarter_operand<1, 0>(d);
-        *reinterpret_cast<hx_h8*>(bcol + 8 * MF_LDA + 8) = quarter_operand<1, 1>(d);
+        const int n = 16 * tc + q;  // B column (LDS row); k chunks 2 tr, 2 tr + 1
+        *reinterpret_cast<hx_h8*>(bs + mf_off(n, 2 * tr)) = quarter_operand<0, 0>(d);
+        *reinterpret_cast<hx_h8*>(bs + mf_off(n, 2 * tr + 1)) = quarter_operand<0, 1>(d);
+        *reinterpret_cast<hx_h8*>(bs + mf_off(n + 8, 2 * tr)) = quarter_operand<1, 0>(d);
+        *reinterpret_cast<hx_h8*>(bs + mf_off(n + 8, 2 * tr + 1)) = quarter_operand<1, 1>(d);
     };
 
     const int nk = K / MF_BK;
@@ -143,11 +159,11 @@ __device__ __forceinline__ void mfma_tile(const _Float16* A, long lda, int rows,
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
                 af[mb] = *reinterpret_cast<const hx_h8*>(
-                    &as[(WM * wm + 16 * mb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
+                    &as[mf_off(WM * wm + 16 * mb + (lane & 15), kk / 8 + (lane >> 4))]);
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb)
                 bf[nb] = *reinterpret_cast<const hx_h8*>(
-                    &bs[(64 * wn + 16 * nb + (lane & 15)) * MF_LDA + kk + 8 * (lane >> 4)]);
+                    &bs[mf_off(64 * wn + 16 * nb + (lane & 15), kk / 8 + (lane >> 4))]);
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -223,6 +239,7 @@ namespace hx {
 // the fp32 additions.  The result lands in the GEMM's accumulator layout (wave (wm, wn) holds rows
 // BM/2*wm + 16*mb + 4*(lane/16) + i, columns 64*wn + 16*nb + lane%16).
 constexpr int MF_LDA2 = 128 + 8;  // halves per row of a staged 128-column block
+static_assert(sizeof(MfmaSmem::hx) == 2 * 128 * MF_LDA2 * sizeof(_Float16), "Hadamard staging size");
 
 // H128 as a B operand block ([n][k], leading dimension MF_LDA2).
 HX_INLINE void h128_to_lds(_Float16* h)

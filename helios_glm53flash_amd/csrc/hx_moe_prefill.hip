@@ -244,8 +244,8 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
     const int e = job.expert;
     const int bg = a.bits_tab[0] ? a.bits_tab[0][e] : a.bits_uniform[0];
     const int bu = a.bits_tab[1] ? a.bits_tab[1][e] : a.bits_uniform[1];
-    _Float16* H = sm.ab[0];
-    _Float16* X = sm.ab[0] + 128 * MF_LDA2;
+    _Float16* H = sm.hx;
+    _Float16* X = sm.hx + 128 * MF_LDA2;
     auto mapped = [&](int row, float v) -> float {
         if constexpr (CB == 2) return fmaf(v, CB2_SCALE, CB2_BIAS * sm.rowsum[row]);
         else return v;
