@@ -57,6 +57,7 @@ SIGNATURES: dict[str, tuple] = {
     "hx_exl3_pack_trellis": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "hx_exl3_unpack_trellis": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "hx_moe_check_status": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "hx_moe_max_concurrency": (C.c_int, [C.c_int]),
     "hx_gemm_nt_f16": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                  C.c_void_p]),
     "hx_moe_workspace_size": (C.c_size_t, [C.c_int] * 5),

@@ -124,6 +124,15 @@ int hx_workspace_init(void* workspace, size_t bytes, hx_stream_t stream)
     return hip_status(hipMemsetAsync(workspace, 0, bytes, (hipStream_t)stream), "hx_workspace_init");
 }
 
+int hx_moe_max_concurrency(int device)
+{
+    int cus = 0;
+    const int r = hip_status(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
+                             "hx_moe_max_concurrency");
+    if (r != 0) return r;
+    return cus / 8 > 0 ? cus / 8 : 1;
+}
+
 int hx_moe_check_status(void* workspace, hx_stream_t stream)
 {
     if (!workspace) return fail(HX_ERR_INVALID, "hx_moe_check_status: null workspace");

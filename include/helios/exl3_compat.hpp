@@ -150,6 +150,9 @@ inline void unpack_trellis(void* unpacked, const void* packed, int rows, int col
     check(hx_exl3_unpack_trellis(unpacked, packed, rows, cols, K, (hx_stream_t)s), "helios::exl3::unpack_trellis");
 }
 
+// reference: src/cuda/quant/exl3_moe.cuh:35
+inline int moe_max_concurrency(int device) { return check(hx_moe_max_concurrency(device), "helios::exl3::moe_max_concurrency"); }
+
 // reference: src/cuda/quant/exl3_moe.cuh:20-31
 struct ExpertTables {
     const uint16_t** gate_trellis;

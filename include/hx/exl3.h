@@ -165,6 +165,13 @@ int hx_gemm_nt_f16(void* y, const void* x, const void* w, int M, int N, int K, i
 
 /* ---- MoE layer ---------------------------------------------------------------------------- */
 
+/* Number of expert groups the engine's moe_grouped temp buffers are sized for ([concurrency,
+ * max_tokens_per_expert, dim]): CU count / 8 of `device` (negative status on error).  This build's
+ * experts do not use those buffers (hx_moe_grouped takes a workspace instead); the value keeps the
+ * engine's buffer sizing valid.  Replaces helios::exl3::moe_max_concurrency
+ * (src/cuda/quant/exl3_moe.cuh:35, exl3_moe.cu:52-56). */
+int hx_moe_max_concurrency(int device);
+
 /* Workspace bytes for hx_moe_grouped / hx_moe_layer with these extents. */
 size_t hx_moe_workspace_size(int tokens, int hidden_dim, int intermediate_dim, int num_experts, int topk);
 

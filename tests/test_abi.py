@@ -61,6 +61,7 @@ def test_cpp_compat_header_compiles_and_links(tmp_path):
                    "    helios::glue::moe_permute(nullptr, nullptr, 1, 8, 288, nullptr, nullptr, nullptr, nullptr);\n"
                    "    helios::glue::gemm_nt_f16(nullptr, nullptr, nullptr, 1, 288, 4096, false, false);\n"
                    "    helios::exl3::pack_trellis(nullptr, nullptr, 1, 1, 2);\n"
+                   "    (void)helios::exl3::moe_max_concurrency(0);\n"
                    "    helios::exl3::reconstruct_had_slice(nullptr, nullptr, nullptr, nullptr, 8, 8, 128, 128, 2, false, true, 0);\n"
                    "  }\n  return 0;\n}\n")
     lib = Path(_lib.LIB_PATH)

@@ -119,3 +119,13 @@ def test_swiglu_clamp(hx):
     torch.cuda.synchronize()
     ref = O.swiglu_clamp(g, u, 10.0).view(np.float16).astype(np.float64)
     assert_close(out.cpu().float().numpy(), ref, what="swiglu")
+
+
+def test_moe_max_concurrency_positive():
+    """helios::exl3::moe_max_concurrency (exl3_moe.cu:52-56): CU count / 8 of the device."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from helios_glm53flash_amd._lib import lib
+    n = lib.hx_moe_max_concurrency(0)
+    assert n == max(1, torch.cuda.get_device_properties(0).multi_processor_count // 8)
