@@ -34,7 +34,8 @@
  *                      +0 above -0), weight formula sums to scale
  *   hx_or_permute      definition (stable counting sort), multiset equality with the atomic version
  *   hx_or_reduce_sorted reference fixture test_deterministic_reductions.cu:49-66 ({1e20,-1e20,1,1})
- *   hx_or_moe_rows     composition of the above; dense numpy composition on a tiny layer
+ *   hx_or_moe_rows     dense numpy restatement of the layer from decoded W_hat and scipy Hadamard on
+ *                      a tiny layer; exact linearity in the routing weight; row selection
  */
 #include "exl3_oracle.h"
 

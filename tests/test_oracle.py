@@ -307,3 +307,134 @@ def test_swiglu_clamp():
     uv = np.clip(u.astype(np.float64), -10.0, 10.0)
     want = (gv / (1 + np.exp(-gv)) * uv).astype(np.float16)
     assert np.array_equal(out.astype(np.float16), want)
+
+
+# ---------------------------------------------------------------- one MoE layer
+
+def _h16(v):
+    with np.errstate(over="ignore"):   # fp16 overflow to inf is part of the reference arithmetic
+        return np.asarray(v, np.float64).astype(np.float16).astype(np.float64)
+
+
+def _silu16(g):
+    """fp16 SiLU evaluated with one fp16 rounding per step: e = exp(-g), s = 1 + e, r = 1/s, g.r."""
+    with np.errstate(over="ignore"):
+        e = _h16(np.exp(-g))
+    s = _h16(1.0 + e)
+    return _h16(g * _h16(1.0 / s))
+
+
+def _moe_layer_numpy(x, hidden, inter, idx, wt, ex, sh, L):
+    """Dense numpy restatement of one MoE layer from decoded W_hat matrices and scipy's Sylvester
+    Hadamard (exl3_moe_kernel.cuh:57-262, hadamard_inner.cuh:284-481, runner.cpp:723-738,918-958)."""
+    H = scipy.linalg.hadamard(128).astype(np.float64) / np.sqrt(128.0)
+
+    def had(v):
+        return (v.reshape(-1, 128) @ H.T).reshape(v.shape)
+
+    def W(tr, K, N, bits):
+        return O.reconstruct(tr, K, N, bits, 2).view(np.float16).astype(np.float64)
+
+    def a_in(xt, suh):
+        return _h16(had(_h16(xt * suh.astype(np.float64))))
+
+    T = x.shape[0]
+    xd = x.astype(np.float64)
+    y_routed = np.zeros((T, hidden), np.float32)
+    for t in range(T):
+        for j in range(idx.shape[1]):
+            e = int(idx[t, j])
+            w_e = float(wt[t, j].view(np.float16))
+            tr = [ex["trellis"][p][e] for p in range(3)]
+            su = [ex["suh"][p][e].view(np.float16).astype(np.float64) for p in range(3)]
+            sv = [ex["svh"][p][e].view(np.float16).astype(np.float64) for p in range(3)]
+            b = [int(ex["bits"][p][e]) for p in range(3)]
+            G = a_in(xd[t], su[0]) @ W(tr[0], hidden, inter, b[0])
+            U = a_in(xd[t], su[1]) @ W(tr[1], hidden, inter, b[1])
+            g = _h16(_h16(had(_h16(G))) * sv[0])
+            u = _h16(_h16(had(_h16(U))) * sv[1])
+            g = _silu16(g)
+            if L:
+                Lh = float(np.float16(L))
+                u = np.clip(u, -Lh, Lh)
+                g = np.minimum(g, Lh)
+            p = _h16(_h16(g * u) * su[2])
+            ad = _h16(had(p))
+            D = _h16(ad @ W(tr[2], inter, hidden, b[2]))
+            c = had(D) * w_e * sv[2]
+            y_routed[t] += c.astype(np.float32)   # fp32 accumulation in rank order
+    y16 = None
+    if sh is not None:
+        def lin(v, p, K, N):
+            su = sh["suh"][p].view(np.float16).astype(np.float64)
+            sv = sh["svh"][p].view(np.float16).astype(np.float64)
+            return had(a_in(v, su) @ W(sh["trellis"][p], K, N, int(sh["bits"][p]))) * sv
+        y16 = np.empty((T, hidden), np.float16)
+        for t in range(T):
+            gs = np.minimum(lin(xd[t], 0, hidden, inter), L)
+            us = np.clip(lin(xd[t], 1, hidden, inter), -L, L)
+            act = _h16(gs / (1.0 + np.exp(-gs)) * us)
+            d = lin(act, 2, inter, hidden).astype(np.float32)
+            y16[t] = (y_routed[t] + d).astype(np.float16)
+    return y_routed.astype(np.float64), y16
+
+
+def _tiny_layer(E, hidden, inter, seed, bits=(2, 3, 2)):
+    ex = {"trellis": [[], [], []], "suh": [[], [], []], "svh": [[], [], []], "bits": []}
+    shapes = [(hidden, inter), (hidden, inter), (inter, hidden)]
+    for p, (K, N) in enumerate(shapes):
+        for e in range(E):
+            tr, suh, svh = make_linear(seed + 10 * e + p, K, N, bits[p])
+            ex["trellis"][p].append(tr)
+            ex["suh"][p].append(suh.view(np.uint16))
+            ex["svh"][p].append(svh.view(np.uint16))
+        ex["bits"].append(np.full(E, bits[p], np.int32))
+    sh = {"trellis": [], "suh": [], "svh": [], "bits": []}
+    for p, (K, N) in enumerate(shapes):
+        tr, suh, svh = make_linear(seed + 1000 + p, K, N, 2)
+        sh["trellis"].append(tr)
+        sh["suh"].append(suh.view(np.uint16))
+        sh["svh"].append(svh.view(np.uint16))
+        sh["bits"].append(2)
+    return ex, sh
+
+
+@pytest.mark.parametrize("L", [6.0, 0.0])
+def test_moe_rows_matches_dense_numpy(L):
+    """hx_or_moe_rows against the dense numpy layer: same fp16 rounding points, fp64 matmuls in a
+    different summation order, so values agree to an fp16 ulp or two where a rounding flips."""
+    E, hidden, inter, topk, T = 4, 256, 256, 2, 3
+    ex, sh = _tiny_layer(E, hidden, inter, 40)
+    x = make_x(41, T, hidden)
+    scores = make_x(42, T, E)
+    idx, w = O.routing(scores, topk, 2.5)
+    yr, yo = O.moe_rows(x, hidden, inter, idx, w, np.arange(T), ex, sh if L else None, L)
+    yr_np, yo_np = _moe_layer_numpy(x, hidden, inter, idx, w, ex, sh if L else None, L)
+    scale = np.abs(yr_np).max()
+    assert scale > 1.0
+    assert np.abs(yr - yr_np).max() <= 2e-3 * scale
+    assert np.mean(np.abs(yr - yr_np) <= 1e-6 * scale) > 0.9   # most rows bit-identical up to fp32 order
+    if L:
+        got = yo.view(np.float16).astype(np.float64)
+        assert np.abs(got - yo_np.astype(np.float64)).max() <= 2e-3 * np.abs(yo_np.astype(np.float64)).max()
+        assert np.mean(got == yo_np.astype(np.float64)) > 0.9
+
+
+def test_moe_rows_weight_linearity_and_row_selection():
+    """c = H(D) . w . svh_d is linear in the routing weight (a power of two scales exactly); rows
+    selects tokens; an expert repeated in both ranks doubles its contribution."""
+    E, hidden, inter = 3, 128, 128
+    ex, _ = _tiny_layer(E, hidden, inter, 50)
+    x = make_x(51, 2, hidden)
+    idx = np.array([[1], [2]], np.int64)
+    w1 = np.array([[1.0], [0.5]], np.float16).view(np.uint16)
+    w2 = np.array([[2.0], [1.0]], np.float16).view(np.uint16)
+    y1, _ = O.moe_rows(x, hidden, inter, idx, w1, np.arange(2), ex, None, 0.0)
+    y2, _ = O.moe_rows(x, hidden, inter, idx, w2, np.arange(2), ex, None, 0.0)
+    assert np.array_equal(y2, 2 * y1)
+    y_sel, _ = O.moe_rows(x, hidden, inter, idx, w1, np.array([1]), ex, None, 0.0)
+    assert np.array_equal(y_sel[0], y1[1])
+    idx2 = np.array([[1, 1]], np.int64)
+    w_pair = np.array([[1.0, 1.0]], np.float16).view(np.uint16)
+    yp, _ = O.moe_rows(x[:1], hidden, inter, idx2, w_pair, np.arange(1), ex, None, 0.0)
+    assert np.array_equal(yp[0], (2 * y1[0].astype(np.float32)).astype(np.float64))
