@@ -105,6 +105,41 @@ int resident_blocks(const void* kernel, int threads, size_t lds)
     return cus * per;
 }
 
+// Occupancy of a decode launch: the decode kernels are tuned for 4 workgroups per CU (16 waves:
+// one round of gate/up units, then the down units as those retire).  When the kernel needs fewer
+// registers, more would fit: the down units of the second round would then be resident from the
+// start, spinning on their inputs, and the streaming units slow down (measured 58 against 51 us at
+// config 3).  decode_resident is the resident count with that cap; decode_lds_pad raises the
+// dynamic LDS so that each workgroup takes more than 1/(max_per_cu + 1) of the CU's 160 KB, which
+// enforces it in hardware (the runtime's occupancy query is not relied on for the LDS size per CU).
+constexpr size_t DEC_LDS_PER_CU = 160 * 1024;
+
+static int dec_per_cu(int max_per_cu)
+{
+    if (const char* v = getenv("HX_DEC_PER_CU")) return atoi(v) > 0 ? atoi(v) : max_per_cu;  // sweeps
+    return max_per_cu;
+}
+
+int decode_resident(const void* kernel, int threads, size_t lds, int max_per_cu)
+{
+    int dev = 0, cus = 0;
+    const int res = resident_blocks(kernel, threads, lds);
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return res;
+    const int cap = dec_per_cu(max_per_cu) * cus;
+    return res < cap ? res : cap;
+}
+
+size_t decode_lds_pad(const void* kernel, size_t lds, int max_per_cu)
+{
+    hipFuncAttributes fa;
+    if (hipFuncGetAttributes(&fa, kernel) != hipSuccess) return lds;
+    const size_t total = DEC_LDS_PER_CU / (size_t)(dec_per_cu(max_per_cu) + 1) + 1024;
+    const size_t dyn = total > fa.sharedSizeBytes ? total - fa.sharedSizeBytes : 0;
+    return lds > dyn ? lds : dyn;
+}
+
 // Units of the decode layer (the grid): gate/up units = one round of resident workgroups, down
 // units likewise (a second round, dispatched as the first one's workgroups finish), each clamped
 // to [column groups, blocks] of its phase; a column group gets U / C or U / C + 1 units (equal k

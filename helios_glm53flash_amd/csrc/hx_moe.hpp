@@ -53,6 +53,8 @@ hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t bits_mask, hipStrea
 // and returns the longest unit's k extent.
 int decode_units(MoeDecodeArgs& a, int resident);
 int resident_blocks(const void* kernel, int threads, size_t lds);
+int decode_resident(const void* kernel, int threads, size_t lds, int max_per_cu);
+size_t decode_lds_pad(const void* kernel, size_t lds, int max_per_cu);
 // Routed experts for T > 8 tokens: writes per-row fp32 contributions (sorted order) when contrib is
 // non-null, y = fp16(routed + shared_rows) when y is non-null, and the fp32 routed sum into
 // y_routed (added to its contents when accumulate) when y_routed is non-null.

@@ -25,11 +25,14 @@ constexpr int DEC_SHARED = -2;  // build_plan: the workgroup's slot is the share
 constexpr int DEC_STATUS_INT = 10242;  // int index of the wait-status word in the counter area
 
 // Routing plan of one call: sorted rows and active-expert slots.
-// Trellis, suh, svh of gate, up, down of one slot's expert (or of the shared expert).
+// Tables of a workgroup's slot's expert (or of the shared expert) that its unit uses: trellis and
+// suh of the projection it streams, and the scale rows of its epilogue (gate/up units: svh of gate,
+// svh of up, suh of down; down units: svh of down).
+constexpr int DEC_TABS = 5;
 struct SlotTables {
-    const void* tr[3];
-    const void* suh[3];
-    const void* svh[3];
+    const void* tr;
+    const void* suh;
+    const void* ep[3];
 };
 
 struct DecodePlan {
@@ -40,7 +43,7 @@ struct DecodePlan {
     int token[DEC_MAX_R];      // token of sorted row r
     float weight[DEC_MAX_R];   // routing weight of sorted row r
     int r2s[DEC_MAX_R];        // flat routing index -> sorted row
-    SlotTables tab;            // tables of the workgroup's own slot
+    SlotTables tab;            // tables of the workgroup's own slot and projection
 };
 
 struct MoeDecodeArgs {
@@ -109,8 +112,15 @@ HX_INLINE float sigmoid_stable(float x)
 // larger first under the monotone unsigned encoding of the fp32 key, ties to the lower index;
 // weights sigmoid(payload) * scale / (sum + 1e-20) rounded to fp16).  Lane k < topk returns
 // selection k in (e, w).
+struct NoTopkHook {
+    HX_INLINE void operator()() const {}
+};
+
+// after_loads() runs once the score loads are issued (a caller issues its own loads there, so that
+// their latencies overlap).
+template <class Hook = NoTopkHook>
 HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, int topk, float scale, int& e_out,
-                         float& w_out)
+                         float& w_out, Hook after_loads = Hook())
 {
     const int lane = threadIdx.x & 63;
     if (!bias) {
@@ -122,6 +132,7 @@ HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, in
         // all loads first (clamped addresses, no branches) so their latencies overlap
 #pragma unroll
         for (int i = 0; i < PER; ++i) raw[i] = h_as_u16(scores[min(lane + 64 * i, E - 1)]);
+        after_loads();
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int e = lane + 64 * i;
@@ -163,6 +174,7 @@ HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, in
         sv[i] = scores[e];
         bv[i] = bias[e];
     }
+    after_loads();
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int e = lane + 64 * i;
@@ -217,45 +229,151 @@ HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, in
     w_out = (float)(_Float16)(w_out * scale / sum);
 }
 
-// Tables of expert e (e < 0: the shared expert).
-HX_INLINE void load_slot_tables(const MoeDecodeArgs& a, SlotTables& t, int e)
+// Element `i` of a 3-array member of the kernel arguments, by selects rather than a run-time index:
+// indexing an argument array at run time makes the compiler copy the whole argument block into
+// per-lane scratch memory.
+// The loaded values pass through an empty asm so that the compiler cannot turn the selects back
+// into one load from a computed address.
+template <class T>
+HX_INLINE T opaque_value(T v)
 {
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        t.tr[j] = e < 0 ? a.sh_tr[j] : a.tr[j][e];
-        t.suh[j] = e < 0 ? a.sh_suh[j] : a.suh[j][e];
-        t.svh[j] = e < 0 ? a.sh_svh[j] : a.svh[j][e];
+    static_assert(sizeof(T) == 8 || sizeof(T) == 4, "pointer or 32-bit value");
+    if constexpr (sizeof(T) == 8) {
+        uint64_t u = __builtin_bit_cast(uint64_t, v);
+        asm volatile("" : "+s"(u));
+        return __builtin_bit_cast(T, u);
+    } else {
+        uint32_t u = __builtin_bit_cast(uint32_t, v);
+        asm volatile("" : "+s"(u));
+        return __builtin_bit_cast(T, u);
     }
 }
 
-// Build the plan in LDS (every workgroup computes the same plan), and the tables of the
-// workgroup's own slot: routed slot my_slot >= 0 if it is active, the shared expert for
-// my_slot == DEC_SHARED, none for -1.  Layer mode routes the tokens; grouped mode reads the caller's expert_count /
-// token_sorted / weight_sorted.
-__device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p, int my_slot)
+template <class T>
+HX_INLINE T pick3(const T (&v)[3], int i)
+{
+    const T v0 = opaque_value(v[0]), v1 = opaque_value(v[1]), v2 = opaque_value(v[2]);
+    return i == 0 ? v0 : (i == 1 ? v1 : v2);
+}
+
+HX_INLINE uint64_t ptr_bits(const void* p) { return reinterpret_cast<uint64_t>(p); }
+HX_INLINE const void* bits_ptr(uint64_t u) { return reinterpret_cast<const void*>(u); }
+
+// Table q (SlotTables order: tr, suh, ep[0..2]) of a unit streaming projection proj: the per-expert
+// pointer array, or null where the unit needs none.
+HX_INLINE const void* const* tab_base(const MoeDecodeArgs& a, int q, int proj)
+{
+    const bool gu = proj < 2;
+    switch (q) {
+        case 0: return pick3(a.tr, proj);
+        case 1: return gu ? pick3(a.suh, proj) : nullptr;
+        case 2: return gu ? a.svh[0] : a.svh[2];
+        case 3: return gu ? a.svh[1] : nullptr;
+        default: return gu ? a.suh[2] : nullptr;
+    }
+}
+
+HX_INLINE const void* sh_tab(const MoeDecodeArgs& a, int q, int proj)
+{
+    const bool gu = proj < 2;
+    switch (q) {
+        case 0: return pick3(a.sh_tr, proj);
+        case 1: return gu ? pick3(a.sh_suh, proj) : nullptr;
+        case 2: return gu ? a.sh_svh[0] : a.sh_svh[2];
+        case 3: return gu ? a.sh_svh[1] : nullptr;
+        default: return gu ? a.sh_suh[2] : nullptr;
+    }
+}
+
+HX_INLINE void set_tab(SlotTables& t, int q, const void* v)
+{
+    if (q == 0) t.tr = v;
+    else if (q == 1) t.suh = v;
+    else t.ep[q - 2] = v;
+}
+
+// Tables of a unit streaming projection proj of expert e (e < 0: the shared expert).
+HX_INLINE void load_slot_tables(const MoeDecodeArgs& a, SlotTables& t, int e, int proj)
+{
+#pragma unroll
+    for (int q = 0; q < DEC_TABS; ++q) {
+        const void* const* b = tab_base(a, q, proj);
+        set_tab(t, q, e < 0 ? sh_tab(a, q, proj) : (b ? b[e] : nullptr));
+    }
+}
+
+// Build the plan in LDS (every workgroup computes the same plan), and the tables of projection
+// proj of the workgroup's own slot: routed slot my_slot >= 0 if it is active, the shared expert for
+// my_slot == DEC_SHARED, none for -1.  Layer mode routes the tokens; grouped mode reads the caller's
+// expert_count / token_sorted / weight_sorted.
+template <int MT>
+__device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p, int my_slot, int proj)
 {
     __shared__ int sel_e[DEC_MAX_R];
     __shared__ float sel_w[DEC_MAX_R];
+    constexpr int TAB_MAX_E = 320, TPL = TAB_MAX_E / 64;
+    __shared__ uint64_t tab_lds[DEC_TABS][TAB_MAX_E];  // table entries of every expert
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int R = a.T * a.topk;
     if (a.scores) {
+        // The slot's table entries would be one more dependent load after the ranking.  Instead
+        // they are loaded for every expert while the scores are in flight and parked in LDS: wave 0
+        // loads trellis and suh (parked after its selection, which then waits for the scores only,
+        // as loads complete in order), wave 1 the epilogue tables.  The owning lane of the slot's
+        // expert takes trellis and suh after the ranking, thread 0 the rest after the plan barrier.
+        const bool pf_tab = my_slot >= 0 && a.E <= TAB_MAX_E;
+        auto load_tabs = [&](int q0, int q1, uint64_t (*v)[TPL]) {
+#pragma unroll
+            for (int q = q0; q < q1; ++q) {
+                const void* const* b = tab_base(a, q, proj);
+#pragma unroll
+                for (int i = 0; i < TPL; ++i) v[q - q0][i] = b ? ptr_bits(b[min(lane + 64 * i, a.E - 1)]) : 0;
+            }
+        };
+        auto park_tabs = [&](int q0, int q1, uint64_t (*v)[TPL]) {
+#pragma unroll
+            for (int q = q0; q < q1; ++q)
+#pragma unroll
+                for (int i = 0; i < TPL; ++i) tab_lds[q][lane + 64 * i] = v[q - q0][i];
+        };
+        uint64_t v_main[2][TPL];
+        auto prefetch = [&]() {
+            if (pf_tab && wave == 0) load_tabs(0, 2, v_main);
+        };
+        if (pf_tab && wave == 1) {
+            uint64_t v_ep[DEC_TABS - 2][TPL];
+            load_tabs(2, DEC_TABS, v_ep);
+            park_tabs(2, DEC_TABS, v_ep);
+        }
         // one token: wave 0 selects and sorts in registers; more: one wave per token, then LDS
+        // (token 0 is peeled off: only its wave issues the table prefetch; MT = 1 has no loop)
         int e1 = 0;
         float w1 = 0.0f;
-        for (int t = wave; t < a.T; t += hx_nwaves()) {
-            int e;
-            float w;
-            wave_topk(a.scores + (size_t)t * a.E, a.bias, a.E, a.topk, a.routed_scale, e, w);
+        if (wave == 0) {
+            wave_topk(a.scores, a.bias, a.E, a.topk, a.routed_scale, e1, w1, prefetch);
+            if (pf_tab) {
+                park_tabs(0, 2, v_main);
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            }
             HX_TS(5);
-            if (a.T == 1) {
-                e1 = e;
-                w1 = w;
-            } else if (lane < a.topk) {
-                sel_e[t * a.topk + lane] = e;
-                sel_w[t * a.topk + lane] = w;
+            if (a.T > 1 && lane < a.topk) {
+                sel_e[lane] = e1;
+                sel_w[lane] = w1;
             }
         }
-        if (a.T > 1) __syncthreads();
+        if constexpr (MT > 1) {
+            for (int t = wave == 0 ? hx_nwaves() : wave; t < a.T; t += hx_nwaves()) {
+                int e;
+                float w;
+                wave_topk(a.scores + (size_t)t * a.E, a.bias, a.E, a.topk, a.routed_scale, e, w);
+                if (lane < a.topk) {
+                    sel_e[t * a.topk + lane] = e;
+                    sel_w[t * a.topk + lane] = w;
+                }
+            }
+            if (a.T > 1) __syncthreads();
+        }
         if (wave == 0) {
             // stable counting sort of the R <= 64 selections by expert (ascending flat index within an
             // expert, glue2.cu:244-293 with a deterministic cursor); selection j is read from lane j
@@ -283,12 +401,19 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
                     p.expert[dless] = ei;
                     p.start[dless] = less;
                     p.count[dless] = cnt;
-                    if (dless == my_slot) load_slot_tables(a, p.tab, ei);
+                    if (dless == my_slot) {
+                        if (pf_tab) {
+                            p.tab.tr = bits_ptr(tab_lds[0][ei]);
+                            p.tab.suh = bits_ptr(tab_lds[1][ei]);
+                        } else {
+                            load_slot_tables(a, p.tab, ei, proj);
+                        }
+                    }
                 }
             }
             if (lane == 0) {
                 p.n = n;
-                if (my_slot == DEC_SHARED) load_slot_tables(a, p.tab, -1);
+                if (my_slot == DEC_SHARED) load_slot_tables(a, p.tab, -1, proj);
             }
         }
     } else {
@@ -325,8 +450,8 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
             if (lane == 0) {
                 p.n = min(seen, DEC_MAX_R);
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-                if (my_slot >= 0 && my_slot < p.n) load_slot_tables(a, p.tab, p.expert[my_slot]);
-                else if (my_slot == DEC_SHARED) load_slot_tables(a, p.tab, -1);
+                if (my_slot >= 0 && my_slot < p.n) load_slot_tables(a, p.tab, p.expert[my_slot], proj);
+                else if (my_slot == DEC_SHARED) load_slot_tables(a, p.tab, -1, proj);
             }
             if (lane < R) {
                 p.token[lane] = min(max((int)a.token_sorted[lane], 0), a.T - 1);
@@ -336,6 +461,12 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
         }
     }
     __syncthreads();
+    // the slot's epilogue tables (the epilogues read them after later barriers)
+    if (a.scores && threadIdx.x == 0 && my_slot >= 0 && my_slot < p.n && a.E <= TAB_MAX_E) {
+        const int e = p.expert[my_slot];
+#pragma unroll
+        for (int q = 2; q < DEC_TABS; ++q) set_tab(p.tab, q, bits_ptr(tab_lds[q][e]));
+    }
 }
 
 HX_INLINE SlotInfo slot_info(const MoeDecodeArgs& a, const DecodePlan& p, int slot)
@@ -352,33 +483,6 @@ HX_INLINE SlotInfo slot_info(const MoeDecodeArgs& a, const DecodePlan& p, int sl
         si.valid = si.count > 0;
     }
     return si;
-}
-
-// Element `i` of a 3-array member of the kernel arguments, by selects rather than a run-time index:
-// indexing an argument array at run time makes the compiler copy the whole argument block into
-// per-lane scratch memory.
-// The loaded values pass through an empty asm so that the compiler cannot turn the selects back
-// into one load from a computed address.
-template <class T>
-HX_INLINE T opaque_value(T v)
-{
-    static_assert(sizeof(T) == 8 || sizeof(T) == 4, "pointer or 32-bit value");
-    if constexpr (sizeof(T) == 8) {
-        uint64_t u = __builtin_bit_cast(uint64_t, v);
-        asm volatile("" : "+s"(u));
-        return __builtin_bit_cast(T, u);
-    } else {
-        uint32_t u = __builtin_bit_cast(uint32_t, v);
-        asm volatile("" : "+s"(u));
-        return __builtin_bit_cast(T, u);
-    }
-}
-
-template <class T>
-HX_INLINE T pick3(const T (&v)[3], int i)
-{
-    const T v0 = opaque_value(v[0]), v1 = opaque_value(v[1]), v2 = opaque_value(v[2]);
-    return i == 0 ? v0 : (i == 1 ? v1 : v2);
 }
 
 HX_INLINE int proj_bits(const MoeDecodeArgs& a, int proj, int expert)
@@ -399,12 +503,9 @@ __device__ __forceinline__ void guad_epilogue(const MoeDecodeArgs& a, const Deco
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = cg * 128 + 2 * lane;
     const bool shared = si.expert < 0;
-    const _Float16* svg = static_cast<const _Float16*>(p.tab.svh[0]);
-    const _Float16* svu = static_cast<const _Float16*>(p.tab.svh[1]);
-    const _Float16* sud = static_cast<const _Float16*>(p.tab.suh[2]);
-    const hx_h2 sg = *reinterpret_cast<const hx_h2*>(svg + c);
-    const hx_h2 su = *reinterpret_cast<const hx_h2*>(svu + c);
-    const hx_h2 sd = *reinterpret_cast<const hx_h2*>(sud + c);
+    const hx_h2 sg = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(p.tab.ep[0]) + c);
+    const hx_h2 su = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(p.tab.ep[1]) + c);
+    const hx_h2 sd = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(p.tab.ep[2]) + c);
     const float L = a.act_limit;
     for (int m = wave; m < si.count && m < MT; m += hx_nwaves()) {
         hx_h2 p;
@@ -458,8 +559,7 @@ __device__ __forceinline__ void down_epilogue(const MoeDecodeArgs& a, const Deco
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = cg * 128 + 2 * lane;
     const bool shared = si.expert < 0;
-    const _Float16* svd = static_cast<const _Float16*>(p.tab.svh[2]);
-    const hx_h2 sd = *reinterpret_cast<const hx_h2*>(svd + c);
+    const hx_h2 sd = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(p.tab.ep[0]) + c);
     const int R = a.T * a.topk;
     for (int m = wave; m < si.count && m < MT; m += hx_nwaves()) {
         float d0, d1, wgt;
@@ -620,8 +720,8 @@ __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodeP
     GemvArgs g;
     g.x = a.x;
     g.rows = rows;
-    g.trellis = static_cast<const uint16_t*>(plan.tab.tr[proj]);
-    g.suh = static_cast<const _Float16*>(plan.tab.suh[proj]);
+    g.trellis = static_cast<const uint16_t*>(plan.tab.tr);
+    g.suh = static_cast<const _Float16*>(plan.tab.suh);
     g.M = si.count;
     g.K = a.hidden;
     g.N = a.inter;
@@ -658,7 +758,7 @@ __device__ __forceinline__ void d_segment(const MoeDecodeArgs& a, const DecodePl
     GemvArgs g;
     g.x = a.act + (size_t)slot * 8 * a.inter;
     g.rows = nullptr;
-    g.trellis = static_cast<const uint16_t*>(plan.tab.tr[2]);
+    g.trellis = static_cast<const uint16_t*>(plan.tab.tr);
     g.suh = nullptr;
     g.M = si.count;
     g.K = a.inter;
@@ -739,12 +839,12 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
     const bool has_shared = a.sh_tr[0] != nullptr;
     const int us = gu ? c / (2 * gg) : c / gd;   // unit slot position (0: the shared expert, if any)
     const bool shared_unit = has_shared && us == 0;
+    const int proj = gu ? (c / gg) & 1 : 2;       // the projection this unit streams
     if (gu && shared_unit && !(w == 0 && a.out_idx)) {
         // the shared expert's gate/up needs no routing: its tables are arguments, its rows every token
-        // (all of them: the SiLU-gate epilogue reads svh of gate and up and suh of down)
         if (threadIdx.x == 0) {
             plan.n = 0;
-            load_slot_tables(a, plan.tab, -1);
+            load_slot_tables(a, plan.tab, -1, proj);
         }
         __syncthreads();
     } else {
@@ -752,7 +852,7 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
         // plan published by one workgroup would be read by all with device-coherent loads of the
         // same few lines (measured: 54 -> 97 us for the config-3 layer, the weight streams through
         // those lines' memory channel stall)
-        build_plan(a, plan, shared_unit ? DEC_SHARED : (has_shared ? us - 1 : us));
+        build_plan<MT>(a, plan, shared_unit ? DEC_SHARED : (has_shared ? us - 1 : us), proj);
     }
     HX_TS(1);
     HX_TS_BASE(8);
@@ -783,9 +883,13 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
     }
 }
 
-// Fixed bit width: at most 128 VGPRs so that 16 waves (4 / DEC_KS workgroups) share a CU.
+// Fixed bit width: at most 128 VGPRs so that 16 waves (4 / DEC_KS workgroups) share a CU, and
+// exactly that occupancy as the scheduling target (4 waves per SIMD).  Without the upper bound the
+// compiler trades the streaming loop's latency hiding for registers to reach 6 waves per SIMD,
+// which the launch never uses (measured 58 against 51 us at config 3).
 template <int BITS, int CB, int MT>
-__global__ __launch_bounds__(DEC_THREADS, 4 / DEC_KS) void moe_decode_kernel(MoeDecodeArgs a)
+__global__ __launch_bounds__(DEC_THREADS, 4 / DEC_KS) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void moe_decode_kernel(MoeDecodeArgs a)
 {
     moe_decode_body<BITS, CB, MT>(a);
 }

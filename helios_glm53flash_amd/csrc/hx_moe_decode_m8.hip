@@ -7,19 +7,21 @@
 
 namespace hx {
 
-// Grid = the gate/up units then the down units (decode_units); LDS = the input rows of the longest unit (the
-// unit count depends on the occupancy, which depends on the LDS: iterated to a fixed point).
+// Grid = the gate/up units then the down units (decode_units).
 template <class Kernel>
 static hipError_t launch_k(Kernel kernel, const MoeDecodeArgs& a0, hipStream_t st)
 {
     MoeDecodeArgs a = a0;
+    // LDS for the input rows of the longest unit: the unit count depends on the occupancy, which
+    // depends on the LDS (iterated to a fixed point); then padded to hold 4 workgroups per CU
+    const void* k = reinterpret_cast<const void*>(kernel);
     size_t lds = (size_t)8 * 1024 * sizeof(_Float16);
     for (int it = 0; it < 4; ++it) {
-        const int res = resident_blocks(reinterpret_cast<const void*>(kernel), DEC_THREADS, lds);
-        const size_t need = (size_t)8 * decode_units(a, res) * sizeof(_Float16);
+        const size_t need = (size_t)8 * decode_units(a, decode_resident(k, DEC_THREADS, lds, 4)) * sizeof(_Float16);
         if (need == lds) break;
         lds = need;
     }
+    lds = decode_lds_pad(k, lds, 4);
     hipLaunchKernelGGL(kernel, dim3(a.units_gu + a.units_d), dim3(DEC_THREADS), lds, st, a);
     return hipGetLastError();
 }
