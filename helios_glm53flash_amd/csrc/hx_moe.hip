@@ -140,23 +140,21 @@ size_t decode_lds_pad(const void* kernel, size_t lds, int max_per_cu)
     return lds > dyn ? lds : dyn;
 }
 
-// Units of the decode layer (the grid): gate/up units = one round of resident workgroups, down
-// units likewise (a second round, dispatched as the first one's workgroups finish), each clamped
-// to [column groups, blocks] of its phase; a column group gets U / C or U / C + 1 units (equal k
-// ranges, one segment each).  Measured (config-3 layer, 1024 resident): 1024 + 1024 units 53 us;
-// 1024 + 512 58-60 us; 576 + 576 (all resident at once) 57 us; 1152 + 576 (every column group in 4
-// / 2 units, some gate/up in the second round) 61 us; a fused variant (workgroup w runs gate/up
-// unit w then down unit w, reusing its plan) 60 us.  HX_MOE_UNITS="g,d" scales the two counts
-// (tuning).  Returns the longest unit's k extent.
+// Units of the decode layer (the grid): gate/up units first, then down units (a second round,
+// dispatched as the first one's workgroups finish).  Each phase gives every column group the same
+// number of units (equal k ranges, one segment each), as many as one round of resident workgroups
+// holds, clamped to [column groups, blocks] of the phase.  Measured (config-3 layer, 1024
+// resident): 864 + 864 units (3 per column group) 50.6 us; 1024 + 1024 (3 or 4 per column group)
+// 52.8 us; 576 + 576 51.5 us; 1152 + 864 (some gate/up in the second round) 58 us; a fused variant
+// (workgroup w runs gate/up unit w then down unit w, reusing its plan) 60 us.  HX_MOE_UNITS="g,d"
+// sets the two counts as fractions of the resident count (tuning).  Returns the longest unit's k
+// extent.
 int decode_units(MoeDecodeArgs& a, int resident)
 {
     const long slots = a.routed_slots + 1;
     const long cg_gu = slots * 2 * (a.inter / 128), kb_gu = a.hidden / 128;
     const long cg_d = slots * (a.hidden / 128), kb_d = a.inter / 128;
     auto clampu = [](long u, long c, long kb) { return u < c ? c : (u > c * kb ? c * kb : u); };
-    // default: the same number of units for every column group, as many as one round of resident
-    // workgroups holds (config 3: 864 of 1024 per phase; measured 50.6 us against 52.8 us with all
-    // 1024, where some column groups get one unit more and finish later)
     auto even = [&](long c, long kb) { return clampu(resident >= c ? c * (resident / c) : (long)resident, c, kb); };
     long ug = even(cg_gu, kb_gu), ud = even(cg_d, kb_d);
     if (const char* v = getenv("HX_MOE_UNITS")) {  // fractions of the resident count, for sweeps
