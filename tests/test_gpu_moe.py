@@ -68,6 +68,13 @@ def test_moe_decode_small(hx, T):
     _run_layer(hx, E=16, hidden=512, inter=256, topk=4, T=T, bits=2, shared_bits=2, seed=10 + T)
 
 
+@pytest.mark.parametrize("E,T", [(320, 1), (384, 1), (384, 4), (512, 2)])
+def test_moe_decode_many_experts(hx, E, T):
+    """Expert counts at and above 320: up to 320 the decode kernel takes every expert's table
+    entries with the scores; above it loads the slot's entries after the ranking (both paths)."""
+    _run_layer(hx, E=E, hidden=256, inter=256, topk=8, T=T, bits=2, shared_bits=2, seed=600 + E + T)
+
+
 def test_moe_decode_mixed_bits(hx):
     bits = [(2, 3, 4) if e % 2 else (3, 2, 2) for e in range(12)]
     _run_layer(hx, E=12, hidden=256, inter=384, topk=3, T=2, bits=bits, shared_bits=(4, 4, 3), seed=3)
