@@ -31,7 +31,8 @@
  *   hx_or_linear       equality with an independent numpy dense pipeline built from the decoded
  *                      W_hat (tests/test_oracle.py), linearity in x
  *   hx_or_routing      brute-force sorted order on small cases, tie rule (lower index first,
- *                      +0 above -0), weight formula sums to scale
+ *                      +0 above -0), weight formula sums to scale; with a correction bias: brute
+ *                      force on key sigmoid + bias, a biased low logit selected with its unbiased weight
  *   hx_or_permute      definition (stable counting sort), multiset equality with the atomic version
  *   hx_or_reduce_sorted reference fixture test_deterministic_reductions.cu:49-66 ({1e20,-1e20,1,1})
  *   hx_or_moe_rows     dense numpy restatement of the layer from decoded W_hat and scipy Hadamard on

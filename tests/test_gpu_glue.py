@@ -44,6 +44,27 @@ def test_routing_bit_exact_indices(hx, bsz, E, K):
     assert np.abs(gw - rw).max() <= 2 ** -9 * 2.5   # sigmoid via exp: within one fp16 ulp
 
 
+@pytest.mark.parametrize("bsz,E,K", [(1, 288, 8), (300, 288, 8), (5, 512, 16)])
+def test_routing_bias_indices(hx, bsz, E, K):
+    """Correction-bias routing (routing.cu:240-326): key sigmoid(logit) + bias, weight the unbiased
+    sigmoid; indices equal to the oracle's, weights within one fp16 ulp."""
+    import torch
+    from oracle import oracle as O
+    r = np.random.default_rng(7 * bsz + E)
+    s = r.standard_normal((bsz, E)).astype(np.float16)
+    b = (r.standard_normal(E) * 0.05).astype(np.float16)
+    b[3] = np.float16(4.0)
+    idx = torch.empty((bsz, K), dtype=torch.int64, device="cuda")
+    w = torch.empty((bsz, K), dtype=torch.float16, device="cuda")
+    hx.routing_ds3_nogroup(_dev(s), _dev(b), idx, w, bsz, E, K, 2.5)
+    torch.cuda.synchronize()
+    ri, rw = O.routing(s, K, 2.5, b)
+    assert np.array_equal(idx.cpu().numpy(), ri)
+    assert (ri[:, 0] == 3).all()
+    gw = w.cpu().float().numpy().astype(np.float64)
+    assert np.abs(gw - rw.view(np.float16).astype(np.float64)).max() <= 2 ** -9 * 2.5
+
+
 @pytest.mark.parametrize("M,E", [(1, 288), (4096, 288), (37, 17)])
 def test_permute_bit_exact(hx, M, E):
     import torch

@@ -38,7 +38,7 @@ def _oracle_shared(sh):
             "svh": [_host(w.svh).view(np.uint16) for w in sh], "bits": [w.bits for w in sh]}
 
 
-def _run_layer(hx, E, hidden, inter, topk, T, bits, shared_bits, seed, rows=None):
+def _run_layer(hx, E, hidden, inter, topk, T, bits, shared_bits, seed, rows=None, bias=False):
     import torch
     from oracle import oracle as O
     exl3, moe = hx
@@ -48,10 +48,12 @@ def _run_layer(hx, E, hidden, inter, topk, T, bits, shared_bits, seed, rows=None
     r = np.random.default_rng(seed + 2)
     x = r.standard_normal((T, hidden)).astype(np.float16)
     scores = r.standard_normal((T, E)).astype(np.float32).astype(np.float16)
+    b = (r.standard_normal(E) * 0.05).astype(np.float16) if bias else None
     y_routed = torch.empty((T, hidden), dtype=torch.float32, device="cuda")
-    y = layer(torch.from_numpy(x).cuda(), torch.from_numpy(scores).cuda(), y_routed=y_routed)
+    y = layer(torch.from_numpy(x).cuda(), torch.from_numpy(scores).cuda(), y_routed=y_routed,
+              bias=torch.from_numpy(b).cuda() if bias else None)
     torch.cuda.synchronize()
-    idx, w = O.routing(scores, topk, 2.5)
+    idx, w = O.routing(scores, topk, 2.5, b)
     rows = np.arange(T) if rows is None else np.asarray(rows)
     used = set(int(e) for e in idx[rows].reshape(-1))
     yr_ref, yo_ref = O.moe_rows(x, hidden, inter, idx, w, rows, _oracle_experts(ex, used),
@@ -73,6 +75,13 @@ def test_moe_decode_many_experts(hx, E, T):
     """Expert counts at and above 320: up to 320 the decode kernel takes every expert's table
     entries with the scores; above it loads the slot's entries after the ranking (both paths)."""
     _run_layer(hx, E=E, hidden=256, inter=256, topk=8, T=T, bits=2, shared_bits=2, seed=600 + E + T)
+
+
+@pytest.mark.parametrize("E,T", [(288, 1), (288, 4), (384, 1), (64, 12)])
+def test_moe_layer_router_bias(hx, E, T):
+    """Router correction bias through the layer: the decode kernel's 64-bit-key top-k (with and
+    without the slot-table prefetch), and the prefill router for T > 8."""
+    _run_layer(hx, E=E, hidden=256, inter=256, topk=8, T=T, bits=2, shared_bits=2, seed=700 + E + T, bias=True)
 
 
 def test_moe_decode_mixed_bits(hx):

@@ -268,6 +268,36 @@ def test_routing_brute_force():
     assert np.allclose(w.view(np.float16).astype(np.float64).sum(1), 2.5, rtol=5e-3)
 
 
+def _route_brute_bias(s16: np.ndarray, b16: np.ndarray, K: int, scale: float):
+    """routing.cu:240-326 with a correction bias: key = fp32(sigmoid(logit)) + fp32(bias), larger
+    first, ties to the lower index; the weight uses the unbiased sigmoid."""
+    f = s16.astype(np.float64)
+    sig = 1.0 / (1.0 + np.exp(-f))
+    key = (sig.astype(np.float32) + b16.astype(np.float32)).astype(np.float32)
+    order = sorted(range(len(f)), key=lambda e: (-float(key[e]), e))[:K]
+    o = sig[order]
+    w = (o * scale / (o.sum() + 1e-20)).astype(np.float16)
+    return np.array(order), w
+
+
+def test_routing_bias_brute_force():
+    r = np.random.default_rng(19)
+    E, K = 288, 8
+    s = r.standard_normal((8, E)).astype(np.float16)
+    b = (r.standard_normal(E) * 0.05).astype(np.float16)
+    s[2, 100] = np.float16(-6.0)
+    b[100] = np.float16(4.0)       # a low logit with a large bias is selected
+    idx, w = O.routing(s, K, 2.5, b)
+    for row in range(8):
+        bi, bw = _route_brute_bias(s[row], b, K, 2.5)
+        assert np.array_equal(idx[row], bi)
+        assert np.array_equal(w[row], bw.view(np.uint16))
+    assert idx[2, 0] == 100
+    # the weight of that expert comes from sigmoid(-6), not from the biased key
+    assert w[2, 0].view(np.float16) < np.float16(0.01)
+    assert not np.array_equal(idx, O.routing(s, K, 2.5)[0])
+
+
 # ---------------------------------------------------------------- permutation / reduction
 
 def test_permute_definition():
