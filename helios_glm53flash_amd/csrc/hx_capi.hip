@@ -161,7 +161,8 @@ size_t hx_exl3_gemm_workspace_size(int M, int N, int K)
 int hx_exl3_gemm(void* y, const void* x, const hx_group_words* w, int M, int N, int K, int bits, int y_fp32,
                  hx_stream_t stream, void* a_had, int mcg, void* workspace, size_t workspace_bytes)
 {
-    if (!w || !y || !x || !w->trellis || !w->suh || !w->svh) return fail(HX_ERR_INVALID, "hx_exl3_gemm: null pointer");
+    if (!w || !w->trellis || !w->suh || !w->svh || (M != 0 && (!y || !x)))
+        return fail(HX_ERR_INVALID, "hx_exl3_gemm: null pointer");
     if (M < 0 || N <= 0 || K <= 0 || N % 128 || K % 128) return fail(HX_ERR_INVALID, "hx_exl3_gemm: K and N must be positive multiples of 128");
     if (bits < 1 || bits > 8) return fail(HX_ERR_INVALID, "hx_exl3_gemm: bits must be in [1, 8]");
     if (w->mul1 && (uint32_t)w->mul1 != 0x83DCD12Du) return fail(HX_ERR_INVALID, "hx_exl3_gemm: unsupported mul1 constant");
@@ -378,10 +379,10 @@ int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const i
                           mul1, "hx_moe_grouped: bad arguments"))
         return r;
     if (act_function != 0) return fail(HX_ERR_UNSUPPORTED, "hx_moe_grouped: only act_function 0 (SiLU)");
+    if (tokens == 0) return 0;  // an empty batch is a no-op (its activation pointers may be null)
     if (!x || !expert_count || !token_sorted || !weight_sorted) return fail(HX_ERR_INVALID, "hx_moe_grouped: null input");
     if (!sorted_contributions && (!y || !route_to_sorted))
         return fail(HX_ERR_INVALID, "hx_moe_grouped: y and route_to_sorted are needed without sorted_contributions");
-    if (tokens == 0) return 0;
     hx::MoeWs L;
     L.plan(tokens, hidden_dim, intermediate_dim, num_experts, topk, false,
            max_bits_of(tables, K_gate, K_up, K_down, nullptr));
@@ -444,6 +445,7 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
     if (int r = moe_check(tables, tokens, hidden_dim, intermediate_dim, num_experts, topk, K_gate, K_up, K_down, mcg,
                           mul1, "hx_moe_layer: bad arguments"))
         return r;
+    if (tokens == 0) return 0;  // an empty batch is a no-op (its activation pointers may be null)
     if (!x || !scores || (!y && !y_routed)) return fail(HX_ERR_INVALID, "hx_moe_layer: null input/output");
     if (shared) {
         if (!shared_bits) return fail(HX_ERR_INVALID, "hx_moe_layer: shared_bits required with a shared expert");
@@ -452,7 +454,6 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
                 return fail(HX_ERR_INVALID, "hx_moe_layer: bad shared expert");
         if (act_limit <= 0.0f) return fail(HX_ERR_INVALID, "hx_moe_layer: the shared-expert swiglu needs act_limit > 0");
     }
-    if (tokens == 0) return 0;
     hx::MoeWs L;
     L.plan(tokens, hidden_dim, intermediate_dim, num_experts, topk, shared != nullptr,
            max_bits_of(tables, K_gate, K_up, K_down, shared ? shared_bits : nullptr));

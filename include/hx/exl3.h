@@ -98,7 +98,8 @@ const char* hx_profile_phase_name(int phase);
  * Replaces helios::exl3::gemm (src/cuda/quant/exl3_gemm.cuh:51-66, exl3_gemm.cu:81-243).
  * M <= 16 runs the fused decode-GEMV (returns HX_GEMM_PATH_GEMV), else the MFMA GEMM (returns
  * HX_GEMM_PATH_MFMA), which needs a_had (M*K fp16 scratch, as in the reference) or, when
- * a_had is NULL, takes it from the workspace.  K % 128 == 0, N % 128 == 0, bits 1..8. */
+ * a_had is NULL, takes it from the workspace.  K % 128 == 0, N % 128 == 0, bits 1..8.  M == 0 is
+ * a no-op (x and y may then be NULL). */
 size_t hx_exl3_gemm_workspace_size(int M, int N, int K);
 int hx_exl3_gemm(void* y, const void* x, const hx_group_words* w, int M, int N, int K, int bits, int y_fp32,
                  hx_stream_t stream, void* a_had, int mcg, void* workspace, size_t workspace_bytes);
@@ -185,7 +186,7 @@ size_t hx_moe_workspace_size(int tokens, int hidden_dim, int intermediate_dim, i
  * (src/cuda/quant/exl3_moe.cuh:74-105, exl3_moe.cu:58-265).  temp_* buffers, max_tokens_per_expert,
  * concurrency and num_active are accepted for signature parity and unused (all scratch comes from
  * the workspace; there is no token cap per expert).  Codebooks: mcg or mul1 (as the reference);
- * act_function must be 0 (SiLU). */
+ * act_function must be 0 (SiLU).  tokens == 0 is a no-op (the activation pointers may then be NULL). */
 int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const int64_t* token_sorted,
                    const void* weight_sorted, void* temp_state_g, void* temp_state_u, void* temp_intermediate_g,
                    void* temp_intermediate_u, const hx_expert_tables* tables, int tokens, int hidden_dim,
@@ -200,7 +201,7 @@ int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const i
  * y = fp16(routed + shared) [tokens][hidden_dim]; y_routed (fp32, optional) receives the routed
  * sum.  Replaces the single-GPU part of helios Runner::moe_ffn (src/engine/runner.cpp:711-959:
  * shared expert :723-738, router :759-762, permute :764, moe_grouped + reduce :918-922,
- * combine :957-958). */
+ * combine :957-958).  tokens == 0 is a no-op (the activation pointers may then be NULL). */
 int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, const void* bias,
                  const hx_expert_tables* tables, const hx_group_words* shared, const int* shared_bits, int tokens,
                  int hidden_dim, int intermediate_dim, int num_experts, int topk, int K_gate, int K_up, int K_down,

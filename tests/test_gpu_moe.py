@@ -84,6 +84,22 @@ def test_moe_layer_router_bias(hx, E, T):
     _run_layer(hx, E=E, hidden=256, inter=256, topk=8, T=T, bits=2, shared_bits=2, seed=700 + E + T, bias=True)
 
 
+def test_empty_batches_are_noops(hx):
+    """tokens == 0 / M == 0 through the layer, the grouped call's Python mirror and the linear: no
+    launch, no error, even with the null data pointers of empty tensors."""
+    import torch
+    exl3, moe = hx
+    ex = moe.ExpertSet.synthetic(8, 256, 256, 2, seed=1)
+    sh = moe.synthetic_dense_mlp(256, 256, 2, seed=2)
+    layer = moe.MoeLayer(ex, sh, topk=2)
+    x = torch.empty((0, 256), dtype=torch.float16, device="cuda")
+    y = layer(x, torch.empty((0, 8), dtype=torch.float16, device="cuda"))
+    assert y.shape == (0, 256)
+    path = exl3.gemm(torch.empty((0, 256), dtype=torch.float16, device="cuda"), x, sh[0], 0, 256, 256, 2)
+    assert path == exl3.HX_GEMM_PATH_GEMV
+    torch.cuda.synchronize()
+
+
 def test_moe_decode_mixed_bits(hx):
     bits = [(2, 3, 4) if e % 2 else (3, 2, 2) for e in range(12)]
     _run_layer(hx, E=12, hidden=256, inter=384, topk=3, T=2, bits=bits, shared_bits=(4, 4, 3), seed=3)
