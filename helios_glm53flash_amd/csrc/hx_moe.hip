@@ -9,6 +9,7 @@
 #include <stdlib.h>
 
 #include <mutex>
+#include <utility>
 #include <vector>
 
 
@@ -120,23 +121,51 @@ static int dec_per_cu(int max_per_cu)
     return max_per_cu;
 }
 
+static int device_cus()
+{
+    static std::mutex mu;
+    static std::vector<std::pair<int, int>> cache;  // (device, CUs)
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& c : cache)
+        if (c.first == dev) return c.second;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+    cache.push_back({dev, cus});
+    return cus;
+}
+
 int decode_resident(const void* kernel, int threads, size_t lds, int max_per_cu)
 {
-    int dev = 0, cus = 0;
     const int res = resident_blocks(kernel, threads, lds);
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        return res;
+    const int cus = device_cus();
+    if (cus <= 0) return res;
     const int cap = dec_per_cu(max_per_cu) * cus;
     return res < cap ? res : cap;
 }
 
 size_t decode_lds_pad(const void* kernel, size_t lds, int max_per_cu)
 {
-    hipFuncAttributes fa;
-    if (hipFuncGetAttributes(&fa, kernel) != hipSuccess) return lds;
+    static std::mutex mu;
+    static std::vector<std::pair<const void*, size_t>> cache;  // (kernel, static LDS bytes)
+    size_t stat = 0;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        bool found = false;
+        for (const auto& c : cache)
+            if (c.first == kernel) {
+                stat = c.second;
+                found = true;
+            }
+        if (!found) {
+            hipFuncAttributes fa;
+            if (hipFuncGetAttributes(&fa, kernel) != hipSuccess) return lds;
+            stat = fa.sharedSizeBytes;
+            cache.push_back({kernel, stat});
+        }
+    }
     const size_t total = DEC_LDS_PER_CU / (size_t)(dec_per_cu(max_per_cu) + 1) + 1024;
-    const size_t dyn = total > fa.sharedSizeBytes ? total - fa.sharedSizeBytes : 0;
+    const size_t dyn = total > stat ? total - stat : 0;
     return lds > dyn ? lds : dyn;
 }
 
