@@ -10,16 +10,25 @@ namespace hx {
 template <int BITS>
 hipError_t launch_gemv_cb(int cb, const GemvArgs& g, const _Float16* svh, void* y, bool y_fp32, hipStream_t st);
 
-// Split-K plan: grid = (N / 128) column groups x (K / kc) splits.  kc grows until the grid would
-// drop below ~2 workgroups per CU; the activation block (M x kc fp16) stays within 32 KiB of LDS.
+// Split-K plan: grid = (N / 128) column groups x (K / kc) splits.  kc shrinks from the largest
+// chunk whose activation block (M x kc fp16) fits 32 KiB of LDS until the grid holds ~2 workgroups
+// per CU, but not below 512: each split adds a partial sum that the last arriver gathers, on the
+// critical path of a small linear.  Measured at K = 4096, M = 1: config 1 (N = 2048, 16 column
+// groups) 13.2 us with 32 splits of 128, 9.0 us with 8 splits of 512, 11.5 us with 4 of 1024;
+// config 2 (N = 12288) best at 8 splits too (15.0 us; 20.6 us with 16 splits).
+constexpr int GEMV_KC_FLOOR = 512;
+
 void gemv_plan(int M, int K, int N, int bits, int* splits, int* kc)
 {
     (void)bits;
     const int groups = N / 128;
     int cap = 16384 / (M < 1 ? 1 : M);
-    if (const char* v = getenv("HX_GEMV_KC")) cap = atoi(v) > 0 ? atoi(v) : cap;
+    if (const char* v = getenv("HX_GEMV_KC")) cap = atoi(v) > 0 ? atoi(v) : cap;  // sweeps
     int c = gemv_kc_for(K, cap);
-    while (c > 128 && (long)groups * (K / c) < 512) {
+    int min_wg = 512, floor_kc = GEMV_KC_FLOOR;
+    if (const char* v = getenv("HX_GEMV_MINWG")) min_wg = atoi(v) > 0 ? atoi(v) : min_wg;  // sweeps
+    if (const char* v = getenv("HX_GEMV_KC_FLOOR")) floor_kc = atoi(v) > 0 ? atoi(v) : floor_kc;
+    while (c > 128 && c > floor_kc && (long)groups * (K / c) < min_wg) {
         const int smaller = gemv_kc_for(K, c - 128);
         if (smaller == c) break;
         c = smaller;
