@@ -6,6 +6,8 @@
       HBM bytes per launch of the MoE decode layer kernel from FETCH_SIZE and WRITE_SIZE passes, each
       scaled by what the same counter reads for the calibration copy (256 MiB read + 256 MiB write)
       of bench.py --profile-only
+  python -m helios_glm53flash_amd.profiling counters <pmc.db> <kernel-name-part>
+      mean value per dispatch of each counter collected for the matching kernels
 """
 from __future__ import annotations
 
@@ -65,11 +67,21 @@ def traffic(fetch_db: str, write_db: str, cmd: str = "") -> dict:
     return out
 
 
+def counters(db: str, key: str) -> dict[str, float]:
+    """Mean value per dispatch of every counter collected for the kernels whose name contains key."""
+    c = sqlite3.connect(db)
+    rows = c.execute("select counter_name, avg(value) from counters_collection where kernel_name like ? "
+                     "group by counter_name", (f"%{key}%",)).fetchall()
+    return {n: float(v) for n, v in rows}
+
+
 def main(argv: list[str]) -> None:
     if len(argv) >= 2 and argv[0] == "stats":
         for r in kernel_stats(argv[1]):
             print(f"{r['calls']:6d}  avg {r['avg_us']:10.3f} us  min {r['min_us']:10.3f}  max {r['max_us']:10.3f}  "
                   f"{r['kernel'][:110]}")
+    elif len(argv) >= 3 and argv[0] == "counters":
+        print(json.dumps(counters(argv[1], argv[2]), indent=1))
     elif len(argv) >= 3 and argv[0] == "traffic":
         cmd = argv[argv.index("--cmd") + 1] if "--cmd" in argv else ""
         print(json.dumps(traffic(argv[1], argv[2], cmd), indent=1))
