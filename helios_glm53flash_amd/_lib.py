@@ -6,11 +6,10 @@ shared object is missing the import of this module raises, naming the build comm
 from __future__ import annotations
 
 import ctypes as C
-import os
 from pathlib import Path
 
 _PKG = Path(__file__).resolve().parent
-LIB_PATH = Path(os.environ.get("HX_EXL3_LIB", _PKG / "libhx_exl3.so"))
+LIB_PATH = _PKG / "libhx_exl3.so"  # the in-tree build only: no override, so a stale copy cannot load
 
 HX_ERR_INVALID = -1
 HX_ERR_WORKSPACE = -2

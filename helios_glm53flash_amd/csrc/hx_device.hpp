@@ -29,19 +29,6 @@ typedef float hx_f16v __attribute__((ext_vector_type(16)));
 #define HX_SETPRIO(p) __builtin_amdgcn_s_setprio(p)
 #endif
 
-#ifdef HX_TIMING
-// Phase timestamps (s_memrealtime, 100 MHz) per workgroup, for a separately built timing library:
-// hx_dbg_ts[block][31] is the base slot of the current work unit, HX_TS(i) stamps slot base + i.
-static __device__ uint64_t hx_dbg_ts[4096][32];
-#define HX_TS_BASE(b) do { if (threadIdx.x == 0 && blockIdx.x < 4096) hx_dbg_ts[blockIdx.x][31] = (b); } while (0)
-#define HX_TS(i) do { if (threadIdx.x == 0 && blockIdx.x < 4096) hx_dbg_ts[blockIdx.x][hx_dbg_ts[blockIdx.x][31] + (i)] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#define HX_TS_VAL(i, v) do { if (threadIdx.x == 0 && blockIdx.x < 4096) hx_dbg_ts[blockIdx.x][hx_dbg_ts[blockIdx.x][31] + (i)] = (v); } while (0)
-#else
-#define HX_TS_BASE(b) do { } while (0)
-#define HX_TS(i) do { } while (0)
-#define HX_TS_VAL(i, v) do { } while (0)
-#endif
-
 static constexpr float HX_RSQRT128 = 0.088388347648f;
 
 // Workgroup size in threads / waves (kernels here run 256 or 1024 threads).

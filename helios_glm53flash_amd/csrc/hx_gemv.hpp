@@ -432,7 +432,6 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     const int voff0 = lane_off + ((q * BITS + NW - 1) % NW) * 4, voff1 = lane_off + q * BITS * 4;
     const int row_bytes = tiles_n * NW * 4;
     auto soff = [&](int st) { return ((k0 + step_k(min(st, steps - 1))) >> 4) * row_bytes; };
-    HX_TS(0);
     InputRegs in;
     if (!g.pre_transformed) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, false);
     if (steps > 0) {
@@ -440,14 +439,11 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
         for (int j = 0; j < PF; ++j) load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff(j));
     }
 
-    HX_TS(1);
     before_input();
-    HX_TS(3);
     if (g.pre_transformed) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, true);
     input_finish(a_lds, in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, g.pre_transformed);
     hx_lds_barrier();
     after_input();
-    HX_TS(2);
     if constexpr (AFFINE) {
         for (int m = wave; m < g.M && m < MT; m += hx_nwaves()) {
             const _Float16* row = reinterpret_cast<const _Float16*>(a_lds) + (size_t)m * kc;
@@ -474,9 +470,15 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
             if (j == PF / 4) HX_SETPRIO(2);
             if (j == PF / 2) HX_SETPRIO(1);
             if (j == 3 * PF / 4) HX_SETPRIO(0);
+            // the decode of a slot past the range is skipped (a range that is not a multiple of PF
+            // steps would otherwise decode the repeated last row); every refill is issued (past the
+            // range it repeats the last row, an L2 hit), so that the count of loads in flight, and
+            // so every wait, is the same at every step
             uint32_t d[16];
-            if constexpr (AFFINE) quarter_affine<BITS>(buf[j], d);
-            else quarter_decode<BITS, CB>(buf[j], d);
+            if (st < steps) {
+                if constexpr (AFFINE) quarter_affine<BITS>(buf[j], d);
+                else quarter_decode<BITS, CB>(buf[j], d);
+            }
             load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff(st + PF));
             if (st < steps) {
                 const int kl = step_k(st) + 16 * gq;
@@ -530,7 +532,7 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
             }
         }
     }
-    __syncthreads();
+    hx_lds_barrier();  // colsum is complete (LDS only: the repeated-row refills still in flight need no wait)
 }
 
 // Split s of K in chunks of g.kc (the last may be shorter).

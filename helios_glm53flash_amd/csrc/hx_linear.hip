@@ -29,8 +29,10 @@ void gemv_plan(int M, int K, int N, int bits, int* splits, int* kc)
     if (const char* v = getenv("HX_GEMV_MINWG")) min_wg = atoi(v) > 0 ? atoi(v) : min_wg;  // sweeps
     if (const char* v = getenv("HX_GEMV_KC_FLOOR")) floor_kc = atoi(v) > 0 ? atoi(v) : floor_kc;
     while (c > 128 && c > floor_kc && (long)groups * (K / c) < min_wg) {
+        // one shrink step can skip past the floor when K has no multiple-of-128 divisor in
+        // [floor_kc, c) (K = 1152: 1152 -> 384): stop at c then
         const int smaller = gemv_kc_for(K, c - 128);
-        if (smaller == c) break;
+        if (smaller == c || smaller < floor_kc) break;
         c = smaller;
     }
     *kc = c;

@@ -356,7 +356,6 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
             }
-            HX_TS(5);
             if (a.T > 1 && lane < a.topk) {
                 sel_e[lane] = e1;
                 sel_w[lane] = w1;
@@ -826,8 +825,6 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
     __shared__ DecodePlan plan;
     __shared__ int rows[8];
     HX_SETPRIO(3);  // the routing plan gates every workgroup
-    HX_TS_BASE(0);
-    HX_TS(0);
     const int gg = a.inter >> 7, gd = a.hidden >> 7;
     const int w = blockIdx.x, G = gridDim.x;
     const int nslots = a.routed_slots + 1;  // units exist for every possible slot
@@ -854,8 +851,6 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
         // those lines' memory channel stall)
         build_plan<MT>(a, plan, shared_unit ? DEC_SHARED : (has_shared ? us - 1 : us), proj);
     }
-    HX_TS(1);
-    HX_TS_BASE(8);
     if (blockIdx.x == 0 && a.out_idx) {
         const int R = a.T * a.topk;
         for (int i = threadIdx.x; i < R; i += hx_nthreads()) {
@@ -867,10 +862,7 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
             a.out_w[i] = (_Float16)plan.weight[pos];
         }
     }
-    if (!gu) HX_TS_BASE(16);
     run_unit<BITS, CB, MT>(a, plan, sp, gu, c, j, a_lds, cs_g, cs_u, rows);
-    HX_TS_BASE(0);
-    HX_TS(4);
     // the last workgroup to finish clears the activation flags for the next call
     __shared__ bool last;
     if (threadIdx.x == 0)

@@ -5,12 +5,6 @@
 
 #include <stdlib.h>
 
-#ifdef HX_TIMING
-extern "C" int hx_dbg_copy(void* host)
-{
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(hx_dbg_ts), sizeof(hx_dbg_ts), 0, hipMemcpyDeviceToHost);
-}
-#endif
 
 namespace hx {
 

@@ -44,18 +44,25 @@ def _need(t: torch.Tensor, name: str, dtypes: tuple) -> None:
         raise ValueError(f"{name} has dtype {t.dtype}, expected one of {dtypes}")
 
 
-_workspaces: dict[int, torch.Tensor] = {}
+_workspaces: dict[tuple, torch.Tensor] = {}
 
 
-def workspace(nbytes: int, device: Optional[torch.device] = None) -> torch.Tensor:
-    """Per-device zero-initialised workspace, grown on demand (counters inside stay zero between
-    calls because every kernel resets what it uses)."""
+def workspace(nbytes: int, device: Optional[torch.device] = None, stream=None) -> torch.Tensor:
+    """Zero-initialised workspace of one (device, stream), grown on demand (the counters inside stay
+    zero between calls because every kernel resets what it uses).  A workspace serves one stream at
+    a time: calls on different streams get different workspaces, so their arrival counters and
+    ready flags never meet.  Growing synchronizes the device twice: before the old buffer is
+    released (kernels still queued on any stream may use it) and after the zero fill (issued on
+    torch's current stream, the kernels run on `stream`).  Grow outside graph capture."""
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    ws = _workspaces.get(idx)
+    key = (idx, _stream(stream))
+    ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
+        torch.cuda.synchronize(idx)
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
-        _workspaces[idx] = ws
+        torch.cuda.synchronize(idx)
+        _workspaces[key] = ws
     return ws
 
 
@@ -101,7 +108,7 @@ def gemm(y: torch.Tensor, x: torch.Tensor, w: GroupWords, M: int, N: int, K: int
     if a_had is not None:
         _need(a_had, "a_had", (torch.float16,))
     nbytes = lib.hx_exl3_gemm_workspace_size(M, N, K)
-    ws = workspace(nbytes, x.device) if (M <= GEMV_MAX_M or a_had is None) else None
+    ws = workspace(nbytes, x.device, stream) if (M <= GEMV_MAX_M or a_had is None) else None
     gw = w.c()
     return check(lib.hx_exl3_gemm(y.data_ptr(), x.data_ptr(), C.byref(gw), M, N, K, bits, int(y_fp32),
                                   _stream(stream), _ptr(a_had), int(mcg), _ptr(ws), ws.numel() if ws is not None else 0),

@@ -129,7 +129,7 @@ def moe_grouped(x: torch.Tensor, y: Optional[torch.Tensor], expert_count: torch.
     ub = experts.uniform_bits() or (0, 0, 0)
     E = experts.num_experts
     nbytes = moe_workspace_bytes(tokens, experts.hidden, experts.inter, E, topk)
-    ws = workspace(nbytes, x.device)
+    ws = workspace(nbytes, x.device, stream)
     mul1 = experts.mul1 and not mcg
     check(lib.hx_moe_grouped(x.data_ptr(), _ptr(y), expert_count.data_ptr(), token_sorted.data_ptr(),
                              weight_sorted.data_ptr(), None, None, None, None, C.byref(experts.tables()), tokens,
@@ -175,7 +175,7 @@ class MoeLayer:
         if y is None:
             y = torch.empty((T, ex.hidden), dtype=torch.float16, device=x.device)
         if ws is None:
-            ws = workspace(self.workspace_bytes(T), x.device)
+            ws = workspace(self.workspace_bytes(T), x.device, stream)
         ub = ex.uniform_bits() or (0, 0, 0)
         check(lib.hx_moe_layer(y.data_ptr(), _ptr(y_routed), x.data_ptr(), scores.data_ptr(), _ptr(bias),
                                C.byref(ex.tables()),
