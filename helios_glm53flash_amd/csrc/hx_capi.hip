@@ -1,6 +1,7 @@
 // hx_capi.hip -- extern "C" boundary of libhx_exl3.so (declarations in include/hx/exl3.h).
 #include <hip/hip_runtime.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <vector>
@@ -151,6 +152,19 @@ int hx_moe_check_status(void* workspace, hx_stream_t stream)
     return fail(HX_ERR_TIMEOUT, "hx_moe_check_status: a bounded wait of the few-token MoE layer gave up");
 }
 
+// Debug option: with HX_MOE_SYNC_CHECK=1 in the environment, every few-token MoE call synchronizes
+// its stream and reports a given-up bounded wait (hx_moe_check_status) as its own return value.
+// Skipped while the stream is being captured into a graph (no synchronization is possible there).
+static int decode_checked(int r, void* workspace, hx_stream_t stream)
+{
+    if (r != 0) return r;
+    const char* v = getenv("HX_MOE_SYNC_CHECK");
+    if (!v || atoi(v) == 0) return 0;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return 0;
+    return hx_moe_check_status(workspace, stream);
+}
+
 size_t hx_exl3_gemm_workspace_size(int M, int N, int K)
 {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
@@ -254,13 +268,13 @@ int hx_routing_ds3_nogroup(const void* scores, const void* bias, int64_t* topk_i
                            int bsz, int num_experts, int K, float scaling_factor, int use_topk, int act_fn,
                            hx_stream_t stream)
 {
-    if (!use_topk || act_fn != 0) return fail(HX_ERR_UNSUPPORTED, "hx_routing_ds3_nogroup: only use_topk=1 with sigmoid");
+    if (act_fn != 0 && act_fn != 1) return fail(HX_ERR_UNSUPPORTED, "hx_routing_ds3_nogroup: act_fn must be 0 (sigmoid) or 1 (sqrt-softplus)");
     if (!scores || !topk_indices || !topk_weights || bsz < 0 || num_experts < 1 || num_experts > 512 || K < 1 ||
         K > 64 || K > num_experts)
         return fail(HX_ERR_INVALID, "hx_routing_ds3_nogroup: bad arguments");
     return hip_status(hx::launch_routing(static_cast<const _Float16*>(scores), static_cast<const _Float16*>(bias),
                                          topk_indices, static_cast<_Float16*>(topk_weights), bsz, num_experts, K,
-                                         scaling_factor, (hipStream_t)stream),
+                                         scaling_factor, (hipStream_t)stream, use_topk != 0, act_fn),
                       "hx_routing_ds3_nogroup");
 }
 
@@ -408,8 +422,9 @@ int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const i
             a.y_routed = y;
             a.y_accumulate = true;
         }
-        return hip_status(hx::run_moe_decode(a, cb, phase_mask(tables, K_gate, K_up) | phase_mask(tables, K_down, 0), st),
-                          "hx_moe_grouped(decode)");
+        return decode_checked(hip_status(hx::run_moe_decode(a, cb, phase_mask(tables, K_gate, K_up) | phase_mask(tables, K_down, 0), st),
+                                         "hx_moe_grouped(decode)"),
+                              workspace, stream);
     }
     hx::PrefillArgs p{};
     p.x = xh;
@@ -495,7 +510,8 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
         a.y = static_cast<_Float16*>(y);
         a.y_routed = y_routed;
         Phase ph(11, st);
-        return hip_status(hx::run_moe_decode(a, cb, mgu | md, st), "hx_moe_layer(decode)");
+        return decode_checked(hip_status(hx::run_moe_decode(a, cb, mgu | md, st), "hx_moe_layer(decode)"), workspace,
+                              stream);
     }
     {
         Phase ph(0, st);

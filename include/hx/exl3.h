@@ -79,8 +79,9 @@ int hx_workspace_init(void* workspace, size_t bytes, hx_stream_t stream);
 /* Whether a bounded wait inside the few-token MoE layer (hx_moe_layer / hx_moe_grouped with T <= 8:
  * a down-projection workgroup waiting for its activations) gave up since the last check: synchronizes
  * `stream`, clears the flag, returns HX_ERR_TIMEOUT if it was set (the results of those calls are
- * then not to be trusted), else 0.  No counterpart in the reference, whose kernels cannot wait on
- * each other. */
+ * then not to be trusted), else 0.  With HX_MOE_SYNC_CHECK=1 in the environment every few-token
+ * hx_moe_layer / hx_moe_grouped call runs this check itself (outside graph capture) and returns its
+ * result (debug option).  No counterpart in the reference, whose kernels cannot wait on each other. */
 int hx_moe_check_status(void* workspace, hx_stream_t stream);
 
 /* Phase profiler (no reference counterpart; the reference times phases with HELIOS_PROF host/event
@@ -132,9 +133,11 @@ int hx_had_r_128(const void* input, void* output, const void* pre_scale, const v
 
 /* ---- router / permutation / reduction ----------------------------------------------------- */
 
-/* Sigmoid top-k: topk_indices int64 [bsz][K], topk_weights fp16 [bsz][K].
- * Replaces helios::aux::routing_ds3_nogroup (src/cuda/aux/routing.cuh:36-49, routing.cu:528-540).
- * use_topk must be 1 and act_fn 0 (sigmoid); E <= 512, K <= 64. */
+/* Router top-k: topk_indices int64 [bsz][K], topk_weights fp16 [bsz][K].  act_fn 0 = sigmoid
+ * (ROUTING_ACT_SIGMOID), 1 = sqrt(softplus) (ROUTING_ACT_SQRTSP); use_topk 0 selects the sorting
+ * variant's key (the activated score; exactly tied activated keys are ordered lower index first,
+ * where the reference's radix network uses its lane order).  E <= 512, K <= 64.
+ * Replaces helios::aux::routing_ds3_nogroup (src/cuda/aux/routing.cuh:36-49, routing.cu:528-540). */
 int hx_routing_ds3_nogroup(const void* scores, const void* bias, int64_t* topk_indices, void* topk_weights,
                            int bsz, int num_experts, int K, float scaling_factor, int use_topk, int act_fn,
                            hx_stream_t stream);

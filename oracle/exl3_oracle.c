@@ -13,6 +13,7 @@
  *   src/cuda/quant/hadamard_inner.cuh:93-279 Hadamard-128                 -> hx_or_had128
  *   src/cuda/quant/exl3_gemm_kernel.cuh:14-31, exl3_gemm_inner.cuh:456-480 -> hx_or_linear
  *   src/cuda/aux/routing.cu:18-76,211-329  sigmoid top-k router           -> hx_or_routing
+ *   src/cuda/aux/routing.cu:18-36,211-443  both activations, both kernels -> hx_or_routing2
  *   src/engine/glue2.cu:244-311,406-414    permute / reduce / swiglu      -> hx_or_permute, ...
  *   src/cuda/quant/exl3_moe_kernel.cuh:57-262, hadamard_inner.cuh:284-481,
  *   src/engine/runner.cpp:723-738,918-958  one MoE layer                  -> hx_or_moe_rows
@@ -301,6 +302,54 @@ static inline uint32_t key_enc(float f)
 }
 
 static double sigmoid_d(double x) { return 1.0 / (1.0 + exp(-x)); }
+
+/* Score activation (routing.cu:18-36): act 0 = sigmoid, act 1 = sqrt(softplus(x)) with softplus's
+ * threshold 20 (x itself above it), both in double then rounded to fp32 as the kernels hold them. */
+static double route_act(double x, int act)
+{
+    if (act == 1) return sqrt(x > 20.0 ? x : log1p(exp(x)));
+    return sigmoid_d(x);
+}
+
+/* routing.cu:211-329 (routing_ds3_nogroup_topk_kernel, use_topk) and routing.cu:333-443
+ * (routing_ds3_nogroup_kernel, the sorting variant), for both score activations (routing.cu:18-36).
+ * Selection key: with a bias, act(logit) + bias in fp32 (both variants); without, the fp16 logit
+ * (use_topk) or act(logit) (sorting variant).  Larger key first; equal keys: lower expert index
+ * first.  Weights: act(logit) normalised over the selection, o * scale / (sum + 1e-20) (use_topk) or
+ * o * (scale / (sum + 1e-20)) (sorting variant), rounded to fp16. */
+void hx_or_routing2(const uint16_t* scores, const uint16_t* bias, int64_t* topk_idx, uint16_t* topk_w,
+                    int bsz, int E, int K, double scale, int use_topk, int act)
+{
+    uint32_t* enc = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)E);
+    char* used = (char*)malloc((size_t)E);
+    for (int r = 0; r < bsz; ++r) {
+        const uint16_t* s = scores + (size_t)r * E;
+        for (int e = 0; e < E; ++e) {
+            float logit = (float)hd(s[e]);
+            float a = (float)route_act(logit, act);
+            float key = bias ? a + (float)hd(bias[e]) : (use_topk ? logit : a);
+            enc[e] = key_enc(key);
+            used[e] = 0;
+        }
+        float o[64];
+        float sum = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            int best = -1;
+            for (int e = 0; e < E; ++e)
+                if (!used[e] && (best < 0 || enc[e] > enc[best])) best = e;
+            used[best] = 1;
+            topk_idx[(size_t)r * K + k] = best;
+            o[k] = (float)route_act(hd(s[best]), act);
+            sum += o[k];
+        }
+        sum += 1e-20f;
+        for (int k = 0; k < K; ++k)
+            topk_w[(size_t)r * K + k] = use_topk ? rh((double)(o[k] * (float)scale / sum))
+                                                 : rh((double)(o[k] * ((float)scale / sum)));
+    }
+    free(enc);
+    free(used);
+}
 
 /* routing.cu:211-329 (routing_ds3_nogroup_topk_kernel, sigmoid activation). */
 void hx_or_routing(const uint16_t* scores, const uint16_t* bias, int64_t* topk_idx, uint16_t* topk_w,

@@ -48,6 +48,8 @@ void     hx_or_linear(double* y /* M*N */, const uint16_t* x /* M*K fp16 */, int
 /* ---- router / permutation / reduction (routing.cu, glue2.cu) ---- */
 void     hx_or_routing(const uint16_t* scores /* bsz*E */, const uint16_t* bias /* E or NULL */,
                        int64_t* topk_idx, uint16_t* topk_w, int bsz, int E, int K, double scale);
+void     hx_or_routing2(const uint16_t* scores, const uint16_t* bias, int64_t* topk_idx, uint16_t* topk_w,
+                        int bsz, int E, int K, double scale, int use_topk, int act);
 void     hx_or_permute(const int64_t* ids, const uint16_t* w, int M, int topk, int E,
                        int64_t* expert_count /* E+1 */, int64_t* token_sorted, uint16_t* weight_sorted,
                        int64_t* route_to_sorted);

@@ -50,6 +50,7 @@ _had = _sig("hx_or_had128", None, [P, C.c_long])
 _had16 = _sig("hx_or_had_r_128_f16", None, [P, P, C.c_long, C.c_long, P, P, C.c_double])
 _linear = _sig("hx_or_linear", None, [P, P, C.c_int, C.c_int, C.c_int, P, P, P, C.c_int, C.c_int, C.c_int])
 _routing = _sig("hx_or_routing", None, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_double])
+_routing2 = _sig("hx_or_routing2", None, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_double, C.c_int, C.c_int])
 _permute = _sig("hx_or_permute", None, [P, P, C.c_int, C.c_int, C.c_int, P, P, P, P])
 _reduce = _sig("hx_or_reduce_sorted", None, [P, P, P, C.c_int, C.c_int, C.c_int])
 _swiglu = _sig("hx_or_swiglu_clamp", None, [P, P, P, C.c_long, C.c_float])
@@ -140,12 +141,18 @@ def linear(x: np.ndarray, trellis: np.ndarray, suh: np.ndarray, svh: np.ndarray,
     return y
 
 
-def routing(scores: np.ndarray, K: int, scale: float, bias: np.ndarray | None = None):
+def routing(scores: np.ndarray, K: int, scale: float, bias: np.ndarray | None = None, use_topk: bool = True,
+            act_fn: int = 0):
+    """act_fn 0 = sigmoid, 1 = sqrt(softplus); use_topk False = the sorting variant (routing.cu:333-443)."""
     s = _u16(scores)
     bsz, E = s.shape
     idx = np.empty((bsz, K), np.int64)
     w = np.empty((bsz, K), np.uint16)
-    _routing(_p(s), _p(None if bias is None else _u16(bias)), _p(idx), _p(w), bsz, E, K, scale)
+    b = None if bias is None else _u16(bias)
+    if use_topk and act_fn == 0:
+        _routing(_p(s), _p(b), _p(idx), _p(w), bsz, E, K, scale)
+    else:
+        _routing2(_p(s), _p(b), _p(idx), _p(w), bsz, E, K, scale, int(use_topk), act_fn)
     return idx, w
 
 

@@ -7,6 +7,10 @@ import pytest
 ROOT = Path(__file__).resolve().parent.parent
 sys.path.insert(0, str(ROOT))
 
+# every few-token MoE call in the tests synchronizes and reports a given-up bounded wait of the
+# decode kernel as an error (hx_moe_check_status), so that no parity test passes on such a call
+os.environ.setdefault("HX_MOE_SYNC_CHECK", "1")
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs through the HIP C ABI)")

@@ -3,7 +3,10 @@ from __future__ import annotations
 
 import numpy as np
 
-TOL = 2e-3  # max-abs error / max|ref| and relative RMS, fp32 accumulate vs fp64 oracle
+# The parity bar: max|got - ref| / max|ref| <= TOL and RMS(got - ref) / RMS(ref) <= TOL over the
+# compared array (a normalised max-abs error, not a per-element relative bound), fp32 accumulate
+# against the fp64 oracle.
+TOL = 2e-3
 
 
 def rng(seed: int) -> np.random.Generator:
@@ -35,3 +38,15 @@ def close(got: np.ndarray, ref: np.ndarray, tol: float = TOL) -> tuple[float, fl
 def assert_close(got, ref, tol: float = TOL, what: str = ""):
     m, r = close(got, ref, tol)
     assert m <= tol and r <= tol, f"{what}: max-abs/max|ref| = {m:.3e}, rel RMS = {r:.3e} (tol {tol})"
+
+
+def zipf_scores(T: int, E: int, s: float, seed: int) -> np.ndarray:
+    """Router logits with Zipf(s)-skewed expert popularity: log of the Zipf
+    popularity of a seeded permutation of the experts plus Gumbel noise, as fp16 [T][E].  The same
+    generator as bench.py's prefill workload."""
+    r = np.random.default_rng(seed)
+    perm = r.permutation(E)
+    pop = np.empty(E)
+    pop[perm] = np.arange(1, E + 1, dtype=np.float64) ** (-s)
+    logits = np.log(pop)[None, :] + r.gumbel(size=(T, E))
+    return logits.astype(np.float16)

@@ -40,7 +40,7 @@ def test_host_side_validation_without_gpu():
     assert r == _lib.HX_ERR_INVALID and b"multiples of 128" in _lib.lib.hx_last_error()
     r = _lib.lib.hx_exl3_gemm(1, 1, ctypes.byref(gw), 1, 128, 128, 2, 1, None, None, 0, None, 0)
     assert r == _lib.HX_ERR_WORKSPACE
-    r = _lib.lib.hx_routing_ds3_nogroup(1, None, 1, 1, 1, 288, 8, 2.5, 0, 0, None)
+    r = _lib.lib.hx_routing_ds3_nogroup(1, None, 1, 1, 1, 288, 8, 2.5, 1, 2, None)
     assert r == _lib.HX_ERR_UNSUPPORTED
     assert _lib.lib.hx_exl3_gemm_workspace_size(1, 2048, 4096) > 0
 

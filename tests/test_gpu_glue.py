@@ -65,6 +65,30 @@ def test_routing_bias_indices(hx, bsz, E, K):
     assert np.abs(gw - rw.view(np.float16).astype(np.float64)).max() <= 2 ** -9 * 2.5
 
 
+@pytest.mark.parametrize("use_topk,act", [(1, 1), (0, 0), (0, 1)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_routing_variants(hx, use_topk, act, with_bias):
+    """The sqrt(softplus) activation (ROUTING_ACT_SQRTSP) and the sorting variant (use_topk = 0,
+    routing.cu:333-443): indices equal to the oracle's, weights within one fp16 ulp; logits past
+    softplus's threshold included."""
+    import torch
+    from oracle import oracle as O
+    bsz, E, K = 64, 288, 8
+    r = np.random.default_rng(31 + 2 * act + use_topk)
+    s = r.standard_normal((bsz, E)).astype(np.float16)
+    s[1, 5] = np.float16(25.0)
+    b = (r.standard_normal(E) * 0.05).astype(np.float16) if with_bias else None
+    idx = torch.empty((bsz, K), dtype=torch.int64, device="cuda")
+    w = torch.empty((bsz, K), dtype=torch.float16, device="cuda")
+    hx.routing_ds3_nogroup(_dev(s), _dev(b) if with_bias else None, idx, w, bsz, E, K, 2.5,
+                           use_topk=bool(use_topk), act_fn=act)
+    torch.cuda.synchronize()
+    ri, rw = O.routing(s, K, 2.5, b, use_topk=bool(use_topk), act_fn=act)
+    assert np.array_equal(idx.cpu().numpy(), ri)
+    gw = w.cpu().float().numpy().astype(np.float64)
+    assert np.abs(gw - rw.view(np.float16).astype(np.float64)).max() <= 2 ** -9 * 2.5
+
+
 @pytest.mark.parametrize("M,E", [(1, 288), (4096, 288), (37, 17)])
 def test_permute_bit_exact(hx, M, E):
     import torch

@@ -298,6 +298,56 @@ def test_routing_bias_brute_force():
     assert not np.array_equal(idx, O.routing(s, K, 2.5)[0])
 
 
+def _route_brute_general(s16, b16, K, scale, use_topk, act):
+    """routing.cu:18-36 activations (sigmoid; sqrt(softplus) with threshold 20), the selection key of
+    routing.cu:240-245 (use_topk) and :366-393 (sorting variant) -- act + bias with a bias, else the
+    logit (use_topk) or act(logit) -- larger first, ties to the lower index; weights act(logit) over
+    the selection in fp32, o * scale / sum (use_topk) or o * (scale / sum)."""
+    f = s16.astype(np.float64)
+    if act == 1:
+        a = np.sqrt(np.where(f > 20.0, f, np.log1p(np.exp(np.minimum(f, 20.0)))))
+    else:
+        a = 1.0 / (1.0 + np.exp(-f))
+    a32 = a.astype(np.float32)
+    if b16 is not None:
+        key = (a32 + b16.astype(np.float32)).astype(np.float32)
+    else:
+        key = f.astype(np.float32) if use_topk else a32
+    order = sorted(range(len(f)), key=lambda e: (-float(key[e]), e))[:K]
+    o = a32[order]
+    tot = np.float32(0.0)
+    for v in o:
+        tot = np.float32(tot + v)
+    tot = np.float32(tot + np.float32(1e-20))
+    sc = np.float32(scale)
+    w = (o * sc / tot) if use_topk else (o * (sc / tot))
+    return np.array(order), w.astype(np.float32).astype(np.float16)
+
+
+@pytest.mark.parametrize("use_topk,act,with_bias", [(1, 1, False), (1, 1, True), (0, 0, False), (0, 0, True),
+                                                    (0, 1, False), (0, 1, True)])
+def test_routing_variants_brute_force(use_topk, act, with_bias):
+    """The router's other activation (sqrt(softplus), DSv4) and the sorting variant (use_topk=false):
+    indices and weights equal a brute-force sort on the closed forms.  Logits above softplus's
+    threshold 20 and a row of large logits (where the sorting variant's activated key saturates and
+    ties differ from the raw-logit order) are included."""
+    r = np.random.default_rng(100 + 10 * use_topk + act)
+    E, K = 288, 8
+    s = r.standard_normal((12, E)).astype(np.float16)
+    s[1, 5] = np.float16(25.0)            # past softplus's threshold
+    s[2, :] = (r.standard_normal(E) * 3 + 22).astype(np.float16)  # sigmoid saturates to 1.0f
+    b = (r.standard_normal(E) * 0.05).astype(np.float16) if with_bias else None
+    idx, w = O.routing(s, K, 2.5, b, use_topk=bool(use_topk), act_fn=act)
+    for row in range(12):
+        bi, bw = _route_brute_general(s[row], b, K, 2.5, use_topk, act)
+        assert np.array_equal(idx[row], bi), row
+        assert np.array_equal(w[row], bw.view(np.uint16)), row
+    if not use_topk and act == 0 and not with_bias:
+        # saturated sigmoid keys tie: the sorting variant takes the lowest indices of the tie,
+        # the use_topk variant the largest logits
+        assert not np.array_equal(idx[2], O.routing(s, K, 2.5)[0][2])
+
+
 # ---------------------------------------------------------------- permutation / reduction
 
 def test_permute_definition():
