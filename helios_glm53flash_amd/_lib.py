@@ -59,6 +59,8 @@ SIGNATURES: dict[str, tuple] = {
     "hx_moe_max_concurrency": (C.c_int, [C.c_int]),
     "hx_gemm_nt_f16": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                  C.c_void_p]),
+    "hx_gather_rows": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    "hx_scatter_add_rows": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     "hx_moe_workspace_size": (C.c_size_t, [C.c_int] * 5),
     "hx_moe_grouped": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                  C.c_void_p, C.c_void_p, C.POINTER(ExpertTablesC)] + [C.c_int] * 12 +

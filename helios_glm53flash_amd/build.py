@@ -72,6 +72,22 @@ def build_hip(jobs: int = 8, force: bool = False) -> Path:
     return LIB
 
 
+DRIVER_SRC = ROOT / "tests" / "cpp" / "compat_driver.cpp"
+DRIVER = ROOT / "tests" / "cpp" / "compat_driver"
+
+
+def build_cpp_driver() -> Path:
+    """The C++ test driver of the reference-signature layer (include/helios/exl3_compat.hpp), linked
+    against the in-tree library (found through its rpath, relative to the driver)."""
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", f"-I{ROOT / 'include'}", str(DRIVER_SRC), "-o",
+           str(DRIVER), f"-L{PKG}", "-lhx_exl3", "-Wl,-rpath,$ORIGIN/../../helios_glm53flash_amd"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("build of tests/cpp/compat_driver failed")
+    return DRIVER
+
+
 def build_oracle() -> Path:
     r = subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], capture_output=True, text=True)
     if r.returncode != 0:
@@ -87,6 +103,7 @@ def main() -> None:
     a = ap.parse_args()
     print(build_hip(a.jobs, a.force))
     print(build_oracle())
+    print(build_cpp_driver())
 
 
 if __name__ == "__main__":

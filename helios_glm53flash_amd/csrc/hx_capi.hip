@@ -306,6 +306,25 @@ int hx_swiglu_clamp(const float* gate, const float* up, void* out, size_t n, flo
                       "hx_swiglu_clamp");
 }
 
+int hx_gather_rows(const void* src, const int64_t* idx, void* dst, int n, int h, hx_stream_t stream)
+{
+    if (n < 0 || h < 0) return fail(HX_ERR_INVALID, "hx_gather_rows: negative extent");
+    if (n > 0 && h > 0 && (!src || !idx || !dst)) return fail(HX_ERR_INVALID, "hx_gather_rows: null pointer");
+    return hip_status(hx::launch_gather_rows(static_cast<const _Float16*>(src), idx, static_cast<_Float16*>(dst), n, h,
+                                             (hipStream_t)stream),
+                      "hx_gather_rows");
+}
+
+int hx_scatter_add_rows(float* y, const float* src, const int64_t* idx, const void* w, int n, int h,
+                        hx_stream_t stream)
+{
+    if (n < 0 || h < 0) return fail(HX_ERR_INVALID, "hx_scatter_add_rows: negative extent");
+    if (n > 0 && h > 0 && (!y || !src || !idx || !w)) return fail(HX_ERR_INVALID, "hx_scatter_add_rows: null pointer");
+    return hip_status(hx::launch_scatter_add_rows(y, src, idx, static_cast<const _Float16*>(w), n, h,
+                                                  (hipStream_t)stream),
+                      "hx_scatter_add_rows");
+}
+
 int hx_gemm_nt_f16(void* y, const void* x, const void* w, int M, int N, int K, int y_fp32, int add,
                    hx_stream_t stream)
 {

@@ -31,7 +31,7 @@ hipError_t launch_reconstruct(_Float16* out, const uint16_t* packed, int packed_
 hipError_t launch_had_r_128(const _Float16* in, _Float16* out, const _Float16* pre, const _Float16* post,
                             long rows, int cols, float r_scale, hipStream_t st);
 hipError_t launch_routing(const _Float16* scores, const _Float16* bias, int64_t* idx, _Float16* w, int bsz, int E,
-                          int K, float scale, hipStream_t st);
+                          int K, float scale, hipStream_t st, bool use_topk = true, int act_fn = 0);
 hipError_t launch_permute(const int64_t* ids, const _Float16* w, int M, int topk, int E, int64_t* expert_count,
                           int64_t* token_sorted, _Float16* weight_sorted, int64_t* route_to_sorted,
                           int64_t* workspace, hipStream_t st);
@@ -48,6 +48,9 @@ hipError_t launch_unpack_trellis(uint16_t* unpacked, const uint16_t* packed, lon
 hipError_t launch_reconstruct_had(_Float16* out, const uint16_t* packed, const _Float16* suh, const _Float16* svh,
                                   int packed_rows, int packed_cols, int unpacked_rows, int unpacked_cols, int bits,
                                   int cb, long n_offset, hipStream_t st);
+hipError_t launch_gather_rows(const _Float16* src, const int64_t* idx, _Float16* dst, int n, int h, hipStream_t st);
+hipError_t launch_scatter_add_rows(float* y, const float* src, const int64_t* idx, const _Float16* w, int n, int h,
+                                   hipStream_t st);
 hipError_t launch_gemm_nt_f16(const _Float16* x, const _Float16* w, void* y, int M, int N, int K, bool y_fp32,
                               bool add, hipStream_t st);
 

@@ -83,11 +83,15 @@ hipError_t launch_had_r_128(const _Float16* in, _Float16* out, const _Float16* p
 
 // ------------------------------------------------------------------ router
 
-// Sigmoid top-k (reference routing.cu:211-329, ROUTING_ACT_SIGMOID).  One wave per token.
-// Selection key without bias is the fp16 logit, with bias sigmoid(logit) + bias.  Order: larger
-// key first using the monotone unsigned encoding of the fp32 key (so +0 ranks above -0), ties to
-// the lower expert index.  Weights: sigmoid(logit) (no bias) or the selected payload, normalised
-// as o * scale / (sum o + 1e-20), rounded to fp16.
+// Router top-k, one wave per token: reference routing_ds3_nogroup_topk_kernel (routing.cu:211-329,
+// use_topk) and routing_ds3_nogroup_kernel (routing.cu:333-443, the sorting variant), for both score
+// activations (ACT 0 sigmoid, 1 sqrt(softplus) with softplus's threshold 20; routing.cu:18-36).
+// Selection key: with a bias act(logit) + bias, else the fp16 logit (use_topk) or act(logit)
+// (sorting variant).  Order: larger key first using the monotone unsigned encoding of the fp32 key
+// (so +0 ranks above -0), ties to the lower expert index.  Weights: act(logit) of the selection,
+// normalised as o * scale / (sum o + 1e-20) (use_topk) or o * (scale / (sum + 1e-20)), in fp16.
+// The reference's sorting variant orders exactly equal activated keys by its radix network's lane
+// order instead; only keys that tie in fp32 can differ.
 HX_INLINE float sigmoid_stable(float x)
 {
     float ez = __expf(-fabsf(x));
@@ -95,6 +99,14 @@ HX_INLINE float sigmoid_stable(float x)
     return x >= 0.0f ? 1.0f - base : base;
 }
 
+template <int ACT>
+HX_INLINE float route_act(float x)
+{
+    if constexpr (ACT == 1) return sqrtf(x > 20.0f ? x : log1pf(__expf(x)));
+    else return sigmoid_stable(x);
+}
+
+template <int ACT, bool SORT>
 __global__ __launch_bounds__(64) void routing_topk_kernel(const _Float16* scores, const _Float16* bias, int64_t* idx,
                                                           _Float16* w, int E, int K, float scale)
 {
@@ -103,20 +115,16 @@ __global__ __launch_bounds__(64) void routing_topk_kernel(const _Float16* scores
     scores += (size_t)row * E;
     constexpr int PER = 8;  // E <= 512
     uint64_t cand[PER];
-    float payload[PER];
+    float act[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int e = lane + 64 * i;
         cand[i] = 0;
-        payload[i] = 0.0f;
+        act[i] = 0.0f;
         if (e < E) {
-            float logit = (float)scores[e];
-            float key = logit;
-            payload[i] = logit;
-            if (bias) {
-                payload[i] = sigmoid_stable(logit);
-                key = payload[i] + (float)bias[e];
-            }
+            const float logit = (float)scores[e];
+            act[i] = route_act<ACT>(logit);
+            const float key = bias ? act[i] + (float)bias[e] : (SORT ? act[i] : logit);
             uint32_t u = __float_as_uint(key);
             u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
             // larger is better: key high, lower index wins ties; +1 keeps valid candidates nonzero
@@ -128,37 +136,38 @@ __global__ __launch_bounds__(64) void routing_topk_kernel(const _Float16* scores
     float sum = 0.0f;
     for (int k = 0; k < K; ++k) {
         uint64_t best = 0;
-        float best_p = 0.0f;
+        float best_a = 0.0f;
 #pragma unroll
         for (int i = 0; i < PER; ++i)
-            if (cand[i] > best) { best = cand[i]; best_p = payload[i]; }
+            if (cand[i] > best) { best = cand[i]; best_a = act[i]; }
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) {
             uint64_t ob = __shfl_xor(best, m, 64);
-            float op = __shfl_xor(best_p, m, 64);
-            if (ob > best) { best = ob; best_p = op; }
+            float oa = __shfl_xor(best_a, m, 64);
+            if (ob > best) { best = ob; best_a = oa; }
         }
         const int e = (int)(0xfffffu + 1u - (uint32_t)(best & 0xffffffffu));
 #pragma unroll
         for (int i = 0; i < PER; ++i)
             if (cand[i] == best) cand[i] = 0;
-        const float o = bias ? best_p : sigmoid_stable(best_p);
-        sum += o;
-        if (lane == k) { o_sel = o; e_sel = e; }
+        sum += best_a;
+        if (lane == k) { o_sel = best_a; e_sel = e; }
     }
     sum += 1e-20f;
     if (lane < K) {
         idx[(size_t)row * K + lane] = e_sel;
-        w[(size_t)row * K + lane] = (_Float16)(o_sel * scale / sum);
+        w[(size_t)row * K + lane] = (_Float16)(SORT ? o_sel * (scale / sum) : o_sel * scale / sum);
     }
 }
 
 hipError_t launch_routing(const _Float16* scores, const _Float16* bias, int64_t* idx, _Float16* w, int bsz, int E,
-                          int K, float scale, hipStream_t st)
+                          int K, float scale, hipStream_t st, bool use_topk, int act_fn)
 {
-    if (E > 512 || K > 64 || K > E || K < 1) return hipErrorInvalidValue;
+    if (E > 512 || K > 64 || K > E || K < 1 || act_fn < 0 || act_fn > 1) return hipErrorInvalidValue;
     if (bsz == 0) return hipSuccess;
-    hipLaunchKernelGGL(routing_topk_kernel, dim3(bsz), dim3(64), 0, st, scores, bias, idx, w, E, K, scale);
+    auto kernel = act_fn == 1 ? (use_topk ? routing_topk_kernel<1, false> : routing_topk_kernel<1, true>)
+                              : (use_topk ? routing_topk_kernel<0, false> : routing_topk_kernel<0, true>);
+    hipLaunchKernelGGL(kernel, dim3(bsz), dim3(64), 0, st, scores, bias, idx, w, E, K, scale);
     return hipGetLastError();
 }
 
@@ -381,6 +390,80 @@ hipError_t launch_swiglu_clamp(const float* g, const float* u, _Float16* out, si
 {
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(swiglu_clamp_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, out, n, limit);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ dense-MoE row glue
+
+// dst[r][:] = src[idx[r]][:] (fp16 rows of h).  Reference glue::gather_rows (src/engine/glue.cu:48-60).
+// 16-byte accesses when h % 8 == 0, else one element per thread.
+__global__ __launch_bounds__(256) void gather_rows_kernel(const _Float16* src, const int64_t* idx, _Float16* dst,
+                                                          long n, int h)
+{
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if ((h & 7) == 0) {
+        const int hv = h >> 3;
+        if (i >= n * hv) return;
+        const long r = i / hv, d = i % hv;
+        reinterpret_cast<hx_u4*>(dst)[r * hv + d] = reinterpret_cast<const hx_u4*>(src)[idx[r] * hv + d];
+    } else {
+        if (i >= n * h) return;
+        const long r = i / h, d = i % h;
+        dst[i] = src[idx[r] * h + d];
+    }
+}
+
+// a * b rounded to fp32 on its own: the empty asm keeps the compiler from fusing it into the add
+// that follows (a fused multiply-add, v_fma_mix_f32 with the fp16 weight, rounds once)
+HX_INLINE float rounded_product(float a, float b)
+{
+    float p = a * b;
+    asm volatile("" : "+v"(p));
+    return p;
+}
+
+// y[idx[r]][:] += fp32(w[r]) * src[r][:], the product and the sum each rounded once (fp32), one
+// writer per element: idx holds distinct rows within a call (reference glue::scatter_add_rows,
+// src/engine/glue.cu:62-82).  4 elements per thread when h % 4 == 0.
+__global__ __launch_bounds__(256) void scatter_add_rows_kernel(float* y, const float* src, const int64_t* idx,
+                                                               const _Float16* w, long n, int h)
+{
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if ((h & 3) == 0) {
+        const int hv = h >> 2;
+        if (i >= n * hv) return;
+        const long r = i / hv, d = i % hv;
+        const float wv = (float)w[r];
+        hx_f4* dst = reinterpret_cast<hx_f4*>(y) + idx[r] * hv + d;
+        const hx_f4 s4 = reinterpret_cast<const hx_f4*>(src)[i];
+        hx_f4 v = *dst;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = v[j] + rounded_product(wv, s4[j]);
+        *dst = v;
+    } else {
+        if (i >= n * h) return;
+        const long r = i / h, d = i % h;
+        float* dst = y + idx[r] * h + d;
+        *dst = *dst + rounded_product((float)w[r], src[i]);
+    }
+}
+
+hipError_t launch_gather_rows(const _Float16* src, const int64_t* idx, _Float16* dst, int n, int h, hipStream_t st)
+{
+    if (n == 0 || h == 0) return hipSuccess;
+    const long work = (long)n * ((h & 7) == 0 ? h / 8 : h);
+    hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, st, src, idx, dst,
+                       (long)n, h);
+    return hipGetLastError();
+}
+
+hipError_t launch_scatter_add_rows(float* y, const float* src, const int64_t* idx, const _Float16* w, int n, int h,
+                                   hipStream_t st)
+{
+    if (n == 0 || h == 0) return hipSuccess;
+    const long work = (long)n * ((h & 3) == 0 ? h / 4 : h);
+    hipLaunchKernelGGL(scatter_add_rows_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, st, y, src, idx,
+                       w, (long)n, h);
     return hipGetLastError();
 }
 

@@ -220,6 +220,29 @@ def swiglu_clamp(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor, n: int
           "hx_swiglu_clamp")
 
 
+def gather_rows(src: torch.Tensor, idx: torch.Tensor, dst: torch.Tensor, n: int, h: int, stream=None) -> None:
+    """dst[r] = src[idx[r]] for r < n, fp16 rows of h (glue.cu:48-60, the dense-MoE row gather)."""
+    _need(src, "src", (torch.float16,))
+    _need(idx, "idx", (torch.int64,))
+    _need(dst, "dst", (torch.float16,))
+    if idx.numel() < n or dst.numel() < n * h:
+        raise ValueError("gather_rows: idx / dst smaller than n / n*h")
+    check(lib.hx_gather_rows(src.data_ptr(), idx.data_ptr(), dst.data_ptr(), n, h, _stream(stream)), "hx_gather_rows")
+
+
+def scatter_add_rows(y: torch.Tensor, src: torch.Tensor, idx: torch.Tensor, w: torch.Tensor, n: int, h: int,
+                     stream=None) -> None:
+    """y[idx[r]] += float(w[r]) * src[r] for r < n (glue.cu:62-82); idx distinct within a call."""
+    _need(y, "y", (torch.float32,))
+    _need(src, "src", (torch.float32,))
+    _need(idx, "idx", (torch.int64,))
+    _need(w, "w", (torch.float16,))
+    if idx.numel() < n or w.numel() < n or src.numel() < n * h:
+        raise ValueError("scatter_add_rows: idx / w / src smaller than n / n / n*h")
+    check(lib.hx_scatter_add_rows(y.data_ptr(), src.data_ptr(), idx.data_ptr(), w.data_ptr(), n, h, _stream(stream)),
+          "hx_scatter_add_rows")
+
+
 def gemm_nt_f16(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor, M: int, N: int, K: int, y_fp32: bool = False,
                 add: bool = False, stream=None) -> None:
     """y[m][n] = sum_k x[m][k] * w[n][k] (glue2.cu:9-65,165-182): the MoE router logits with w the

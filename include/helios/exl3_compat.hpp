@@ -197,6 +197,36 @@ inline void moe_grouped(const void* x, void* y, const int64_t* expert_count, con
           "helios::exl3::moe_grouped");
 }
 
+// The whole single-GPU MoE FFN layer in one call (router, permutation, routed experts, shared
+// expert, ordered combine; hx_moe_layer).  No reference counterpart: it replaces the sequence of
+// runner.cpp:711-959 (Runner::moe_ffn) for one GPU.  shared may be null (no shared expert).
+inline void moe_layer(void* y, float* y_routed, const void* x, const void* scores, const void* bias,
+                      const ExpertTables& tables, const GroupWords* shared, const int* shared_bits, int tokens,
+                      int hidden_dim, int intermediate_dim, int num_experts, int topk, int K_gate, int K_up,
+                      int K_down, float routed_scale, float act_limit = 10.0f, bool mcg = false, bool mul1 = true,
+                      Stream s = 0)
+{
+    const hx_expert_tables t{reinterpret_cast<const void* const*>(tables.gate_trellis),
+                             reinterpret_cast<const void* const*>(tables.gate_suh),
+                             reinterpret_cast<const void* const*>(tables.gate_svh),
+                             reinterpret_cast<const void* const*>(tables.up_trellis),
+                             reinterpret_cast<const void* const*>(tables.up_suh),
+                             reinterpret_cast<const void* const*>(tables.up_svh),
+                             reinterpret_cast<const void* const*>(tables.down_trellis),
+                             reinterpret_cast<const void* const*>(tables.down_suh),
+                             reinterpret_cast<const void* const*>(tables.down_svh),
+                             nullptr, nullptr, nullptr, 0u};
+    hx_group_words sh[3];
+    if (shared)
+        for (int i = 0; i < 3; ++i) sh[i] = hx_group_words{shared[i].trellis, shared[i].suh, shared[i].svh, shared[i].mul1};
+    const size_t ws_bytes = hx_moe_workspace_size(tokens, hidden_dim, intermediate_dim, num_experts, topk);
+    void* ws = Workspace::get().acquire(ws_bytes, s);
+    check(hx_moe_layer(y, y_routed, x, scores, bias, &t, shared ? sh : nullptr, shared_bits, tokens, hidden_dim,
+                       intermediate_dim, num_experts, topk, K_gate, K_up, K_down, routed_scale, act_limit, mcg, mul1,
+                       ws, Workspace::get().size(), (hx_stream_t)s),
+          "helios::exl3::moe_layer");
+}
+
 // reference: src/cuda/quant/hadamard.cuh:14-43 (fp16)
 inline void had_r_128(const void* input, void* output, const void* pre_scale, const void* post_scale, int64_t rows,
                       int cols, float r_scale = 0.088388347648f, Stream s = 0)
@@ -238,6 +268,16 @@ inline void moe_reduce_sorted(float* y, const float* contributions, const int64_
 inline void swiglu_clamp(const float* gate, const float* up, void* out, size_t n, float limit, Stream s = 0)
 {
     exl3::check(hx_swiglu_clamp(gate, up, out, n, limit, (hx_stream_t)s), "helios::glue::swiglu_clamp");
+}
+// reference: src/engine/glue.cuh:14-17 (the dense-MoE fallback, runner.cpp:902-907)
+inline void gather_rows(const void* src, const int64_t* idx, void* dst, int n, int h, Stream s = 0)
+{
+    exl3::check(hx_gather_rows(src, idx, dst, n, h, (hx_stream_t)s), "helios::glue::gather_rows");
+}
+inline void scatter_add_rows(float* y, const float* src, const int64_t* idx, const void* w, int n, int h,
+                             Stream s = 0)
+{
+    exl3::check(hx_scatter_add_rows(y, src, idx, w, n, h, (hx_stream_t)s), "helios::glue::scatter_add_rows");
 }
 // reference: src/engine/glue2.cuh:9-10 (router logits and other dense fp16 NT products)
 inline void gemm_nt_f16(void* y, const void* x, const void* w, int M, int N, int K, bool y_fp32, bool add,

@@ -160,6 +160,17 @@ int hx_moe_reduce_sorted(float* y, const float* contributions, const int64_t* ro
  * Replaces helios::glue::swiglu_clamp (src/engine/glue2.cuh:64, glue2.cu:406-414). */
 int hx_swiglu_clamp(const float* gate, const float* up, void* out, size_t n, float limit, hx_stream_t stream);
 
+/* dst[r][:] = src[idx[r]][:] for r < n, fp16 rows of h elements (the dense-MoE fallback's row
+ * gather).  Replaces helios::glue::gather_rows (src/engine/glue.cuh:14, glue.cu:48-60). */
+int hx_gather_rows(const void* src, const int64_t* idx, void* dst, int n, int h, hx_stream_t stream);
+
+/* y[idx[r]][:] += float(w[r]) * src[r][:] for r < n (fp32 y and src, fp16 w), the product and the sum
+ * each rounded once; idx must hold distinct rows within a call, and calls that share y must be
+ * ordered on one stream.  Replaces helios::glue::scatter_add_rows (src/engine/glue.cuh:16-17,
+ * glue.cu:62-82). */
+int hx_scatter_add_rows(float* y, const float* src, const int64_t* idx, const void* w, int n, int h,
+                        hx_stream_t stream);
+
 /* Dense fp16 NT GEMM y[m][n] = sum_k x[m][k] * w[n][k] (x [M][K], w [N][K] row-major, fp32
  * accumulate): fp16 output rounded once (y_fp32 = 0) or fp32 output, added to y when add != 0.  The
  * MoE router logits (w = the router gate [E][hidden]) are its main use.  K % 32 == 0.

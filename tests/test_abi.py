@@ -53,9 +53,17 @@ def test_cpp_compat_header_compiles_and_links(tmp_path):
     from helios_glm53flash_amd import _lib
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     src = tmp_path / "t.cpp"
-    src.write_text('#include "helios/exl3_compat.hpp"\n'
+    src.write_text('#include "helios/exl3_compat.hpp"\n#include <hip/hip_fp16.h>\n'
                    "int main(int argc, char**) {\n"
                    "  if (argc > 5) {\n"
+                   "    // the dense-MoE fallback's call sites (runner.cpp:902-907) with the engine's half types\n"
+                   "    const half* x = nullptr; half* dense_x = nullptr; const half* wsorted = nullptr;\n"
+                   "    const int64_t* idx = nullptr; float* y = nullptr; const float* dense_d = nullptr;\n"
+                   "    helios::glue::gather_rows(x, idx, dense_x, 4, 4096, nullptr);\n"
+                   "    helios::glue::scatter_add_rows(y, dense_d, idx, wsorted, 4, 4096, nullptr);\n"
+                   "    helios::exl3::ExpertTables t{};\n"
+                   "    helios::exl3::moe_layer(nullptr, nullptr, nullptr, nullptr, nullptr, t, nullptr, nullptr, 1, 4096,"
+                   " 2048, 288, 8, 2, 2, 2, 2.5f);\n"
                    "    helios::exl3::GroupWords w{nullptr, nullptr, nullptr, 0};\n"
                    "    helios::exl3::gemm(nullptr, nullptr, w, 1, 128, 128, 2);\n"
                    "    helios::glue::moe_permute(nullptr, nullptr, 1, 8, 288, nullptr, nullptr, nullptr, nullptr);\n"

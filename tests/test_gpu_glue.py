@@ -174,3 +174,26 @@ def test_moe_max_concurrency_positive():
     from helios_glm53flash_amd._lib import lib
     n = lib.hx_moe_max_concurrency(0)
     assert n == max(1, torch.cuda.get_device_properties(0).multi_processor_count // 8)
+
+
+@pytest.mark.parametrize("h", [4096, 100])
+def test_gather_and_scatter_add_rows(hx, h):
+    """The dense-MoE fallback's row glue (glue.cu:48-82): gather is a copy; scatter-add rounds the
+    product and the sum once each in fp32, so it equals numpy's float32 arithmetic bit for bit."""
+    import torch
+    r = np.random.default_rng(h)
+    rows, n = 64, 40
+    src = r.standard_normal((rows, h)).astype(np.float16)
+    idx = r.permutation(rows)[:n].astype(np.int64)
+    dst = torch.empty((n, h), dtype=torch.float16, device="cuda")
+    hx.gather_rows(_dev(src), _dev(idx), dst, n, h)
+    y0 = r.standard_normal((rows, h)).astype(np.float32)
+    add = r.standard_normal((n, h)).astype(np.float32)
+    w = r.random(n).astype(np.float16)
+    y = _dev(y0)
+    hx.scatter_add_rows(y, _dev(add), _dev(idx), _dev(w), n, h)
+    torch.cuda.synchronize()
+    assert np.array_equal(dst.cpu().numpy(), src[idx])
+    want = y0.copy()
+    want[idx] = want[idx] + (w.astype(np.float32)[:, None] * add)
+    assert np.array_equal(y.cpu().numpy(), want)
