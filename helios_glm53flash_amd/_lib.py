@@ -41,6 +41,9 @@ SIGNATURES: dict[str, tuple] = {
     "hx_exl3_gemm_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
     "hx_exl3_gemm": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(GroupWordsC), C.c_int, C.c_int, C.c_int, C.c_int,
                                C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_size_t]),
+    "hx_exl3_gemm_noalloc_max_bytes": (C.c_size_t, []),
+    "hx_exl3_gemm_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(GroupWordsC), C.c_int, C.c_int, C.c_int,
+                                       C.c_int, C.c_int, C.c_void_p, C.c_int]),
     "hx_exl3_reconstruct_slice": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                             C.c_int, C.c_int64, C.c_void_p]),
     "hx_had_r_128": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_float,

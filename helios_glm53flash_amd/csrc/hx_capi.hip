@@ -4,6 +4,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "../../include/hx/exl3.h"
@@ -204,6 +205,68 @@ int hx_exl3_gemm(void* y, const void* x, const hx_group_words* w, int M, int N, 
     if (r) return r;
     r = hip_status(hx::launch_linear_mfma(ah, tr, svh, y, M, K, N, bits, cb, y_fp32 != 0, st), "hx_exl3_gemm(mfma)");
     return r ? r : HX_GEMM_PATH_MFMA;
+}
+
+}  // extern "C"
+
+// ---- the allocation-free linear: its workspace is a device array of this library, not an argument
+//
+// `scratch` is the workspace of hx_exl3_gemm_noalloc on every GPU this library runs on (each holds
+// its own copy until the process ends).  Host code uses the address hipGetSymbolAddress returns for
+// the current device, never the array's name (on the host that name is not a device address).  The
+// first HX_COUNTER_BYTES are arrival counters: zero when the code object loads (static storage) and
+// left at zero by every kernel that uses them, so no call clears them; the rest (split-K partials,
+// or the transformed activations of the MFMA path) is written before it is read in every call.
+namespace {
+
+constexpr size_t HX_NOALLOC_SCRATCH_BYTES = 8u << 20;
+constexpr int HX_NOALLOC_MAX_DEVICES = 64;
+__device__ __align__(256) static unsigned char scratch[HX_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[HX_NOALLOC_MAX_DEVICES];
+
+// The current device's copy of `scratch`, looked up once per device (with that device current).
+int scratch_ptr(void** out)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= HX_NOALLOC_MAX_DEVICES)
+        return fail(HX_ERR_HIP, "hx_exl3_gemm_noalloc: no current device (or more than 64 devices)");
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_status(e != hipSuccess ? e : hipErrorInvalidSymbol, "hx_exl3_gemm_noalloc(scratch)");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t hx_exl3_gemm_noalloc_max_bytes(void) { return HX_NOALLOC_SCRATCH_BYTES; }
+
+int hx_exl3_gemm_noalloc(void* y, const void* x, const hx_group_words* w, int M, int N, int K, int bits, int y_fp32,
+                         hx_stream_t stream, int mcg)
+{
+    if (M < 0 || N <= 0 || K <= 0) return fail(HX_ERR_INVALID, "hx_exl3_gemm_noalloc: bad extents");
+    const size_t need = hx_exl3_gemm_workspace_size(M, N, K);
+    if (need > HX_NOALLOC_SCRATCH_BYTES) {
+        snprintf(g_err, sizeof(g_err),
+                 "hx_exl3_gemm_noalloc: M=%d N=%d K=%d needs %zu bytes of scratch, more than its %zu (use hx_exl3_gemm "
+                 "with a workspace)",
+                 M, N, K, need, HX_NOALLOC_SCRATCH_BYTES);
+        return HX_ERR_WORKSPACE;
+    }
+    void* ws = nullptr;
+    if (M > 0) {
+        const int r = scratch_ptr(&ws);
+        if (r) return r;
+    }
+    return hx_exl3_gemm(y, x, w, M, N, K, bits, y_fp32, stream, nullptr, mcg, ws, HX_NOALLOC_SCRATCH_BYTES);
 }
 
 int hx_exl3_reconstruct_slice(void* unpacked, const void* packed, int packed_rows, int packed_cols,

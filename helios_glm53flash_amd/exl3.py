@@ -115,6 +115,19 @@ def gemm(y: torch.Tensor, x: torch.Tensor, w: GroupWords, M: int, N: int, K: int
                  "hx_exl3_gemm")
 
 
+def gemm_noalloc(y: torch.Tensor, x: torch.Tensor, w: GroupWords, M: int, N: int, K: int, bits: int,
+                 y_fp32: bool = False, stream=None, mcg: bool = False) -> int:
+    """gemm without a workspace and without allocation (the library's fixed per-GPU scratch array of
+    hx_exl3_gemm_noalloc_max_bytes()); calls overlapping on one GPU race."""
+    _need(x, "x", (torch.float16,))
+    _need(y, "y", (torch.float32,) if y_fp32 else (torch.float16,))
+    if x.numel() < M * K or y.numel() < M * N:
+        raise ValueError("x / y smaller than M*K / M*N")
+    gw = w.c()
+    return check(lib.hx_exl3_gemm_noalloc(y.data_ptr(), x.data_ptr(), C.byref(gw), M, N, K, bits, int(y_fp32),
+                                          _stream(stream), int(mcg)), "hx_exl3_gemm_noalloc")
+
+
 def gemv(y, x, w: GroupWords, M, N, K, bits, y_fp32=False, stream=None, a_had=None, mcg=False) -> None:
     """Forced small-M path (reference gemv, exl3_gemm.cuh:70-83); M must be <= 16."""
     if M > GEMV_MAX_M:

@@ -105,6 +105,17 @@ size_t hx_exl3_gemm_workspace_size(int M, int N, int K);
 int hx_exl3_gemm(void* y, const void* x, const hx_group_words* w, int M, int N, int K, int bits, int y_fp32,
                  hx_stream_t stream, void* a_had, int mcg, void* workspace, size_t workspace_bytes);
 
+/* hx_exl3_gemm without a workspace argument and without any allocation: the scratch memory (arrival
+ * counters, split-K partials, the MFMA path's transformed activations) is a fixed device array of
+ * the library, hx_exl3_gemm_noalloc_max_bytes() = 8 MiB per GPU, held until the process ends.
+ * Calls whose hx_exl3_gemm_workspace_size(M, N, K) exceeds it return HX_ERR_WORKSPACE.  Every call
+ * on one GPU uses that GPU's array: calls that overlap on one GPU (two streams, two host threads)
+ * race.  No counterpart in the reference; it is for callers that cannot allocate, such as code
+ * under graph capture or serving loops that forbid hipMalloc. */
+size_t hx_exl3_gemm_noalloc_max_bytes(void);
+int hx_exl3_gemm_noalloc(void* y, const void* x, const hx_group_words* w, int M, int N, int K, int bits, int y_fp32,
+                         hx_stream_t stream, int mcg);
+
 /* Bit-exact decode of a trellis slice to W_hat fp16 [packed_rows*16][unpacked_cols] (no
  * Hadamard).  Replaces helios::exl3::reconstruct_slice (src/cuda/quant/reconstruct.cuh:15-35,
  * reconstruct.cu:97-142); bits is the reference's K argument. */
