@@ -30,6 +30,10 @@ class ExpertTablesC(C.Structure):
         "down_trellis", "down_suh", "down_svh", "gate_bits", "up_bits", "down_bits")] + [("bits_mask", C.c_uint32)]
 
 
+class ExpertLayoutC(C.Structure):
+    _fields_ = [("off", C.c_uint64 * 12), ("piece", C.c_uint64 * 12), ("bits", C.c_int * 3), ("stride", C.c_uint64)]
+
+
 # name -> (restype, argtypes); the exported symbol set is exactly the declarations of exl3.h
 SIGNATURES: dict[str, tuple] = {
     "hx_version": (C.c_char_p, []),
@@ -64,6 +68,17 @@ SIGNATURES: dict[str, tuple] = {
                                  C.c_void_p]),
     "hx_gather_rows": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     "hx_scatter_add_rows": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    "hx_ckpt_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    "hx_ckpt_close": (None, [C.c_void_p]),
+    "hx_ckpt_tensor_count": (C.c_int, [C.c_void_p]),
+    "hx_ckpt_tensor_info": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int64), C.c_int,
+                                      C.POINTER(C.c_int), C.POINTER(C.c_uint64)]),
+    "hx_ckpt_read": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_uint64]),
+    "hx_ckpt_expert_layout": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(ExpertLayoutC)]),
+    "hx_ckpt_load_experts": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.POINTER(ExpertLayoutC), C.c_void_p,
+                                       C.c_size_t, C.c_int, C.c_void_p]),
+    "hx_ckpt_expert_tables": (C.c_int, [C.POINTER(ExpertLayoutC), C.c_void_p, C.c_int, C.c_void_p,
+                                        C.POINTER(ExpertTablesC), C.c_void_p]),
     "hx_moe_workspace_size": (C.c_size_t, [C.c_int] * 5),
     "hx_moe_grouped": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                  C.c_void_p, C.c_void_p, C.POINTER(ExpertTablesC)] + [C.c_int] * 12 +

@@ -255,3 +255,70 @@ def load_router(shards: ShardSet, layer: int, experts: int, hidden: int, device=
     mean = np.float32(f.astype(np.float64).sum() / f.size)
     b = (f - mean).astype(np.float16)
     return w, torch.from_numpy(b).to(device)
+
+
+# ---------------------------------------------------------------- native loader (C ABI, C++ host code)
+
+class NativeCheckpoint:
+    """The library's C++ loader (hx_ckpt_*: safetensors.hpp / expert_layout.cpp / model.cpp:254-340
+    restated): the path a C++ engine binds.  Same validation as the Python loader above, the
+    reference's one-width-per-projection rule and its 64-byte-aligned slab layout."""
+
+    def __init__(self, directory) -> None:
+        import ctypes as C
+        from ._lib import check, lib
+        self._lib = lib
+        h = C.c_void_p()
+        check(lib.hx_ckpt_open(str(directory).encode(), C.byref(h)), "hx_ckpt_open")
+        self._h = h
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.hx_ckpt_close(self._h)
+            self._h = None
+
+    def __del__(self) -> None:
+        self.close()
+
+    def tensor_count(self) -> int:
+        return self._lib.hx_ckpt_tensor_count(self._h)
+
+    def expert_layout(self, layer: int, experts: int, hidden: int, inter: int):
+        from ._lib import ExpertLayoutC, check
+        import ctypes as C
+        lay = ExpertLayoutC()
+        check(self._lib.hx_ckpt_expert_layout(self._h, layer, experts, hidden, inter, C.byref(lay)),
+              "hx_ckpt_expert_layout")
+        return lay
+
+    def load_experts(self, layer: int, experts: int, hidden: int, inter: int, device="cuda",
+                     readers: int = 8) -> ExpertSet:
+        """Every routed expert of a layer in one device slab (layout of hx_ckpt_expert_layout); the
+        ExpertSet's tensors are views of the slab and its pointer tables come from hx_ckpt_expert_tables."""
+        import ctypes as C
+        from ._lib import ExpertTablesC, check
+        from .exl3 import _stream
+        lay = self.expert_layout(layer, experts, hidden, inter)
+        slab = torch.empty(experts * lay.stride, dtype=torch.uint8, device=device)
+        st = _stream(None)
+        check(self._lib.hx_ckpt_load_experts(self._h, layer, experts, C.byref(lay), slab.data_ptr(), slab.numel(),
+                                             readers, st), "hx_ckpt_load_experts")
+        tables = torch.empty(9 * experts, dtype=torch.int64, device=device)
+        tc = ExpertTablesC()
+        check(self._lib.hx_ckpt_expert_tables(C.byref(lay), slab.data_ptr(), experts, tables.data_ptr(),
+                                              C.byref(tc), st), "hx_ckpt_expert_tables")
+        tr, su, sv, bt = [[], [], []], [[], [], []], [[], [], []], [[], [], []]
+        for e in range(experts):
+            base = e * lay.stride
+            for p in range(3):
+                K, N = (inter, hidden) if p == 2 else (hidden, inter)
+                b = lay.bits[p]
+                ot, os_, ov = (base + lay.off[4 * p + q] for q in range(3))
+                tr[p].append(slab[ot:ot + K * N * b // 8].view(torch.int16).view(K // 16, N // 16, 16 * b))
+                su[p].append(slab[os_:os_ + 2 * K].view(torch.float16))
+                sv[p].append(slab[ov:ov + 2 * N].view(torch.float16))
+                bt[p].append(b)
+        ex = ExpertSet(hidden, inter, tr, su, sv, bt, True)
+        ex._keep = [tables]
+        ex._tables = tc
+        return ex

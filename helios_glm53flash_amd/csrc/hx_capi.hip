@@ -13,7 +13,7 @@
 #include "hx_moe_decode.hpp"
 
 namespace {
-thread_local char g_err[256] = "";
+thread_local char g_err[512] = "";
 
 // Optional phase profiler: HIP events recorded around each phase of hx_moe_layer on its stream.
 struct Prof {
@@ -82,6 +82,11 @@ int codebook(int mcg, int mul1) { return mcg ? 1 : (mul1 ? 2 : 0); }
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 }  // namespace
+
+namespace hx {
+// Error text for hx_last_error from the other translation units of the library.
+void set_error(const char* msg) { snprintf(g_err, sizeof(g_err), "%s", msg); }
+}  // namespace hx
 
 extern "C" {
 

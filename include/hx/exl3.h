@@ -233,6 +233,51 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
                  float routed_scale, float act_limit, int mcg, int mul1, void* workspace, size_t workspace_bytes,
                  hx_stream_t stream);
 
+/* ---- checkpoint loading (host side) -------------------------------------------------------- */
+
+/* A directory of safetensors shards, headers parsed (the index file's weight map names the shards,
+ * else every *.safetensors file by name); tensor data is read on demand.  Replaces
+ * helios::ShardSet::load_dir / find / read (src/core/safetensors.hpp:28-44, safetensors.cpp:35-120). */
+typedef struct hx_ckpt hx_ckpt;
+int hx_ckpt_open(const char* dir, hx_ckpt** out);
+void hx_ckpt_close(hx_ckpt* ckpt);
+int hx_ckpt_tensor_count(const hx_ckpt* ckpt);
+/* dtype codes: 0 F16, 1 BF16, 2 F32, 3 F64, 4 I32, 5 I16, 6 I8, 7 U8, 8 BOOL, 9 I64 */
+int hx_ckpt_tensor_info(const hx_ckpt* ckpt, const char* name, int* dtype, int64_t* shape, int max_dims, int* ndim,
+                        uint64_t* bytes);
+int hx_ckpt_read(const hx_ckpt* ckpt, const char* name, void* host_dst, uint64_t bytes);
+
+/* Slab layout of one layer's routed experts: expert e occupies [e * stride, (e + 1) * stride) of the
+ * slab, piece q = 4 * projection + (0 trellis, 1 suh, 2 svh, 3 mul1) at off[q] with piece[q] bytes,
+ * each projection 64-byte aligned.  Replaces helios::ExpertLayout (src/core/expert_layout.hpp:8-16). */
+typedef struct hx_expert_layout {
+    uint64_t off[12];
+    uint64_t piece[12];
+    int bits[3];
+    uint64_t stride;
+} hx_expert_layout;
+
+/* Validates every routed expert of `layer` (names model.language_model.layers.<l>.mlp.experts.<e>.
+ * {gate,up,down}_proj.{trellis,suh,svh,mul1}, shapes, dtypes, byte sizes, mul1 == 0x83DCD12D, one bit
+ * width per projection across the layer) and returns the slab layout; HX_ERR_INVALID with the tensor's
+ * name otherwise.  Replaces helios::expert_layout (src/core/expert_layout.cpp:6-55); 7-bit experts are
+ * accepted (the reference refuses them: its fused kernels are not built for 7 bits). */
+int hx_ckpt_expert_layout(const hx_ckpt* ckpt, int layer, int experts, int hidden, int intermediate,
+                          hx_expert_layout* out);
+
+/* Copies the layer's experts into a device slab of >= experts * layout.stride bytes (pinned staging,
+ * `readers` reader threads, asynchronous copies on `stream`; returns once the copies are done).
+ * Replaces the expert part of helios Model::load (src/core/model.cpp:254-340), which fills a host
+ * arena for PCIe streaming: here every expert stays resident in HBM. */
+int hx_ckpt_load_experts(const hx_ckpt* ckpt, int layer, int experts, const hx_expert_layout* layout, void* slab,
+                         size_t slab_bytes, int readers, hx_stream_t stream);
+
+/* Writes the nine per-expert pointer arrays of a loaded slab into table_storage (device memory of
+ * 9 * experts pointers) and fills *out for hx_moe_layer / hx_moe_grouped (uniform bit widths:
+ * bits arrays NULL).  The engine's per-layer ExpertTables build (src/engine/runner.cpp:845-866). */
+int hx_ckpt_expert_tables(const hx_expert_layout* layout, const void* slab, int experts, void* table_storage,
+                          hx_expert_tables* out, hx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -181,3 +181,104 @@ def test_router_bias_is_centred_and_gate_converted(tmp_path):
     assert b is None
     assert np.array_equal(w.numpy(), (bf16.astype(np.uint32) << 16).view(np.float32).astype(np.float16))
     assert ck.load_router(ck.ShardSet(tmp_path), 3, E, H, device="cpu") == (None, None)
+
+
+# ---------------------------------------------------------------- the native (C++) loader
+
+def _ref_layout(pieces):
+    """expert_layout.cpp:48-52: pieces in order, each projection's end rounded up to 64 bytes."""
+    off, pos = [], 0
+    for q, n in enumerate(pieces):
+        off.append(pos)
+        pos += n
+        if q % 4 == 3:
+            pos = (pos + 63) & ~63
+    return off, pos
+
+
+def test_native_layout_follows_the_reference(tmp_path):
+    """hx_ckpt_open / hx_ckpt_expert_layout (C++, host only): every tensor found across the shards,
+    the bit widths, piece sizes and offsets of expert_layout.cpp, and the index file's shard list."""
+    from helios_glm53flash_amd import checkpoint as ck
+    E, hidden, inter = 3, 256, 128
+    tensors = make_checkpoint(tmp_path, E=E, hidden=hidden, inter=inter, bits=((2, 3, 4),) * E)
+    nc = ck.NativeCheckpoint(tmp_path)
+    assert nc.tensor_count() == len(tensors)
+    lay = nc.expert_layout(0, E, hidden, inter)
+    assert list(lay.bits) == [2, 3, 4]
+    pieces = []
+    for p, (K, N) in enumerate([(hidden, inter), (hidden, inter), (inter, hidden)]):
+        pieces += [K * N * lay.bits[p] // 8, 2 * K, 2 * N, 4]
+    off, stride = _ref_layout(pieces)
+    assert list(lay.piece) == pieces and list(lay.off) == off and lay.stride == stride
+    # an index file names the shards: an extra, unlisted shard is not read
+    import json
+    names = sorted(p.name for p in tmp_path.glob("*.safetensors"))
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": {"a": names[0]}}))
+    assert ck.NativeCheckpoint(tmp_path).tensor_count() < len(tensors)
+
+
+@pytest.mark.parametrize("defect", ["missing", "mul1", "shape", "dtype", "suh_len", "mixed"])
+def test_native_validation_names_the_tensor(tmp_path, defect):
+    from helios_glm53flash_amd import checkpoint as ck
+    from helios_glm53flash_amd._lib import HxError
+    tensors = make_checkpoint(tmp_path, shards=1, bits=((2, 2, 2),) * 3)
+    bad = f"{PREFIX}.0.mlp.experts.1.up_proj"
+    if defect == "missing":
+        del tensors[bad + ".svh"]
+    elif defect == "mul1":
+        tensors[bad + ".mul1"] = np.array(12345, dtype=np.int32)
+    elif defect == "shape":
+        tensors[bad + ".trellis"] = tensors[bad + ".trellis"][:, :4].copy()
+    elif defect == "dtype":
+        tensors[bad + ".suh"] = tensors[bad + ".suh"].astype(np.float32)
+    elif defect == "suh_len":
+        tensors[bad + ".suh"] = tensors[bad + ".suh"][:128].copy()
+    else:  # another width than expert 0's: the reference's layout has one width per projection
+        tensors[bad + ".trellis"] = np.zeros((256 // 16, 128 // 16, 48), np.int16)
+    for f in tmp_path.glob("*.safetensors"):
+        f.unlink()
+    safetensors_numpy.save_file(tensors, str(tmp_path / "model.safetensors"))
+    nc = ck.NativeCheckpoint(tmp_path)
+    with pytest.raises(HxError, match="experts.1.up_proj"):
+        nc.expert_layout(0, 3, 256, 128)
+
+
+def test_native_rejects_truncated_shard(tmp_path):
+    from helios_glm53flash_amd import checkpoint as ck
+    from helios_glm53flash_amd._lib import HxError
+    make_checkpoint(tmp_path, shards=1)
+    f = next(tmp_path.glob("*.safetensors"))
+    f.write_bytes(f.read_bytes()[:-100])
+    with pytest.raises(HxError, match="data range"):
+        ck.NativeCheckpoint(tmp_path)
+
+
+@pytest.mark.gpu
+def test_native_load_experts_and_layer(tmp_path):
+    """hx_ckpt_load_experts + hx_ckpt_expert_tables: the slab holds every expert's bytes at the
+    layout's offsets, and a layer run on the native tables equals the same layer on the Python
+    loader's (bit for bit)."""
+    import torch
+    from helios_glm53flash_amd import checkpoint as ck
+    from helios_glm53flash_amd import moe
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    E, hidden, inter = 6, 512, 256
+    tensors = make_checkpoint(tmp_path, E=E, hidden=hidden, inter=inter, bits=((2, 2, 3),) * E, shared=None, shards=3)
+    nat = ck.NativeCheckpoint(tmp_path).load_experts(0, E, hidden, inter)
+    py = ck.load_experts(ck.ShardSet(tmp_path), 0, E, hidden, inter)
+    for e in range(E):
+        for p, pn in enumerate(("gate_proj", "up_proj", "down_proj")):
+            base = f"{PREFIX}.0.mlp.experts.{e}.{pn}"
+            assert np.array_equal(nat.trellis[p][e].cpu().numpy(), tensors[base + ".trellis"])
+            assert np.array_equal(nat.suh[p][e].cpu().numpy(), tensors[base + ".suh"])
+            assert np.array_equal(nat.svh[p][e].cpu().numpy(), tensors[base + ".svh"])
+    r = np.random.default_rng(1)
+    for T in (1, 20):
+        x = torch.from_numpy(r.standard_normal((T, hidden)).astype(np.float16)).cuda()
+        s = torch.from_numpy(r.standard_normal((T, E)).astype(np.float16)).cuda()
+        ya = moe.MoeLayer(nat, None, topk=2)(x, s)
+        yb = moe.MoeLayer(py, None, topk=2)(x, s)
+        torch.cuda.synchronize()
+        assert torch.equal(ya, yb), T
