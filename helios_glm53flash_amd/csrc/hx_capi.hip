@@ -479,7 +479,8 @@ int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const i
     if (int r = moe_check(tables, tokens, hidden_dim, intermediate_dim, num_experts, topk, K_gate, K_up, K_down, mcg,
                           mul1, "hx_moe_grouped: bad arguments"))
         return r;
-    if (act_function != 0) return fail(HX_ERR_UNSUPPORTED, "hx_moe_grouped: only act_function 0 (SiLU)");
+    if (act_function < HX_ACT_SILU || act_function > HX_ACT_RELU2_NOGATE)
+        return fail(HX_ERR_UNSUPPORTED, "hx_moe_grouped: act_function must be 0 (SiLU), 1 (GELU) or 2 (relu2, no gate)");
     if (tokens == 0) return 0;  // an empty batch is a no-op (its activation pointers may be null)
     if (!x || !expert_count || !token_sorted || !weight_sorted) return fail(HX_ERR_INVALID, "hx_moe_grouped: null input");
     if (!sorted_contributions && (!y || !route_to_sorted))
@@ -502,6 +503,7 @@ int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const i
         a.route_to_sorted = route_to_sorted;
         fill_tables(tables, a.tr, a.suh, a.svh, a.bits_tab, a.bits_uniform, K_gate, K_up, K_down);
         a.act_limit = act_limit;
+        a.act_fn = act_function;
         if (sorted_contributions) {
             a.contrib = sorted_contributions;
         } else {
@@ -527,6 +529,7 @@ int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const i
     p.r2s = route_to_sorted;
     fill_tables(tables, p.tr, p.suh, p.svh, p.bits_tab, p.bits_uniform, K_gate, K_up, K_down);
     p.act_limit = act_limit;
+    p.act_fn = act_function;
     p.cb = cb;
     p.ws = base;
     p.lay = &L;

@@ -279,3 +279,25 @@ HX_INLINE _Float16 hx_silu_h(_Float16 g)
     _Float16 r = (_Float16)(1.0f / (float)s);
     return (_Float16)((float)g * (float)r);
 }
+
+// Tanh-form GELU of an fp16 value in fp32, rounded to fp16 (hadamard_inner.cuh:342-349):
+// 0.5 x (1 + tanh(y)), y = sqrt(2/pi) (x + 0.044715 x^3), written as x / (1 + exp(-2y)) -- the same
+// function without the cancellation of 1 + tanh(y) at large negative y.
+HX_INLINE _Float16 hx_gelu_h(_Float16 g)
+{
+    const float x = (float)g;
+    const float y = 0.797884560803f * (x + 0.044715f * x * x * x);
+    return (_Float16)(x / (1.0f + __expf(-2.0f * y)));
+}
+
+// Routed-expert activations of the MoE kernels (exl3_moe_common.cuh:6-8).
+enum : int { HX_ACT_SILU = 0, HX_ACT_GELU = 1, HX_ACT_RELU2_NOGATE = 2 };
+
+// The gate lane after activation: SiLU / GELU of the transformed gate, or relu(u) for the
+// non-gated relu2 (hadamard_inner.cuh:365-385); the clamps follow.
+HX_INLINE _Float16 hx_gate_act(int act, _Float16 g, _Float16 u)
+{
+    if (act == HX_ACT_GELU) return hx_gelu_h(g);
+    if (act == HX_ACT_RELU2_NOGATE) return u > (_Float16)0.0f ? u : (_Float16)0.0f;
+    return hx_silu_h(g);
+}

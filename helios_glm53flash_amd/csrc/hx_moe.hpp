@@ -42,6 +42,7 @@ struct PrefillArgs {
     const int32_t* bits_tab[3];
     int bits_uniform[3];
     float act_limit;
+    int act_fn;        // HX_ACT_* of the routed experts
     int cb;
     char* ws;
     const MoeWs* lay;

@@ -70,6 +70,7 @@ struct MoeDecodeArgs {
     const void* sh_svh[3];
     int sh_bits[3];
     float act_limit;
+    int act_fn;                    // routed experts: HX_ACT_SILU, HX_ACT_GELU or HX_ACT_RELU2_NOGATE
     int routed_slots;              // upper bound of active experts = min(E, T*topk)
     // workspace
     int* counter_gu;               // [slots][inter/128]
@@ -502,7 +503,10 @@ __device__ __forceinline__ void guad_epilogue(const MoeDecodeArgs& a, const Deco
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = cg * 128 + 2 * lane;
     const bool shared = si.expert < 0;
-    const hx_h2 sg = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(p.tab.ep[0]) + c);
+    // (the gate's svh of a non-gated expert need not exist)
+    const hx_h2 sg = shared || a.act_fn != HX_ACT_RELU2_NOGATE
+                         ? *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(p.tab.ep[0]) + c)
+                         : hx_h2{(_Float16)0.0f, (_Float16)0.0f};
     const hx_h2 su = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(p.tab.ep[1]) + c);
     const hx_h2 sd = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(p.tab.ep[2]) + c);
     const float L = a.act_limit;
@@ -510,15 +514,20 @@ __device__ __forceinline__ void guad_epilogue(const MoeDecodeArgs& a, const Deco
         hx_h2 p;
         if (!shared) {
             // G, U as fp16 (the reference GEMM writes fp16), transform, fp16, times svh (fp16)
-            hx_h2 G = {(_Float16)cs_g[m * 128 + 2 * lane], (_Float16)cs_g[m * 128 + 2 * lane + 1]};
+            // (the non-gated relu2 has no gate sums: its gate lane comes from u)
             hx_h2 U = {(_Float16)cs_u[m * 128 + 2 * lane], (_Float16)cs_u[m * 128 + 2 * lane + 1]};
-            float g0 = (float)G.x, g1 = (float)G.y, u0 = (float)U.x, u1 = (float)U.y;
-            hx_had128_wave(g0, g1);
+            float u0 = (float)U.x, u1 = (float)U.y;
             hx_had128_wave(u0, u1);
-            hx_h2 g = hx_h2{(_Float16)g0, (_Float16)g1} * sg;
             hx_h2 u = hx_h2{(_Float16)u0, (_Float16)u1} * su;
-            g.x = hx_silu_h(g.x);
-            g.y = hx_silu_h(g.y);
+            hx_h2 g = {(_Float16)0.0f, (_Float16)0.0f};
+            if (a.act_fn != HX_ACT_RELU2_NOGATE) {
+                hx_h2 G = {(_Float16)cs_g[m * 128 + 2 * lane], (_Float16)cs_g[m * 128 + 2 * lane + 1]};
+                float g0 = (float)G.x, g1 = (float)G.y;
+                hx_had128_wave(g0, g1);
+                g = hx_h2{(_Float16)g0, (_Float16)g1} * sg;
+            }
+            g.x = hx_gate_act(a.act_fn, g.x, u.x);
+            g.y = hx_gate_act(a.act_fn, g.y, u.y);
             if (L != 0.0f) {
                 const _Float16 Lh = (_Float16)L, nLh = (_Float16)(-L);
                 u.x = u.x < nLh ? nLh : (u.x > Lh ? Lh : u.x);
@@ -712,30 +721,34 @@ __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodeP
     const int proj = (int)((c / gg) & 1), cg = (int)(c % gg);
     const SlotInfo si = slot_info(a, plan, slot);
     const bool shared = si.expert < 0;
-    if (threadIdx.x < 8)
-        rows[threadIdx.x] = shared ? (int)threadIdx.x : plan.token[si.start + min((int)threadIdx.x, si.count - 1)];
-    hx_lds_barrier();
+    // the non-gated relu2 skips the routed gate GEMM: its gate units only arrive
+    const bool gated = shared || a.act_fn != HX_ACT_RELU2_NOGATE;
+    if (gated || proj == 1) {
+        if (threadIdx.x < 8)
+            rows[threadIdx.x] = shared ? (int)threadIdx.x : plan.token[si.start + min((int)threadIdx.x, si.count - 1)];
+        hx_lds_barrier();
 
-    GemvArgs g;
-    g.x = a.x;
-    g.rows = rows;
-    g.trellis = static_cast<const uint16_t*>(plan.tab.tr);
-    g.suh = static_cast<const _Float16*>(plan.tab.suh);
-    g.M = si.count;
-    g.K = a.hidden;
-    g.N = a.inter;
-    g.pre_transformed = false;
-    gemv_range<BITS, CB, MT, DEC_KS>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
+        GemvArgs g;
+        g.x = a.x;
+        g.rows = rows;
+        g.trellis = static_cast<const uint16_t*>(plan.tab.tr);
+        g.suh = static_cast<const _Float16*>(plan.tab.suh);
+        g.M = si.count;
+        g.K = a.hidden;
+        g.N = a.inter;
+        g.pre_transformed = false;
+        gemv_range<BITS, CB, MT, DEC_KS>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
 
-    // partial of segment i of (slot, proj, cg): partial_{g,u}[((slot*gg + cg) * (KB + 1) + i) * 8 + m][128]
-    float* pbase = (proj == 0 ? a.partial_g : a.partial_u) + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
-    publish_partial<MT>(pbase, si.count, 128, 0, j, cs_g);
+        // partial of segment i of (slot, proj, cg): partial_{g,u}[((slot*gg + cg) * (KB + 1) + i) * 8 + m][128]
+        float* pbase = (proj == 0 ? a.partial_g : a.partial_u) + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
+        publish_partial<MT>(pbase, si.count, 128, 0, j, cs_g);
+    }
     const long cgate = c - proj * gg, cup = cgate + gg;
     const int ng = sp.count(cgate), nu = sp.count(cup);
     if (!arrive_last(&a.counter_gu[slot * gg + cg], ng + nu)) return;
     float* pg = a.partial_g + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
     float* pu = a.partial_u + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
-    gather_partials<MT>(pg, si.count, 128, ng, 0, cs_g);
+    if (gated) gather_partials<MT>(pg, si.count, 128, ng, 0, cs_g);
     gather_partials<MT>(pu, si.count, 128, nu, 0, cs_u);
     guad_epilogue<MT>(a, plan, si, slot, cg, cs_g, cs_u);
     // the activations of this block are stored (device-coherent): flag them for the down phase
@@ -799,7 +812,11 @@ __device__ __forceinline__ void run_unit(const MoeDecodeArgs& a, const DecodePla
     const int slot = unit_slot(a, plan, (int)(gu ? c / (2 * gg) : c / gd));
     if (slot < 0) return;
     int bits = BITS;
-    if constexpr (BITS == 0) bits = slot_bits(a, plan, slot, gu ? (int)((c / gg) & 1) : 2);
+    if constexpr (BITS == 0) {
+        // a skipped gate GEMM (non-gated relu2) dispatches on the up projection's width
+        const int pj = gu ? (a.act_fn == HX_ACT_RELU2_NOGATE && slot != a.routed_slots ? 1 : (int)((c / gg) & 1)) : 2;
+        bits = slot_bits(a, plan, slot, pj);
+    }
     switch (bits) {
 #define HX_SEG_CASE(B)                                                                             \
     case B:                                                                                        \

@@ -99,12 +99,13 @@ __global__ __launch_bounds__(512) void prefill_plan_kernel(const int64_t* expert
 __global__ __launch_bounds__(256) void prefill_gather_kernel(const _Float16* x, const int64_t* token_sorted,
                                                             const int* row_expert, const void* const* suh_g,
                                                             const void* const* suh_u, _Float16* xg, _Float16* xu,
-                                                            int hidden)
+                                                            int hidden, bool gated)
 {
     const long r = blockIdx.x;
     const int e = row_expert[r];
     const _Float16* xr = x + (size_t)token_sorted[r] * hidden;
-    const _Float16* sg = static_cast<const _Float16*>(suh_g[e]);
+    // the non-gated relu2 has no gate GEMM, so no gate input (exl3_moe_kernel.cuh:84-97)
+    const _Float16* sg = static_cast<const _Float16*>(gated ? suh_g[e] : suh_u[e]);
     const _Float16* su = static_cast<const _Float16*>(suh_u[e]);
     _Float16* og = xg + r * hidden;
     _Float16* ou = xu + r * hidden;
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(256) void prefill_gather_kernel(const _Float16* x, 
             oa[j] = (_Float16)a[j];
             ob[j] = (_Float16)b[j];
         }
-        *reinterpret_cast<hx_h8*>(og + c) = oa;
+        if (gated) *reinterpret_cast<hx_h8*>(og + c) = oa;
         *reinterpret_cast<hx_h8*>(ou + c) = ob;
     }
 }
@@ -204,6 +205,7 @@ struct GuArgs {
     int bits_uniform[2];
     int K, N;            // hidden, inter
     float act_limit;
+    int act_fn;          // HX_ACT_SILU, HX_ACT_GELU or HX_ACT_RELU2_NOGATE (no gate GEMM)
     _Float16* act;       // [R][inter] down-projection inputs
     _Float16* g_scratch; // [R][inter] fp16 G, then u, of the tiles in flight
     _Float16* u_scratch;
@@ -267,10 +269,13 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
                     if (row < job.rows) dst[(size_t)row * a.N + col] = f(row, col, acc[mb][nb][r]);
                 }
     };
+    const bool gated = a.act_fn != HX_ACT_RELU2_NOGATE;
     // gate: G = fp16(mapped sum)
-    gu_tile_bits<CB, BM>(bg, a.xg + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[0][e], a.N, cg, sm, acc);
-    frag_store(gs, [&](int row, int, float v) { return (_Float16)mapped(row, v); });
-    __syncthreads();  // rowsum is reused by the up tile
+    if (gated) {
+        gu_tile_bits<CB, BM>(bg, a.xg + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[0][e], a.N, cg, sm, acc);
+        frag_store(gs, [&](int row, int, float v) { return (_Float16)mapped(row, v); });
+        __syncthreads();  // rowsum is reused by the up tile
+    }
     gu_tile_bits<CB, BM>(bu, a.xu + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[1][e], a.N, cg, sm, acc);
 
     // u = fp16(H(U)) * svh_u
@@ -278,35 +283,37 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
     acc_to_lds_f16<BM>(acc, X, [&](int row, int, float v) { return mapped(row, v); });
     __syncthreads();
     hadamard_mfma<BM>(X, H, acc);
-    const _Float16* svg = static_cast<const _Float16*>(a.svh[0][e]) + cg * 128;
+    const _Float16* svg = gated ? static_cast<const _Float16*>(a.svh[0][e]) + cg * 128 : nullptr;
     const _Float16* svu = static_cast<const _Float16*>(a.svh[1][e]) + cg * 128;
     const _Float16* sud = static_cast<const _Float16*>(a.suh_d[e]) + cg * 128;
     frag_store(us, [&](int, int col, float v) { return (_Float16)((_Float16)v * svu[col]); });
     __syncthreads();  // G and u stores done (workgroup scope), X free
     // g = fp16(H(G)) * svh_g
-    for (int i = threadIdx.x; i < BM * 16; i += MF_THREADS) {
-        const int row = i >> 4, c8 = (i & 15) * 8;
-        hx_u4v v = {0u, 0u, 0u, 0u};
-        if (row < job.rows) v = *reinterpret_cast<const hx_u4v*>(gs + (size_t)row * a.N + c8);
-        *reinterpret_cast<hx_u4v*>(&X[row * MF_LDA2 + c8]) = v;
+    if (gated) {
+        for (int i = threadIdx.x; i < BM * 16; i += MF_THREADS) {
+            const int row = i >> 4, c8 = (i & 15) * 8;
+            hx_u4v v = {0u, 0u, 0u, 0u};
+            if (row < job.rows) v = *reinterpret_cast<const hx_u4v*>(gs + (size_t)row * a.N + c8);
+            *reinterpret_cast<hx_u4v*>(&X[row * MF_LDA2 + c8]) = v;
+        }
+        __syncthreads();
+        hadamard_mfma<BM>(X, H, acc);
     }
-    __syncthreads();
-    hadamard_mfma<BM>(X, H, acc);
     const float L = a.act_limit;
     const _Float16 Lh = (_Float16)L, nLh = (_Float16)(-L);
     __syncthreads();
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
         const int col = 64 * wn + 16 * nb + (lane & 15);
-        const _Float16 sg = svg[col], sd = sud[col];
+        const _Float16 sg = gated ? svg[col] : (_Float16)0.0f, sd = sud[col];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = WM * wm + 16 * mb + 4 * (lane >> 4) + r;
-                _Float16 g = (_Float16)acc[mb][nb][r] * sg;
+                _Float16 g = gated ? (_Float16)acc[mb][nb][r] * sg : (_Float16)0.0f;
                 _Float16 uu = row < job.rows ? us[(size_t)row * a.N + col] : (_Float16)0.0f;
-                g = hx_silu_h(g);
+                g = hx_gate_act(a.act_fn, g, uu);
                 if (L != 0.0f) {
                     uu = uu < nLh ? nLh : (uu > Lh ? Lh : uu);
                     g = g > Lh ? Lh : g;
@@ -450,7 +457,7 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
                        p.E, p.R, jobs, njobs, row_expert);
     if (p.R > 0)
         hipLaunchKernelGGL(prefill_gather_kernel, dim3((unsigned)p.R), dim3(256), 0, st, p.x, p.token_sorted,
-                           row_expert, p.suh[0], p.suh[1], xg, xu, p.hidden);
+                           row_expert, p.suh[0], p.suh[1], xg, xu, p.hidden, p.act_fn != HX_ACT_RELU2_NOGATE);
 
     GuArgs gu{};
     gu.jobs = jobs;
@@ -469,6 +476,7 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     gu.K = p.hidden;
     gu.N = p.inter;
     gu.act_limit = p.act_limit;
+    gu.act_fn = p.act_fn;
     gu.act = A;
     gu.g_scratch = G;
     gu.u_scratch = U;

@@ -123,8 +123,9 @@ def moe_workspace_bytes(tokens: int, hidden: int, inter: int, num_experts: int, 
 def moe_grouped(x: torch.Tensor, y: Optional[torch.Tensor], expert_count: torch.Tensor, token_sorted: torch.Tensor,
                 weight_sorted: torch.Tensor, experts: ExpertSet, tokens: int, topk: int, act_limit: float = 10.0,
                 stream=None, sorted_contributions: Optional[torch.Tensor] = None,
-                route_to_sorted: Optional[torch.Tensor] = None, mcg: bool = False) -> None:
-    """Reference moe_grouped: y (fp32) += routed sum, or sorted_contributions (fp32 rows)."""
+                route_to_sorted: Optional[torch.Tensor] = None, mcg: bool = False, act_function: int = 0) -> None:
+    """Reference moe_grouped: y (fp32) += routed sum, or sorted_contributions (fp32 rows).
+    act_function: 0 SiLU, 1 GELU (tanh form), 2 non-gated relu2 (exl3_moe_common.cuh:6-8)."""
     _need(x, "x", (torch.float16,))
     ub = experts.uniform_bits() or (0, 0, 0)
     E = experts.num_experts
@@ -134,7 +135,7 @@ def moe_grouped(x: torch.Tensor, y: Optional[torch.Tensor], expert_count: torch.
     check(lib.hx_moe_grouped(x.data_ptr(), _ptr(y), expert_count.data_ptr(), token_sorted.data_ptr(),
                              weight_sorted.data_ptr(), None, None, None, None, C.byref(experts.tables()), tokens,
                              experts.hidden, experts.inter, E, topk, tokens, 0, ub[0], ub[1], ub[2], int(mcg),
-                             int(mul1), act_limit, 0, -1, _stream(stream), _ptr(sorted_contributions),
+                             int(mul1), act_limit, act_function, -1, _stream(stream), _ptr(sorted_contributions),
                              _ptr(route_to_sorted), ws.data_ptr(), ws.numel()), "hx_moe_grouped")
 
 

@@ -202,7 +202,7 @@ int hx_moe_max_concurrency(int device);
 size_t hx_moe_workspace_size(int tokens, int hidden_dim, int intermediate_dim, int num_experts, int topk);
 
 /* Routed experts of one MoE layer: per expert, gather its rows, input Hadamard with suh_g/suh_u,
- * gate/up GEMMs, SiLU-gate with act_limit clamp, down GEMM, times the routing weight and svh_d.
+ * gate/up GEMMs, activation gate with act_limit clamp, down GEMM, times the routing weight and svh_d.
  * With sorted_contributions (fp32 [tokens*topk][hidden_dim], token_sorted order) each weighted row
  * is written once for a fixed-order reduction (hx_moe_reduce_sorted); without it y (fp32
  * [tokens][hidden_dim]) receives y += the routed sum in ascending routing rank (deterministic;
@@ -211,7 +211,9 @@ size_t hx_moe_workspace_size(int tokens, int hidden_dim, int intermediate_dim, i
  * (src/cuda/quant/exl3_moe.cuh:74-105, exl3_moe.cu:58-265).  temp_* buffers, max_tokens_per_expert,
  * concurrency and num_active are accepted for signature parity and unused (all scratch comes from
  * the workspace; there is no token cap per expert).  Codebooks: mcg or mul1 (as the reference);
- * act_function must be 0 (SiLU).  tokens == 0 is a no-op (the activation pointers may then be NULL). */
+ * act_function (exl3_moe_common.cuh:6-8): 0 SiLU, 1 tanh-form GELU, 2 non-gated relu2 (the gate GEMM
+ * and gate input are skipped; the gate tables must still be valid arrays, their per-expert pointers
+ * are not read).  tokens == 0 is a no-op (the activation pointers may then be NULL). */
 int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const int64_t* token_sorted,
                    const void* weight_sorted, void* temp_state_g, void* temp_state_u, void* temp_intermediate_g,
                    void* temp_intermediate_u, const hx_expert_tables* tables, int tokens, int hidden_dim,

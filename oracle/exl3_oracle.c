@@ -437,8 +437,18 @@ static uint16_t silu_h(uint16_t g)
     return rh(hd(g) * hd(r));
 }
 
+/* tanh-form GELU of an fp16 value, rounded to fp16 (hadamard_inner.cuh:342-349; the reference's
+ * fp32 tanh approximation is restated as the exact function) */
+static uint16_t gelu_h(uint16_t g)
+{
+    double x = hd(g);
+    return rh(0.5 * x * (1.0 + tanh(0.797884560803 * (x + 0.044715 * x * x * x))));
+}
+
+/* act: 0 SiLU, 1 GELU, 2 non-gated relu2 (exl3_moe_common.cuh:6-8; the gate GEMM is skipped and the
+ * gate lane is relu(u), hadamard_inner.cuh:378-382) */
 static void expert_row(double* c_out, const uint16_t* xt, int hidden, int inter,
-                       const hx_or_experts* ex, int e, uint16_t wt, float L)
+                       const hx_or_experts* ex, int e, uint16_t wt, float L, int act)
 {
     uint16_t* ag = (uint16_t*)malloc(2 * (size_t)hidden);
     uint16_t* au = (uint16_t*)malloc(2 * (size_t)hidden);
@@ -449,13 +459,15 @@ static void expert_row(double* c_out, const uint16_t* xt, int hidden, int inter,
     double buf[128];
 
     /* 1. gather + input Hadamard (exl3_moe_kernel.cuh:85-112) */
-    input_had(ag, xt, ex->suh[0][e], hidden);
+    const int gated = act != 2;
+    if (gated) input_had(ag, xt, ex->suh[0][e], hidden);
     input_had(au, xt, ex->suh[1][e], hidden);
     /* 2. G, U with fp16 output, no output transform (exl3_gemm_kernel_inner<..., false>) */
-    matmul_trellis(G, ag, 1, hidden, inter, ex->trellis[0][e], ex->bits[0][e], ex->cb);
+    if (gated) matmul_trellis(G, ag, 1, hidden, inter, ex->trellis[0][e], ex->bits[0][e], ex->cb);
+    else for (int i = 0; i < inter; ++i) G[i] = 0.0;
     matmul_trellis(U, au, 1, hidden, inter, ex->trellis[1][e], ex->bits[1][e], ex->cb);
     /* 3-6. guad (hadamard_inner.cuh:284-413) */
-    const uint16_t* svg = ex->svh[0][e];
+    const uint16_t* svg = gated ? ex->svh[0][e] : NULL;
     const uint16_t* svu = ex->svh[1][e];
     const uint16_t* sud = ex->suh[2][e];
     uint16_t Lh = rh(L), nLh = rh(-L);
@@ -463,12 +475,13 @@ static void expert_row(double* c_out, const uint16_t* xt, int hidden, int inter,
         uint16_t g16[128], u16[128], p16[128];
         for (int j = 0; j < 128; ++j) buf[j] = hd(rh(G[c0 + j]));
         hx_or_had128(buf, 128);
-        for (int j = 0; j < 128; ++j) g16[j] = rh(hd(rh(buf[j])) * hd(svg[c0 + j]));
+        for (int j = 0; j < 128; ++j) g16[j] = gated ? rh(hd(rh(buf[j])) * hd(svg[c0 + j])) : 0;
         for (int j = 0; j < 128; ++j) buf[j] = hd(rh(U[c0 + j]));
         hx_or_had128(buf, 128);
         for (int j = 0; j < 128; ++j) u16[j] = rh(hd(rh(buf[j])) * hd(svu[c0 + j]));
         for (int j = 0; j < 128; ++j) {
-            uint16_t g = silu_h(g16[j]), u = u16[j];
+            uint16_t u = u16[j];
+            uint16_t g = act == 1 ? gelu_h(g16[j]) : act == 2 ? (hd(u) > 0.0 ? u : 0) : silu_h(g16[j]);
             if (L != 0.0f) {
                 if (hd(u) < hd(nLh)) u = nLh;
                 if (hd(u) > hd(Lh)) u = Lh;
@@ -493,7 +506,7 @@ static void expert_row(double* c_out, const uint16_t* xt, int hidden, int inter,
 void hx_or_moe_rows(double* y_routed, uint16_t* y_out16, const uint16_t* x, int hidden, int inter,
                     const int64_t* topk_idx, const uint16_t* topk_w, int topk,
                     const int* rows, int n_rows, const hx_or_experts* ex,
-                    const hx_or_dense_mlp* shared, float act_limit)
+                    const hx_or_dense_mlp* shared, float act_limit, int act)
 {
     double* c = (double*)malloc(sizeof(double) * (size_t)hidden);
     for (int r = 0; r < n_rows; ++r) {
@@ -503,7 +516,7 @@ void hx_or_moe_rows(double* y_routed, uint16_t* y_out16, const uint16_t* x, int 
         float* yf = (float*)calloc((size_t)hidden, sizeof(float));
         for (int j = 0; j < topk; ++j) {
             expert_row(c, xt, hidden, inter, ex, (int)topk_idx[(size_t)t * topk + j],
-                       topk_w[(size_t)t * topk + j], act_limit);
+                       topk_w[(size_t)t * topk + j], act_limit, act);
             /* ordered fp32 reduction, ascending rank (glue2.cu:297-306) */
             for (int i = 0; i < hidden; ++i) yf[i] += (float)c[i];
         }

@@ -80,7 +80,7 @@ typedef struct {
 void     hx_or_moe_rows(double* y_routed, uint16_t* y_out16, const uint16_t* x, int hidden, int inter,
                         const int64_t* topk_idx, const uint16_t* topk_w, int topk,
                         const int* rows, int n_rows, const hx_or_experts* ex,
-                        const hx_or_dense_mlp* shared, float act_limit);
+                        const hx_or_dense_mlp* shared, float act_limit, int act);
 
 /* ---- CPU baseline: fp32-accumulate decode + GEMV, OpenMP (threads<=0: all) ----
  * returns wall seconds of one call. */

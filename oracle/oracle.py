@@ -54,7 +54,7 @@ _routing2 = _sig("hx_or_routing2", None, [P, P, P, P, C.c_int, C.c_int, C.c_int,
 _permute = _sig("hx_or_permute", None, [P, P, C.c_int, C.c_int, C.c_int, P, P, P, P])
 _reduce = _sig("hx_or_reduce_sorted", None, [P, P, P, C.c_int, C.c_int, C.c_int])
 _swiglu = _sig("hx_or_swiglu_clamp", None, [P, P, P, C.c_long, C.c_float])
-_moe = _sig("hx_or_moe_rows", None, [P, P, P, C.c_int, C.c_int, P, P, C.c_int, P, C.c_int, P, P, C.c_float])
+_moe = _sig("hx_or_moe_rows", None, [P, P, P, C.c_int, C.c_int, P, P, C.c_int, P, C.c_int, P, P, C.c_float, C.c_int])
 _cpu_linear = _sig("hx_cpu_linear_f32", C.c_double, [P, P, C.c_int, C.c_int, C.c_int, P, P, P, C.c_int, C.c_int,
                                                       C.c_int])
 _cpu_threads = _sig("hx_cpu_max_threads", C.c_int, [])
@@ -192,9 +192,11 @@ class _Dense(C.Structure):
 
 
 def moe_rows(x: np.ndarray, hidden: int, inter: int, topk_idx: np.ndarray, topk_w: np.ndarray, rows,
-             experts: dict, shared: dict | None, act_limit: float, cb: int = 2):
+             experts: dict, shared: dict | None, act_limit: float, cb: int = 2, act: int = 0):
     """experts: {"trellis": [gate_list, up_list, down_list], "suh": [...], "svh": [...], "bits": [arr_g, arr_u, arr_d]}
     (host numpy arrays per expert); shared: {"trellis": [g, u, d], "suh": [...], "svh": [...], "bits": [bg, bu, bd]}.
+    act: routed activation, 0 SiLU, 1 GELU (tanh form), 2 non-gated relu2 (the gate lists are then
+    not read and may hold any arrays).
     Returns (y_routed fp64 [n_rows][hidden], y_out fp16 bits [n_rows][hidden] or None)."""
     keep = []
     ex = _Experts()
@@ -224,7 +226,7 @@ def moe_rows(x: np.ndarray, hidden: int, inter: int, topk_idx: np.ndarray, topk_
     yo = np.empty((rows.size, hidden), np.uint16) if shared is not None else None
     _moe(_p(yr), _p(yo), _p(_u16(x)), hidden, inter, _p(np.ascontiguousarray(topk_idx, np.int64)),
          _p(_u16(topk_w)), topk_idx.shape[1], _p(rows), rows.size, C.byref(ex),
-         C.byref(sh) if sh is not None else None, act_limit)
+         C.byref(sh) if sh is not None else None, act_limit, act)
     return yr, yo
 
 

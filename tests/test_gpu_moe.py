@@ -162,3 +162,42 @@ def test_moe_decode_config3_several_tokens(hx, T):
     resident workgroups), 2 sampled tokens against the oracle."""
     _run_layer(hx, E=288, hidden=4096, inter=2048, topk=8, T=T, bits=2, shared_bits=2, seed=500 + T,
                rows=[0, T - 1])
+
+
+@pytest.mark.parametrize("act", [1, 2])
+@pytest.mark.parametrize("T", [1, 5, 24, 40])
+def test_moe_grouped_activations(hx, act, T):
+    """act_function 1 (tanh-form GELU) and 2 (non-gated relu2) through hx_moe_grouped, on the
+    few-token decode kernel (T <= 8) and the grouped MFMA path.  For relu2 the gate weights and
+    scales are filled with +inf first: any read of them would poison the output."""
+    import torch
+    from oracle import oracle as O
+    exl3, moe = hx
+    E, hidden, inter, topk = 16, 512, 256, 4
+    ex = moe.ExpertSet.synthetic(E, hidden, inter, 2, seed=900 + T + act)
+    r = np.random.default_rng(900 + T)
+    xh = (r.standard_normal((T, hidden)) * 0.5).astype(np.float16)
+    sh = r.standard_normal((T, E)).astype(np.float16)
+    idx, w = O.routing(sh, topk, 2.5)
+    used = set(int(e) for e in idx.reshape(-1))
+    oe = _oracle_experts(ex, used)
+    if act == 2:
+        for e in range(E):
+            ex.suh[0][e].fill_(float("inf"))
+            ex.svh[0][e].fill_(float("inf"))
+            ex.trellis[0][e].fill_(-1)
+    x = torch.from_numpy(xh).cuda()
+    idx_d = torch.from_numpy(idx).cuda()
+    w_d = torch.from_numpy(w.view(np.float16)).cuda()
+    cnt = torch.empty(E + 1, dtype=torch.int64, device="cuda")
+    ts = torch.empty(T * topk, dtype=torch.int64, device="cuda")
+    wsr = torch.empty(T * topk, dtype=torch.float16, device="cuda")
+    r2s = torch.empty(T * topk, dtype=torch.int64, device="cuda")
+    exl3.moe_permute(idx_d, w_d, T, topk, E, cnt, ts, wsr, None, route_to_sorted=r2s)
+    y = torch.zeros((T, hidden), dtype=torch.float32, device="cuda")
+    moe.moe_grouped(x, y, cnt, ts, wsr, ex, T, topk, act_limit=10.0, route_to_sorted=r2s, act_function=act)
+    torch.cuda.synchronize()
+    ref, _ = O.moe_rows(xh.view(np.uint16), hidden, inter, idx, w, np.arange(T), oe, None, 10.0, act=act)
+    got = y.cpu().numpy()
+    assert np.isfinite(got).all()
+    assert_close(got, ref, what=f"act={act} T={T}")

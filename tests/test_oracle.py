@@ -10,6 +10,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 import scipy.linalg
+import scipy.special
 
 from oracle import oracle as O
 from helpers import make_linear, make_x
@@ -404,9 +405,15 @@ def _silu16(g):
     return _h16(g * _h16(1.0 / s))
 
 
-def _moe_layer_numpy(x, hidden, inter, idx, wt, ex, sh, L):
+def _gelu_erf16(g):
+    """x . Phi(x) (the exact GELU, scipy's erf), rounded to fp16."""
+    return _h16(0.5 * g * (1.0 + scipy.special.erf(g / np.sqrt(2.0))))
+
+
+def _moe_layer_numpy(x, hidden, inter, idx, wt, ex, sh, L, act=None):
     """Dense numpy restatement of one MoE layer from decoded W_hat matrices and scipy's Sylvester
-    Hadamard (exl3_moe_kernel.cuh:57-262, hadamard_inner.cuh:284-481, runner.cpp:723-738,918-958)."""
+    Hadamard (exl3_moe_kernel.cuh:57-262, hadamard_inner.cuh:284-481, runner.cpp:723-738,918-958).
+    act: None SiLU, "gelu_erf" the exact GELU, "relu2" the non-gated relu2 (no gate GEMM)."""
     H = scipy.linalg.hadamard(128).astype(np.float64) / np.sqrt(128.0)
 
     def had(v):
@@ -429,11 +436,14 @@ def _moe_layer_numpy(x, hidden, inter, idx, wt, ex, sh, L):
             su = [ex["suh"][p][e].view(np.float16).astype(np.float64) for p in range(3)]
             sv = [ex["svh"][p][e].view(np.float16).astype(np.float64) for p in range(3)]
             b = [int(ex["bits"][p][e]) for p in range(3)]
-            G = a_in(xd[t], su[0]) @ W(tr[0], hidden, inter, b[0])
             U = a_in(xd[t], su[1]) @ W(tr[1], hidden, inter, b[1])
-            g = _h16(_h16(had(_h16(G))) * sv[0])
             u = _h16(_h16(had(_h16(U))) * sv[1])
-            g = _silu16(g)
+            if act == "relu2":
+                g = np.maximum(u, 0.0)
+            else:
+                G = a_in(xd[t], su[0]) @ W(tr[0], hidden, inter, b[0])
+                g = _h16(_h16(had(_h16(G))) * sv[0])
+                g = _gelu_erf16(g) if act == "gelu_erf" else _silu16(g)
             if L:
                 Lh = float(np.float16(L))
                 u = np.clip(u, -Lh, Lh)
@@ -518,3 +528,49 @@ def test_moe_rows_weight_linearity_and_row_selection():
     w_pair = np.array([[1.0, 1.0]], np.float16).view(np.uint16)
     yp, _ = O.moe_rows(x[:1], hidden, inter, idx2, w_pair, np.arange(1), ex, None, 0.0)
     assert np.array_equal(yp[0], (2 * y1[0].astype(np.float32)).astype(np.float64))
+
+
+def test_moe_rows_gelu_near_exact_gelu():
+    """act 1 (tanh-form GELU): the tanh form stays within 1e-3 of x.Phi(x) (its published maximum
+    deviation is about 5e-4 near |x| = 2), so the layer lands within a few fp16 ulps of the same
+    layer with the exact GELU; and it differs from the SiLU layer (the activation is applied; both tend to x for large x, so
+    the difference is small but well above rounding)."""
+    E, hidden, inter, topk, T = 4, 256, 256, 2, 3
+    ex, _ = _tiny_layer(E, hidden, inter, 60)
+    x = make_x(61, T, hidden)
+    idx, w = O.routing(make_x(62, T, E), topk, 2.5)
+    yr, _ = O.moe_rows(x, hidden, inter, idx, w, np.arange(T), ex, None, 6.0, act=1)
+    y_erf, _ = _moe_layer_numpy(x, hidden, inter, idx, w, ex, None, 6.0, act="gelu_erf")
+    y_silu, _ = O.moe_rows(x, hidden, inter, idx, w, np.arange(T), ex, None, 6.0, act=0)
+    scale = np.abs(y_erf).max()
+    assert scale > 1.0
+    assert np.abs(yr - y_erf).max() <= 1e-2 * scale
+    assert np.abs(yr - y_silu).max() > 0.01 * scale
+
+
+@pytest.mark.parametrize("L", [6.0, 0.0])
+def test_moe_rows_relu2_nogate(L):
+    """act 2 (non-gated relu2): the gate projection is never read (garbage gate weights change
+    nothing), the activation is relu(u) . clamp(u) -- matched by the dense numpy layer -- and,
+    with no limit, halving x quarters the down input before rounding (degree-2 homogeneity,
+    checked on the layer within fp16 rounding)."""
+    E, hidden, inter, topk, T = 4, 256, 256, 2, 3
+    ex, _ = _tiny_layer(E, hidden, inter, 70)
+    x = make_x(71, T, hidden)
+    idx, w = O.routing(make_x(72, T, E), topk, 2.5)
+    yr, _ = O.moe_rows(x, hidden, inter, idx, w, np.arange(T), ex, None, L, act=2)
+    junk = {k: [list(v) for v in ex[k]] if k != "bits" else list(ex[k]) for k in ex}
+    rng = np.random.default_rng(73)
+    junk["trellis"][0] = [rng.integers(0, 65536, t.shape, dtype=np.uint16) for t in ex["trellis"][0]]
+    junk["suh"][0] = [np.full_like(a, 0x7C00) for a in ex["suh"][0]]   # +inf: would poison any read
+    junk["svh"][0] = [np.full_like(a, 0x7C00) for a in ex["svh"][0]]
+    yj, _ = O.moe_rows(x, hidden, inter, idx, w, np.arange(T), junk, None, L, act=2)
+    assert np.array_equal(yr, yj)
+    y_np, _ = _moe_layer_numpy(x, hidden, inter, idx, w, ex, None, L, act="relu2")
+    scale = np.abs(y_np).max()
+    assert scale > 1.0
+    assert np.abs(yr - y_np).max() <= 2e-3 * scale
+    if not L:
+        xh = (x.view(np.float16) * np.float16(0.5)).view(np.uint16)
+        yh, _ = O.moe_rows(xh, hidden, inter, idx, w, np.arange(T), ex, None, 0.0, act=2)
+        assert np.abs(4 * yh - yr).max() <= 2e-2 * scale
