@@ -207,8 +207,10 @@ hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t bits_mask, hipStrea
     if (slots * (a.inter / 128) > 4096 || slots * (a.hidden / 128) > 4096 || a.hidden / 128 > 2048 ||
         slots * (a.inter / 128) > 6080)
         return hipErrorInvalidValue;
-    // one bit width everywhere -> the fixed-width kernel; several -> per-unit dispatch
-    const int bits = (bits_mask & (bits_mask - 1)) ? 0 : __builtin_ctz(bits_mask);
+    // one bit width everywhere -> the fixed-width kernel; several, or the non-gated relu2 (whose gate
+    // units skip their stream) -> per-unit dispatch
+    const bool one = (bits_mask & (bits_mask - 1)) == 0 && a.act_fn != HX_ACT_RELU2_NOGATE;
+    const int bits = one ? __builtin_ctz(bits_mask) : 0;
     if (a.T <= 1) return launch_moe_decode_m1(a, cb, bits, st);
     if (a.T <= 4) return launch_moe_decode_m4(a, cb, bits, st);
     return launch_moe_decode_m8(a, cb, bits, st);

@@ -712,37 +712,17 @@ HX_INLINE int unit_slot(const MoeDecodeArgs& a, const DecodePlan& p, int us)
     return us < p.n ? us : -1;
 }
 
-template <int BITS, int CB, int MT>
-__device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, long c,
-                                           int j, int slot, uint32_t* a_lds, float* cs_g, float* cs_u, int* rows)
+// Arrival of a gate/up unit; the last of a column group's units adds the partial sums and runs the
+// epilogue.  The gate partials exist for all but the routed experts of the non-gated relu2, which
+// only the run-time-width kernel (RT) runs.
+template <int MT, bool RT>
+__device__ __forceinline__ void gu_finish(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, long c,
+                                          int slot, float* cs_g, float* cs_u)
 {
-    const int kb0 = sp.kb_begin(c, j), kb1 = sp.kb_begin(c, j + 1);
     const int gg = a.inter >> 7, KB = a.hidden >> 7;
     const int proj = (int)((c / gg) & 1), cg = (int)(c % gg);
     const SlotInfo si = slot_info(a, plan, slot);
-    const bool shared = si.expert < 0;
-    // the non-gated relu2 skips the routed gate GEMM: its gate units only arrive
-    const bool gated = shared || a.act_fn != HX_ACT_RELU2_NOGATE;
-    if (gated || proj == 1) {
-        if (threadIdx.x < 8)
-            rows[threadIdx.x] = shared ? (int)threadIdx.x : plan.token[si.start + min((int)threadIdx.x, si.count - 1)];
-        hx_lds_barrier();
-
-        GemvArgs g;
-        g.x = a.x;
-        g.rows = rows;
-        g.trellis = static_cast<const uint16_t*>(plan.tab.tr);
-        g.suh = static_cast<const _Float16*>(plan.tab.suh);
-        g.M = si.count;
-        g.K = a.hidden;
-        g.N = a.inter;
-        g.pre_transformed = false;
-        gemv_range<BITS, CB, MT, DEC_KS>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
-
-        // partial of segment i of (slot, proj, cg): partial_{g,u}[((slot*gg + cg) * (KB + 1) + i) * 8 + m][128]
-        float* pbase = (proj == 0 ? a.partial_g : a.partial_u) + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
-        publish_partial<MT>(pbase, si.count, 128, 0, j, cs_g);
-    }
+    const bool gated = !RT || si.expert < 0 || a.act_fn != HX_ACT_RELU2_NOGATE;
     const long cgate = c - proj * gg, cup = cgate + gg;
     const int ng = sp.count(cgate), nu = sp.count(cup);
     if (!arrive_last(&a.counter_gu[slot * gg + cg], ng + nu)) return;
@@ -755,6 +735,36 @@ __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodeP
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_store(&a.ready[slot * gg + cg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Streams gate/up unit (c, j) and publishes its partial sum (gu_finish follows).
+template <int BITS, int CB, int MT>
+__device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, long c,
+                                           int j, int slot, uint32_t* a_lds, float* cs_g, float* cs_u, int* rows)
+{
+    const int kb0 = sp.kb_begin(c, j), kb1 = sp.kb_begin(c, j + 1);
+    const int gg = a.inter >> 7, KB = a.hidden >> 7;
+    const int proj = (int)((c / gg) & 1), cg = (int)(c % gg);
+    const SlotInfo si = slot_info(a, plan, slot);
+    const bool shared = si.expert < 0;
+    if (threadIdx.x < 8)
+        rows[threadIdx.x] = shared ? (int)threadIdx.x : plan.token[si.start + min((int)threadIdx.x, si.count - 1)];
+    hx_lds_barrier();
+
+    GemvArgs g;
+    g.x = a.x;
+    g.rows = rows;
+    g.trellis = static_cast<const uint16_t*>(plan.tab.tr);
+    g.suh = static_cast<const _Float16*>(plan.tab.suh);
+    g.M = si.count;
+    g.K = a.hidden;
+    g.N = a.inter;
+    g.pre_transformed = false;
+    gemv_range<BITS, CB, MT, DEC_KS>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
+
+    // partial of segment i of (slot, proj, cg): partial_{g,u}[((slot*gg + cg) * (KB + 1) + i) * 8 + m][128]
+    float* pbase = (proj == 0 ? a.partial_g : a.partial_u) + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
+    publish_partial<MT>(pbase, si.count, 128, 0, j, cs_g);
 }
 
 template <int BITS, int CB, int MT>
@@ -811,13 +821,14 @@ __device__ __forceinline__ void run_unit(const MoeDecodeArgs& a, const DecodePla
     const int gg = a.inter >> 7, gd = a.hidden >> 7;
     const int slot = unit_slot(a, plan, (int)(gu ? c / (2 * gg) : c / gd));
     if (slot < 0) return;
+    // the non-gated relu2 (run on the BITS = 0 kernel only) has no routed gate GEMM: its gate units
+    // only arrive
+    const bool stream =
+        BITS != 0 || !gu || a.act_fn != HX_ACT_RELU2_NOGATE || slot == a.routed_slots || ((c / gg) & 1) == 1;
     int bits = BITS;
-    if constexpr (BITS == 0) {
-        // a skipped gate GEMM (non-gated relu2) dispatches on the up projection's width
-        const int pj = gu ? (a.act_fn == HX_ACT_RELU2_NOGATE && slot != a.routed_slots ? 1 : (int)((c / gg) & 1)) : 2;
-        bits = slot_bits(a, plan, slot, pj);
-    }
-    switch (bits) {
+    if constexpr (BITS == 0) bits = slot_bits(a, plan, slot, gu ? (int)((c / gg) & 1) : 2);
+    if (stream) {
+        switch (bits) {
 #define HX_SEG_CASE(B)                                                                             \
     case B:                                                                                        \
         if constexpr (BITS == 0 || BITS == B) {                                                    \
@@ -825,14 +836,17 @@ __device__ __forceinline__ void run_unit(const MoeDecodeArgs& a, const DecodePla
             else d_segment<B, CB, MT>(a, plan, sp, c, j, slot, a_lds, cs_g);                         \
         }                                                                                          \
         break;
-        HX_SEG_CASE(1) HX_SEG_CASE(2) HX_SEG_CASE(3) HX_SEG_CASE(4)
-        HX_SEG_CASE(5) HX_SEG_CASE(6) HX_SEG_CASE(7) HX_SEG_CASE(8)
+            HX_SEG_CASE(1) HX_SEG_CASE(2) HX_SEG_CASE(3) HX_SEG_CASE(4)
+            HX_SEG_CASE(5) HX_SEG_CASE(6) HX_SEG_CASE(7) HX_SEG_CASE(8)
 #undef HX_SEG_CASE
-        default: break;
+            default: break;
+        }
     }
+    if (gu) gu_finish<MT, BITS == 0>(a, plan, sp, c, slot, cs_g, cs_u);
 }
 
-// BITS = 0 dispatches each segment on its projection's bit width at run time (mixed-bit layers).
+// BITS = 0 dispatches each segment on its projection's bit width at run time (mixed-bit layers, and
+// every layer of the non-gated relu2).
 template <int BITS, int CB, int MT>
 __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
 {
