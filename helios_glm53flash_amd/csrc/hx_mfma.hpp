@@ -197,6 +197,181 @@ __device__ __forceinline__ void mfma_tile(const _Float16* A, long lda, int rows,
     }
 }
 
+// ---- quarter-operand tile: the decoded weights never leave the registers
+//
+// Same BM x 128 output tile and LDS-staged A as mfma_tile, but each wave owns 32 columns (tile
+// columns 2w, 2w+1) for all BM rows and decodes its own B: lane l = 16g + 8t + q decodes quarter
+// q of the tile in row g (of the chunk's 4 tile rows) and column 2w + t, and the 32 decoded values
+// are four MFMA B operands directly (quarter_operand<nh, kh>: column 8nh + q of tile t, k = 16g +
+// 8kh + 0..7 of the chunk), as in the GEMV core.  The A fragment of operand (rb, kh) is therefore
+// row 16rb + l%16, k = 16(l/16) + 8kh + 0..7.  Only A goes through LDS (stored once, read by the
+// 4 waves); no wave decodes a weight another wave uses, and B costs no LDS traffic at all.
+// Accumulator acc[rb][nh]: lane l holds rows 16rb + 4(l/16) + i, column 32w + 16t + 8nh + q.
+template <int BM>
+HX_INLINE void qt_rowcol(int rb, int nh, int i, int& row, int& col)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    row = 16 * rb + 4 * (lane >> 4) + i;
+    col = 32 * wave + 16 * ((lane >> 3) & 1) + 8 * nh + (lane & 7);
+}
+
+// Chunks of global loads in flight for the quarter-operand tile (2 keeps it at 3 workgroups per CU).
+#ifndef HX_QT_PF
+#define HX_QT_PF 2
+#endif
+constexpr int QT_PF = HX_QT_PF;
+
+// LDS of a kernel that uses only quarter-operand tiles: the A buffers, the epilogue staging.
+struct MfmaSmemQ {
+    union {
+        _Float16 ab[2][MF_BM * MF_LDA];
+        float c[64 * MF_LDC];
+    };
+    float rowsum[MF_BM];
+};
+
+template <int BITS, int CB, int BM, int PF = QT_PF, class Smem>
+__device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int rows, const uint32_t* trellis, int K,
+                                            int N, int tn0, Smem& sm, hx_f4 (&acc)[BM / 16][2])
+{
+    static_assert(BM == 64 || BM == 128, "row tile");
+    constexpr int RB = BM / 16;
+    constexpr int NA = BM / 32;   // 16-byte A loads per thread per chunk
+    constexpr int NW = 8 * BITS;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int tiles_n = N >> 4;
+#pragma unroll
+    for (int i = 0; i < RB; ++i) acc[i][0] = acc[i][1] = hx_f4{0.f, 0.f, 0.f, 0.f};
+
+    const __amdgpu_buffer_rsrc_t ra = mf_rsrc(A, (size_t)max(rows, 0) * lda * sizeof(_Float16));
+    const __amdgpu_buffer_rsrc_t rt = mf_rsrc(trellis, (size_t)(K >> 4) * tiles_n * NW * 4);
+    int a_voff[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int idx = t + MF_THREADS * i;
+        a_voff[i] = (int)(((idx >> 3) * lda + 8 * (idx & 7)) * sizeof(_Float16));
+    }
+    const int g = lane >> 4, tq = (lane >> 3) & 1, q = lane & 7;
+    const int t_off = ((g * tiles_n + tn0 + 2 * wave + tq) * NW) * 4;
+    const int voff0 = t_off + ((q * BITS + NW - 1) % NW) * 4, voff1 = t_off + q * BITS * 4;
+    const int row_bytes = tiles_n * NW * 4;
+
+    hx_u4v av[PF][NA];
+    uint32_t wv[PF][BITS + 1];
+    float rs[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) rs[i] = 0.0f;
+    auto load_chunk = [&](int slot, int k0) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) av[slot][i] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[i], k0 * 2, 0);
+        load_quarter_buf<BITS>(wv[slot], rt, voff0, voff1, (k0 >> 4) * row_bytes);
+    };
+    auto store_a = [&](int slot, int buf, bool count) {
+        _Float16* as = sm.ab[buf];
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            const int idx = t + MF_THREADS * i;
+            *reinterpret_cast<hx_u4v*>(&as[mf_off(idx >> 3, idx & 7)]) = av[slot][i];
+            if (CB == 2 && count) {
+                const hx_h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+                float s = rs[i];
+                s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].x), one, s, false);
+                s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].y), one, s, false);
+                s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].z), one, s, false);
+                s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].w), one, s, false);
+                rs[i] = s;
+            }
+        }
+    };
+    auto decode = [&](int slot, uint32_t* d) {
+        if constexpr (CB == 2) quarter_affine<BITS>(wv[slot], d);
+        else quarter_decode<BITS, CB>(wv[slot], d);
+    };
+
+    const int nk = K / MF_BK;
+#pragma unroll
+    for (int s = 0; s < PF; ++s) load_chunk(s, min(s, nk - 1) * MF_BK);
+    store_a(0, 0, true);
+    // d holds the decoded quarter of the chunk being multiplied; the next chunk's quarter is decoded
+    // while the matrix cores work on this one
+    uint32_t d[16];
+    decode(0, d);
+    hx_lds_barrier();
+    auto step = [&](int c, int u) {
+        load_chunk(u, min(c + PF, nk - 1) * MF_BK);
+        const _Float16* as = sm.ab[c & 1];
+        const hx_h8 b00 = quarter_operand<0, 0>(d), b01 = quarter_operand<0, 1>(d);
+        const hx_h8 b10 = quarter_operand<1, 0>(d), b11 = quarter_operand<1, 1>(d);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int r = 16 * rb + (lane & 15);
+            const hx_h8 a0 = *reinterpret_cast<const hx_h8*>(&as[mf_off(r, 2 * g)]);
+            const hx_h8 a1 = *reinterpret_cast<const hx_h8*>(&as[mf_off(r, 2 * g + 1)]);
+            acc[rb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b00, acc[rb][0], 0, 0, 0);
+            acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b10, acc[rb][1], 0, 0, 0);
+            acc[rb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b01, acc[rb][0], 0, 0, 0);
+            acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b11, acc[rb][1], 0, 0, 0);
+        }
+        decode((u + 1) % PF, d);
+        store_a((u + 1) % PF, (c + 1) & 1, c + 1 < nk);
+        hx_lds_barrier();
+    };
+    const int nmain = nk - nk % PF;
+    for (int c0 = 0; c0 < nmain; c0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) step(c0 + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u < PF - 1; ++u)
+        if (nmain + u < nk) step(nmain + u, u);
+    if constexpr (CB == 2) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            float s = rs[i];
+            s += __shfl_xor(s, 1, 64);
+            s += __shfl_xor(s, 2, 64);
+            s += __shfl_xor(s, 4, 64);
+            if ((t & 7) == 0) sm.rowsum[(t + MF_THREADS * i) >> 3] = s;
+        }
+        __syncthreads();
+    }
+}
+
+// Calls f(row, col, value) for every accumulator element of a quarter-operand tile.
+template <int BM, class F>
+HX_INLINE void qt_foreach(const hx_f4 (&acc)[BM / 16][2], F f)
+{
+#pragma unroll
+    for (int rb = 0; rb < BM / 16; ++rb)
+#pragma unroll
+        for (int nh = 0; nh < 2; ++nh)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                int row, col;
+                qt_rowcol<BM>(rb, nh, i, row, col);
+                f(row, col, acc[rb][nh][i]);
+            }
+}
+
+// Stage rows [64*half, 64*half + 64) of a quarter-operand tile to LDS (sm.c[row - 64*half][col]).
+template <int BM, class Smem>
+HX_INLINE void qt_stage_c_half(const hx_f4 (&acc)[BM / 16][2], int half, Smem& sm)
+{
+#pragma unroll
+    for (int rb = 0; rb < BM / 16; ++rb) {
+        if (16 * rb >= 64 * half && 16 * rb < 64 * half + 64) {
+#pragma unroll
+            for (int nh = 0; nh < 2; ++nh)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    int row, col;
+                    qt_rowcol<BM>(rb, nh, i, row, col);
+                    sm.c[(row - 64 * half) * MF_LDC + col] = acc[rb][nh][i];
+                }
+        }
+    }
+}
+
 // Stage rows [64*half, 64*half + 64) of the accumulated tile to LDS (sm.c[row - 64*half][col]).
 template <int BM>
 HX_INLINE void stage_c_half(const hx_f4 (&acc)[BM / 32][4], int half, MfmaSmem& sm)
@@ -219,8 +394,8 @@ HX_INLINE void stage_c_half(const hx_f4 (&acc)[BM / 32][4], int half, MfmaSmem& 
 }
 
 // Staged value of tile row r (within the half) and column c, with the codebook-2 map applied.
-template <int CB>
-HX_INLINE float staged_value(const MfmaSmem& sm, int half, int r, int c)
+template <int CB, class Smem>
+HX_INLINE float staged_value(const Smem& sm, int half, int r, int c)
 {
     const float v = sm.c[r * MF_LDC + c];
     if constexpr (CB == 2) return fmaf(v, CB2_SCALE, CB2_BIAS * sm.rowsum[64 * half + r]);
@@ -293,6 +468,54 @@ HX_INLINE void hadamard_mfma(const _Float16* x, const _Float16* h, hx_f4 (&y)[BM
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb)
                 y[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mb], bf[nb], y[mb][nb], 0, 0, 0);
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) y[mb][nb] = y[mb][nb] * HX_RSQRT128;
+}
+
+// The same transform with H128 generated in registers instead of read from LDS.  For B operand
+// (nb, kk) lane l holds n = 64wn + 16nb + c (c = l % 16) and k = kk + 8g + j (g = l / 16, j < 8),
+// so popcount(n & k) mod 2 = popcount(c & j & 7) + (c3 g0) + (nb0 g1) + (nb1 kk5) + (wn kk6): a fixed
+// per-lane fragment F (the j-dependent part) times a per-lane sign for each (nb, kk), applied as an
+// XOR of the fp16 sign bits.
+template <int BM>
+HX_INLINE void hadamard_mfma_reg(const _Float16* x, hx_f4 (&y)[BM / 32][4])
+{
+    constexpr int WM = BM / 2, MB = WM / 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int c = lane & 15, g = lane >> 4;
+    uint32_t f[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t s0 = __builtin_popcount(c & (2 * i) & 7) & 1, s1 = __builtin_popcount(c & (2 * i + 1) & 7) & 1;
+        f[i] = (0x3c00u | (s0 << 15)) | ((0x3c00u | (s1 << 15)) << 16);
+    }
+    const uint32_t base = (uint32_t)(((c >> 3) & g) & 1);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) y[mb][nb] = hx_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 128; kk += 32) {
+        hx_h8 af[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+            af[mb] = *reinterpret_cast<const hx_h8*>(&x[(WM * wm + 16 * mb + (lane & 15)) * MF_LDA2 + kk + 8 * g]);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+            const uint32_t sgn = base ^ ((uint32_t)(nb & 1) & (uint32_t)(g >> 1)) ^ (uint32_t)((nb >> 1) & (kk >> 5) & 1) ^
+                                 (uint32_t)(wn & (kk >> 6) & 1);
+            const uint32_t m = sgn ? 0x80008000u : 0u;
+            typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+            const u4v bv = {f[0] ^ m, f[1] ^ m, f[2] ^ m, f[3] ^ m};
+            const hx_h8 bf = __builtin_bit_cast(hx_h8, bv);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+                y[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mb], bf, y[mb][nb], 0, 0, 0);
+        }
     }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)

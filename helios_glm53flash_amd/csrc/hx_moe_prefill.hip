@@ -15,6 +15,10 @@
 #include "hx_kernels.hpp"
 #include "hx_moe.hpp"
 
+#ifndef HX_MF_Q
+#define HX_MF_Q 1
+#endif
+
 namespace hx {
 
 static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -145,17 +149,36 @@ struct GroupedGemmArgs {
     int K, N, nproj;
 };
 
+#if HX_MF_Q
+typedef MfmaSmemQ GemmSmem;
+#ifndef HX_MFQ_OCC
+#define HX_MFQ_OCC 3
+#endif
+#else
+typedef MfmaSmem GemmSmem;
+#define HX_MFQ_OCC 2
+#endif
+
 template <int BITS, int CB, int BM>
-__device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job& job, int proj, int cg, MfmaSmem& sm)
+__device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job& job, int proj, int cg, GemmSmem& sm)
 {
     const _Float16* A = g.A[proj] + (size_t)job.row0 * g.K;
     const uint32_t* tr = static_cast<const uint32_t*>(g.tr[proj][job.expert]);
+#if HX_MF_Q
+    hx_f4 acc[BM / 16][2];
+    mfma_tile_q<BITS, CB, BM>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc);
+#else
     hx_f4 acc[BM / 32][4];
     mfma_tile<BITS, CB, BM>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc);
+#endif
     _Float16* out = g.out[proj] + (size_t)job.row0 * g.N + cg * 128;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int half = 0; half < BM / 64; ++half) {
+#if HX_MF_Q
+        qt_stage_c_half<BM>(acc, half, sm);
+#else
         stage_c_half<BM>(acc, half, sm);
+#endif
         __syncthreads();
         for (int r = wave; r < 64; r += 4) {
             const int row = 64 * half + r;
@@ -168,9 +191,9 @@ __device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job
 }
 
 template <int CB>
-__global__ __launch_bounds__(MF_THREADS, 2) void grouped_gemm_kernel(GroupedGemmArgs g)
+__global__ __launch_bounds__(MF_THREADS, HX_MFQ_OCC) void grouped_gemm_kernel(GroupedGemmArgs g)
 {
-    __shared__ MfmaSmem sm;
+    __shared__ GemmSmem sm;
     const int job_i = blockIdx.y;
     if (job_i >= *g.njobs) return;
     const Job job = g.jobs[job_i];
@@ -211,16 +234,42 @@ struct GuArgs {
     _Float16* u_scratch;
 };
 
+#if HX_MF_Q
+// accumulator of the gate/up tiles (quarter-operand layout); LDS: the tile's A buffers, reused as the
+// staging block of the matrix-core Hadamard transforms (H128 itself is generated in registers)
+template <int BM>
+using GuAcc = hx_f4[BM / 16][2];
+struct GuSmem {
+    union {
+        _Float16 ab[2][MF_BM * MF_LDA];
+        _Float16 hx[128 * MF_LDA2];
+    };
+    float rowsum[MF_BM];
+};
+#ifndef HX_GU_OCC
+#define HX_GU_OCC 3
+#endif
+#else
+template <int BM>
+using GuAcc = hx_f4[BM / 32][4];
+typedef MfmaSmem GuSmem;
+#define HX_GU_OCC 2
+#endif
+
 template <int BITS, int CB, int BM>
 __device__ __forceinline__ void gu_tile(const _Float16* A, int K, int rows, const void* tr, int N, int cg,
-                                        MfmaSmem& sm, hx_f4 (&acc)[BM / 32][4])
+                                        GuSmem& sm, GuAcc<BM>& acc)
 {
+#if HX_MF_Q
+    mfma_tile_q<BITS, CB, BM, QT_PF>(A, K, rows, static_cast<const uint32_t*>(tr), K, N, cg * 8, sm, acc);
+#else
     mfma_tile<BITS, CB, BM>(A, K, rows, static_cast<const uint32_t*>(tr), K, N, cg * 8, sm, acc);
+#endif
 }
 
 template <int CB, int BM>
 __device__ __forceinline__ void gu_tile_bits(int bits, const _Float16* A, int K, int rows, const void* tr, int N,
-                                             int cg, MfmaSmem& sm, hx_f4 (&acc)[BM / 32][4])
+                                             int cg, GuSmem& sm, GuAcc<BM>& acc)
 {
     switch (bits) {
         case 1: gu_tile<1, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
@@ -238,7 +287,7 @@ __device__ __forceinline__ void gu_tile_bits(int bits, const _Float16* A, int K,
 // transform on the matrix cores (hadamard_inner.cuh:284-413 op order: G, U rounded to fp16, H,
 // fp16, times svh in fp16, fp16 SiLU chain, clamps, times suh_d in fp16, H, fp16).
 template <int CB, int BM>
-__device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg, MfmaSmem& sm)
+__device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg, GuSmem& sm)
 {
     constexpr int WM = BM / 2, MB = WM / 16;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -246,14 +295,21 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
     const int e = job.expert;
     const int bg = a.bits_tab[0] ? a.bits_tab[0][e] : a.bits_uniform[0];
     const int bu = a.bits_tab[1] ? a.bits_tab[1][e] : a.bits_uniform[1];
+#if HX_MF_Q
+    _Float16* X = sm.hx;
+#define HX_HAD(dst) hadamard_mfma_reg<BM>(X, dst)
+#else
     _Float16* H = sm.hx;
     _Float16* X = sm.hx + 128 * MF_LDA2;
+#define HX_HAD(dst) hadamard_mfma<BM>(X, H, dst)
+#endif
     auto mapped = [&](int row, float v) -> float {
         if constexpr (CB == 2) return fmaf(v, CB2_SCALE, CB2_BIAS * sm.rowsum[row]);
         else return v;
     };
 
-    hx_f4 acc[MB][4];
+    GuAcc<BM> acc;
+    hx_f4 hacc[MB][4];  // Hadamard results (the matrix-core transform's layout)
     // The fp16 tiles G and then u wait in global scratch (this workgroup's rows and columns only; they
     // stay in L2) instead of registers, which would halve the waves per SIMD of the main loops.
     _Float16* gs = a.g_scratch + (size_t)job.row0 * a.N + cg * 128;
@@ -266,23 +322,35 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int row = WM * wm + 16 * mb + 4 * (lane >> 4) + r, col = 64 * wn + 16 * nb + (lane & 15);
-                    if (row < job.rows) dst[(size_t)row * a.N + col] = f(row, col, acc[mb][nb][r]);
+                    if (row < job.rows) dst[(size_t)row * a.N + col] = f(row, col, hacc[mb][nb][r]);
                 }
     };
     const bool gated = a.act_fn != HX_ACT_RELU2_NOGATE;
     // gate: G = fp16(mapped sum)
     if (gated) {
         gu_tile_bits<CB, BM>(bg, a.xg + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[0][e], a.N, cg, sm, acc);
+#if HX_MF_Q
+        qt_foreach<BM>(acc, [&](int row, int col, float v) {
+            if (row < job.rows) gs[(size_t)row * a.N + col] = (_Float16)mapped(row, v);
+        });
+#else
         frag_store(gs, [&](int row, int, float v) { return (_Float16)mapped(row, v); });
+#endif
         __syncthreads();  // rowsum is reused by the up tile
     }
     gu_tile_bits<CB, BM>(bu, a.xu + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[1][e], a.N, cg, sm, acc);
 
     // u = fp16(H(U)) * svh_u
+#if !HX_MF_Q
     h128_to_lds(H);
+#endif
+#if HX_MF_Q
+    qt_foreach<BM>(acc, [&](int row, int col, float v) { X[row * MF_LDA2 + col] = (_Float16)mapped(row, v); });
+#else
     acc_to_lds_f16<BM>(acc, X, [&](int row, int, float v) { return mapped(row, v); });
+#endif
     __syncthreads();
-    hadamard_mfma<BM>(X, H, acc);
+    HX_HAD(hacc);
     const _Float16* svg = gated ? static_cast<const _Float16*>(a.svh[0][e]) + cg * 128 : nullptr;
     const _Float16* svu = static_cast<const _Float16*>(a.svh[1][e]) + cg * 128;
     const _Float16* sud = static_cast<const _Float16*>(a.suh_d[e]) + cg * 128;
@@ -297,7 +365,7 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
             *reinterpret_cast<hx_u4v*>(&X[row * MF_LDA2 + c8]) = v;
         }
         __syncthreads();
-        hadamard_mfma<BM>(X, H, acc);
+        HX_HAD(hacc);
     }
     const float L = a.act_limit;
     const _Float16 Lh = (_Float16)L, nLh = (_Float16)(-L);
@@ -311,7 +379,7 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = WM * wm + 16 * mb + 4 * (lane >> 4) + r;
-                _Float16 g = gated ? (_Float16)acc[mb][nb][r] * sg : (_Float16)0.0f;
+                _Float16 g = gated ? (_Float16)hacc[mb][nb][r] * sg : (_Float16)0.0f;
                 _Float16 uu = row < job.rows ? us[(size_t)row * a.N + col] : (_Float16)0.0f;
                 g = hx_gate_act(a.act_fn, g, uu);
                 if (L != 0.0f) {
@@ -323,9 +391,9 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
     }
     __syncthreads();
     // act = fp16(H(p)), staged back to LDS for row-wise stores
-    hadamard_mfma<BM>(X, H, acc);
+    HX_HAD(hacc);
     __syncthreads();
-    acc_to_lds_f16<BM>(acc, X, [](int, int, float v) { return v; });
+    acc_to_lds_f16<BM>(hacc, X, [](int, int, float v) { return v; });
     __syncthreads();
     _Float16* out = a.act + (size_t)job.row0 * a.N + cg * 128;
     for (int i = threadIdx.x; i < BM * 16; i += MF_THREADS) {
@@ -334,11 +402,12 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
             *reinterpret_cast<hx_u4v*>(out + (size_t)row * a.N + c8) = *reinterpret_cast<const hx_u4v*>(&X[row * MF_LDA2 + c8]);
     }
 }
+#undef HX_HAD
 
 template <int CB>
-__global__ __launch_bounds__(MF_THREADS, 2) void grouped_gu_kernel(GuArgs a)
+__global__ __launch_bounds__(MF_THREADS, HX_GU_OCC) void grouped_gu_kernel(GuArgs a)
 {
-    __shared__ MfmaSmem sm;
+    __shared__ GuSmem sm;
     const int job_i = blockIdx.y;
     if (job_i >= *a.njobs) return;
     const Job job = a.jobs[job_i];
