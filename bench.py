@@ -152,9 +152,10 @@ def graph_time_us(torch, fn, reps: int = 20, inner: int = 20) -> float:
     """Average microseconds of one fn() call: `inner` calls captured back to back in one HIP graph,
     replayed `reps` times (one call per graph would add the replay's own launch cost, tens of us, to
     every µs-scale kernel).  fn must be capture-safe."""
-    fn()
-    torch.cuda.synchronize()
     stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        fn()  # warm up on the capturing stream: its workspace is allocated outside the capture
+    torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         for _ in range(inner):

@@ -31,8 +31,8 @@ hipError_t launch_input_had(const _Float16* x, const _Float16* suh, _Float16* a,
 }
 
 // Output epilogue for a staged 64-row half: y[row][cg*128 + c] = svh . H128(C[row][:]).
-template <int CB>
-__device__ void linear_tile_epilogue(const MfmaSmem& sm, int half, int rows, const _Float16* svh, void* y, int N,
+template <int CB, class Smem>
+__device__ void linear_tile_epilogue(const Smem& sm, int half, int rows, const _Float16* svh, void* y, int N,
                                      int cg, bool y_fp32)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -53,20 +53,22 @@ __device__ void linear_tile_epilogue(const MfmaSmem& sm, int half, int rows, con
     }
 }
 
+// Quarter-operand tile (each wave decodes its own 32 columns into MFMA B operands; only A is staged
+// in LDS), three workgroups per CU.
 template <int BITS, int CB>
-__global__ __launch_bounds__(MF_THREADS, 2) void linear_mfma_kernel(const _Float16* a, const uint32_t* trellis,
+__global__ __launch_bounds__(MF_THREADS, 3) void linear_mfma_kernel(const _Float16* a, const uint32_t* trellis,
                                                                 const _Float16* svh, void* y, int M, int K, int N,
                                                                 bool y_fp32)
 {
-    __shared__ MfmaSmem sm;
+    __shared__ MfmaSmemQ sm;
     const int cg = blockIdx.x;
     const int m0 = blockIdx.y * MF_BM;
     const int rows = min(MF_BM, M - m0);
-    hx_f4 acc[MF_BM / 32][4];
-    mfma_tile<BITS, CB, MF_BM>(a + (size_t)m0 * K, K, rows, trellis, K, N, cg * 8, sm, acc);
+    hx_f4 acc[MF_BM / 16][2];
+    mfma_tile_q<BITS, CB, MF_BM>(a + (size_t)m0 * K, K, rows, trellis, K, N, cg * 8, sm, acc);
     void* yt = y_fp32 ? (void*)(static_cast<float*>(y) + (size_t)m0 * N) : (void*)(static_cast<_Float16*>(y) + (size_t)m0 * N);
     for (int half = 0; half < 2; ++half) {
-        stage_c_half<MF_BM>(acc, half, sm);
+        qt_stage_c_half<MF_BM>(acc, half, sm);
         __syncthreads();
         linear_tile_epilogue<CB>(sm, half, rows, svh, yt, N, cg, y_fp32);
         __syncthreads();

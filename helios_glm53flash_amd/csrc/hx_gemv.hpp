@@ -247,6 +247,18 @@ HX_INLINE void quarter_affine_pairs(const uint32_t* r, const uint32_t* M, uint32
     }
 }
 
+// Positions [P0, P1) of quarter_affine_pairs (for spreading a quarter's decode over a loop).
+template <int BITS, int P0, int P1>
+HX_INLINE void quarter_affine_range(const uint32_t* r, const uint32_t* M, uint32_t* out)
+{
+    if constexpr (P0 < P1) {
+        const uint32_t x0 = quarter_window<BITS, P0>(r, M) * 0x83DCD12Du;
+        const uint32_t x1 = quarter_window<BITS, P0 + 1>(r, M) * 0x83DCD12Du;
+        out[P0 / 2] = __builtin_amdgcn_sad_hi_u8(x1, 0u, __builtin_amdgcn_sad_u8(x0, 0u, 0x64006400u));
+        quarter_affine_range<BITS, P0 + 2, P1>(r, M, out);
+    }
+}
+
 // h of a quarter as fp16 pairs: out[i] = positions (2i, 2i+1) = (k, k+1) of one column.
 template <int BITS>
 HX_INLINE void quarter_affine(const uint32_t* r, uint32_t* out)

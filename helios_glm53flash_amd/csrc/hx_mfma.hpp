@@ -18,6 +18,8 @@
 #pragma once
 #include "hx_gemv.hpp"
 
+#include <utility>
+
 namespace hx {
 
 constexpr int MF_THREADS = 256;
@@ -220,6 +222,15 @@ HX_INLINE void qt_rowcol(int rb, int nh, int i, int& row, int& col)
 #define HX_QT_PF 2
 #endif
 constexpr int QT_PF = HX_QT_PF;
+#ifndef HX_QT_SCHED
+#define HX_QT_SCHED 0
+#endif
+#ifndef HX_QT_ILV_MAXBITS
+#define HX_QT_ILV_MAXBITS 3  // wider words leave too few registers for two decoded quarters
+#endif
+#ifndef HX_QT_ILV
+#define HX_QT_ILV 1
+#endif
 
 // LDS of a kernel that uses only quarter-operand tiles: the A buffers, the epilogue staging.
 struct MfmaSmemQ {
@@ -230,9 +241,12 @@ struct MfmaSmemQ {
     float rowsum[MF_BM];
 };
 
-template <int BITS, int CB, int BM, int PF = QT_PF, class Smem>
+// With rs_src (codebook 2), the row sums of A come precomputed as rs_n fp32 partial sums per row
+// (rs_src[r * rs_n + b]) instead of being accumulated from the staged A.
+template <int BITS, int CB, int BM, int PF = QT_PF, bool EXT_RS = false, class Smem>
 __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int rows, const uint32_t* trellis, int K,
-                                            int N, int tn0, Smem& sm, hx_f4 (&acc)[BM / 16][2])
+                                            int N, int tn0, Smem& sm, hx_f4 (&acc)[BM / 16][2],
+                                            const float* rs_src = nullptr, int rs_n = 0)
 {
     static_assert(BM == 64 || BM == 128, "row tile");
     constexpr int RB = BM / 16;
@@ -272,7 +286,7 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
         for (int i = 0; i < NA; ++i) {
             const int idx = t + MF_THREADS * i;
             *reinterpret_cast<hx_u4v*>(&as[mf_off(idx >> 3, idx & 7)]) = av[slot][i];
-            if (CB == 2 && count) {
+            if (CB == 2 && !EXT_RS && count) {
                 const hx_h2 one = {(_Float16)1.0f, (_Float16)1.0f};
                 float s = rs[i];
                 s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].x), one, s, false);
@@ -289,6 +303,17 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
     };
 
     const int nk = K / MF_BK;
+    float rs_ext = 0.0f;  // row t's precomputed sum (requested before the tile streams)
+    if constexpr (CB == 2 && EXT_RS) {
+        if (t < BM && t < rows)
+            for (int b0 = 0; b0 < rs_n; b0 += 16) {  // 16 independent loads per round trip
+                float v[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[j] = b0 + j < rs_n ? rs_src[(size_t)t * rs_n + b0 + j] : 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) rs_ext += v[j];
+            }
+    }
 #pragma unroll
     for (int s = 0; s < PF; ++s) load_chunk(s, min(s, nk - 1) * MF_BK);
     store_a(0, 0, true);
@@ -297,6 +322,51 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
     uint32_t d[16];
     decode(0, d);
     hx_lds_barrier();
+#if HX_QT_ILV
+    if constexpr (CB == 2 && PF % 2 == 0 && BITS <= HX_QT_ILV_MAXBITS) {
+        // Codebook 2: the next quarter's decode is spread between this chunk's MFMAs in program
+        // order (2 of its 16 pairs after each 16-row block for BM = 128), so the wave issues VALU
+        // work while its matrix-core ops run instead of parking it behind the last MFMA (issue is in
+        // order).  The decoded quarters alternate between d and dn (PF even: chunk parity = slot
+        // parity).
+        uint32_t dn[16];
+        auto step2 = [&](int c, int u, uint32_t* dc, uint32_t* dx) {
+            load_chunk(u, min(c + PF, nk - 1) * MF_BK);
+            const _Float16* as = sm.ab[c & 1];
+            const hx_h8 b00 = quarter_operand<0, 0>(dc), b01 = quarter_operand<0, 1>(dc);
+            const hx_h8 b10 = quarter_operand<1, 0>(dc), b11 = quarter_operand<1, 1>(dc);
+            const uint32_t* wn = wv[(u + 1) % PF];
+            uint32_t M[BITS + 1];
+#pragma unroll
+            for (int j = 1; j <= BITS; ++j) M[j] = __builtin_amdgcn_alignbit(wn[j - 1], wn[j], 16);
+            auto block = [&](auto rbc) {
+                constexpr int rb = decltype(rbc)::value;
+                const int r = 16 * rb + (lane & 15);
+                const hx_h8 a0 = *reinterpret_cast<const hx_h8*>(&as[mf_off(r, 2 * g)]);
+                const hx_h8 a1 = *reinterpret_cast<const hx_h8*>(&as[mf_off(r, 2 * g + 1)]);
+                acc[rb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b00, acc[rb][0], 0, 0, 0);
+                acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b10, acc[rb][1], 0, 0, 0);
+                acc[rb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b01, acc[rb][0], 0, 0, 0);
+                acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b11, acc[rb][1], 0, 0, 0);
+                quarter_affine_range<BITS, 32 * rb / RB, 32 * (rb + 1) / RB>(wn, M, dx);
+            };
+            [&]<int... I>(std::integer_sequence<int, I...>) {
+                (block(std::integral_constant<int, I>{}), ...);
+            }(std::make_integer_sequence<int, RB>{});
+            store_a((u + 1) % PF, (c + 1) & 1, c + 1 < nk);
+            hx_lds_barrier();
+        };
+        const int nmain = nk - nk % PF;
+        for (int c0 = 0; c0 < nmain; c0 += PF) {
+#pragma unroll
+            for (int u = 0; u < PF; ++u) step2(c0 + u, u, (u & 1) ? dn : d, (u & 1) ? d : dn);
+        }
+#pragma unroll
+        for (int u = 0; u < PF - 1; ++u)
+            if (nmain + u < nk) step2(nmain + u, u, (u & 1) ? dn : d, (u & 1) ? d : dn);
+    } else
+#endif
+    {
     auto step = [&](int c, int u) {
         load_chunk(u, min(c + PF, nk - 1) * MF_BK);
         const _Float16* as = sm.ab[c & 1];
@@ -313,6 +383,23 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
             acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b11, acc[rb][1], 0, 0, 0);
         }
         decode((u + 1) % PF, d);
+#if HX_QT_SCHED
+        // issue order: the next quarter's decode interleaved between this chunk's MFMAs, so that the
+        // wave issues VALU work while its matrix-core ops run (in-order issue would otherwise park
+        // the decode behind the last MFMA)
+        {
+            constexpr int NV = HX_QT_SCHED * (BM == 128 ? 1 : 2);
+#pragma unroll
+            for (int i = 0; i < RB; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
+                }
+            }
+        }
+#endif
         store_a((u + 1) % PF, (c + 1) & 1, c + 1 < nk);
         hx_lds_barrier();
     };
@@ -324,7 +411,11 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
 #pragma unroll
     for (int u = 0; u < PF - 1; ++u)
         if (nmain + u < nk) step(nmain + u, u);
-    if constexpr (CB == 2) {
+    }
+    if constexpr (CB == 2 && EXT_RS) {
+        if (t < BM) sm.rowsum[t] = rs_ext;
+        __syncthreads();
+    } else if constexpr (CB == 2) {
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
             float s = rs[i];

@@ -40,6 +40,7 @@ void MoeWs::prefill_layout(size_t o)
     off_G = o;          o = al(o + sizeof(_Float16) * (size_t)R * inter);
     off_U = o;          o = al(o + sizeof(_Float16) * (size_t)R * inter);
     off_A = o;          o = al(o + sizeof(_Float16) * (size_t)R * inter);
+    off_rs = o;         o = al(o + sizeof(float) * (size_t)R * (2 + inter / 128));
     off_D = off_xg;     // D reuses xg (xg is consumed by the gate GEMM before the down GEMM runs)
     off_sh_a = o;       o = al(o + sizeof(_Float16) * (size_t)T * kmax);
     off_sh_g = o;       o = al(o + sizeof(float) * (size_t)T * inter);
@@ -103,8 +104,10 @@ __global__ __launch_bounds__(512) void prefill_plan_kernel(const int64_t* expert
 __global__ __launch_bounds__(256) void prefill_gather_kernel(const _Float16* x, const int64_t* token_sorted,
                                                             const int* row_expert, const void* const* suh_g,
                                                             const void* const* suh_u, _Float16* xg, _Float16* xu,
-                                                            int hidden, bool gated)
+                                                            int hidden, bool gated, float* rs_g, float* rs_u)
 {
+    __shared__ float red[2][4];
+    float sg_sum = 0.0f, su_sum = 0.0f;
     const long r = blockIdx.x;
     const int e = row_expert[r];
     const _Float16* xr = x + (size_t)token_sorted[r] * hidden;
@@ -133,6 +136,27 @@ __global__ __launch_bounds__(256) void prefill_gather_kernel(const _Float16* x, 
         }
         if (gated) *reinterpret_cast<hx_h8*>(og + c) = oa;
         *reinterpret_cast<hx_h8*>(ou + c) = ob;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            sg_sum += (float)oa[j];
+            su_sum += (float)ob[j];
+        }
+    }
+    // row sums of the transformed inputs (the codebook-2 map of the grouped GEMMs)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        sg_sum += __shfl_xor(sg_sum, o, 64);
+        su_sum += __shfl_xor(su_sum, o, 64);
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        red[0][wave] = sg_sum;
+        red[1][wave] = su_sum;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (gated) rs_g[r] = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+        rs_u[r] = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
     }
 }
 
@@ -147,6 +171,8 @@ struct GroupedGemmArgs {
     const int32_t* bits_tab[2];
     int bits_uniform[2];
     int K, N, nproj;
+    const float* rs[2];  // precomputed row sums of A: rs_n partial sums per row
+    int rs_n;
 };
 
 #if HX_MF_Q
@@ -166,7 +192,8 @@ __device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job
     const uint32_t* tr = static_cast<const uint32_t*>(g.tr[proj][job.expert]);
 #if HX_MF_Q
     hx_f4 acc[BM / 16][2];
-    mfma_tile_q<BITS, CB, BM>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc);
+    mfma_tile_q<BITS, CB, BM, QT_PF, true>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc,
+                                            g.rs[proj] + (size_t)job.row0 * g.rs_n, g.rs_n);
 #else
     hx_f4 acc[BM / 32][4];
     mfma_tile<BITS, CB, BM>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc);
@@ -232,6 +259,9 @@ struct GuArgs {
     _Float16* act;       // [R][inter] down-projection inputs
     _Float16* g_scratch; // [R][inter] fp16 G, then u, of the tiles in flight
     _Float16* u_scratch;
+    const float* rs_g;   // [R] row sums of xg, xu
+    const float* rs_u;
+    float* rs_act;       // [R][inter / 128] row sums of act per 128-column block
 };
 
 #if HX_MF_Q
@@ -258,10 +288,10 @@ typedef MfmaSmem GuSmem;
 
 template <int BITS, int CB, int BM>
 __device__ __forceinline__ void gu_tile(const _Float16* A, int K, int rows, const void* tr, int N, int cg,
-                                        GuSmem& sm, GuAcc<BM>& acc)
+                                        GuSmem& sm, GuAcc<BM>& acc, const float* rs)
 {
 #if HX_MF_Q
-    mfma_tile_q<BITS, CB, BM, QT_PF>(A, K, rows, static_cast<const uint32_t*>(tr), K, N, cg * 8, sm, acc);
+    mfma_tile_q<BITS, CB, BM, QT_PF, true>(A, K, rows, static_cast<const uint32_t*>(tr), K, N, cg * 8, sm, acc, rs, 1);
 #else
     mfma_tile<BITS, CB, BM>(A, K, rows, static_cast<const uint32_t*>(tr), K, N, cg * 8, sm, acc);
 #endif
@@ -269,17 +299,17 @@ __device__ __forceinline__ void gu_tile(const _Float16* A, int K, int rows, cons
 
 template <int CB, int BM>
 __device__ __forceinline__ void gu_tile_bits(int bits, const _Float16* A, int K, int rows, const void* tr, int N,
-                                             int cg, GuSmem& sm, GuAcc<BM>& acc)
+                                             int cg, GuSmem& sm, GuAcc<BM>& acc, const float* rs)
 {
     switch (bits) {
-        case 1: gu_tile<1, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
-        case 2: gu_tile<2, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
-        case 3: gu_tile<3, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
-        case 4: gu_tile<4, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
-        case 5: gu_tile<5, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
-        case 6: gu_tile<6, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
-        case 7: gu_tile<7, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
-        default: gu_tile<8, CB, BM>(A, K, rows, tr, N, cg, sm, acc); break;
+        case 1: gu_tile<1, CB, BM>(A, K, rows, tr, N, cg, sm, acc, rs); break;
+        case 2: gu_tile<2, CB, BM>(A, K, rows, tr, N, cg, sm, acc, rs); break;
+        case 3: gu_tile<3, CB, BM>(A, K, rows, tr, N, cg, sm, acc, rs); break;
+        case 4: gu_tile<4, CB, BM>(A, K, rows, tr, N, cg, sm, acc, rs); break;
+        case 5: gu_tile<5, CB, BM>(A, K, rows, tr, N, cg, sm, acc, rs); break;
+        case 6: gu_tile<6, CB, BM>(A, K, rows, tr, N, cg, sm, acc, rs); break;
+        case 7: gu_tile<7, CB, BM>(A, K, rows, tr, N, cg, sm, acc, rs); break;
+        default: gu_tile<8, CB, BM>(A, K, rows, tr, N, cg, sm, acc, rs); break;
     }
 }
 
@@ -328,7 +358,8 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
     const bool gated = a.act_fn != HX_ACT_RELU2_NOGATE;
     // gate: G = fp16(mapped sum)
     if (gated) {
-        gu_tile_bits<CB, BM>(bg, a.xg + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[0][e], a.N, cg, sm, acc);
+        gu_tile_bits<CB, BM>(bg, a.xg + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[0][e], a.N, cg, sm, acc,
+                             a.rs_g + job.row0);
 #if HX_MF_Q
         qt_foreach<BM>(acc, [&](int row, int col, float v) {
             if (row < job.rows) gs[(size_t)row * a.N + col] = (_Float16)mapped(row, v);
@@ -338,7 +369,8 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
 #endif
         __syncthreads();  // rowsum is reused by the up tile
     }
-    gu_tile_bits<CB, BM>(bu, a.xu + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[1][e], a.N, cg, sm, acc);
+    gu_tile_bits<CB, BM>(bu, a.xu + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[1][e], a.N, cg, sm, acc,
+                         a.rs_u + job.row0);
 
     // u = fp16(H(U)) * svh_u
 #if !HX_MF_Q
@@ -396,10 +428,20 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
     acc_to_lds_f16<BM>(hacc, X, [](int, int, float v) { return v; });
     __syncthreads();
     _Float16* out = a.act + (size_t)job.row0 * a.N + cg * 128;
+    const int nblk = a.N >> 7;
     for (int i = threadIdx.x; i < BM * 16; i += MF_THREADS) {
         const int row = i >> 4, c8 = (i & 15) * 8;
-        if (row < job.rows)
-            *reinterpret_cast<hx_u4v*>(out + (size_t)row * a.N + c8) = *reinterpret_cast<const hx_u4v*>(&X[row * MF_LDA2 + c8]);
+        const hx_h8 v = *reinterpret_cast<const hx_h8*>(&X[row * MF_LDA2 + c8]);
+        if (row < job.rows) *reinterpret_cast<hx_h8*>(out + (size_t)row * a.N + c8) = v;
+        // this block's part of the row sum of act (the down GEMM's codebook-2 map): 16 lanes per row
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sum += (float)v[j];
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 4, 64);
+        sum += __shfl_xor(sum, 8, 64);
+        if ((i & 15) == 0 && row < job.rows) a.rs_act[(size_t)(job.row0 + row) * nblk + cg] = sum;
     }
 }
 #undef HX_HAD
@@ -520,13 +562,16 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     _Float16* U = reinterpret_cast<_Float16*>(ws + L.off_U);
     _Float16* A = reinterpret_cast<_Float16*>(ws + L.off_A);
     _Float16* D = reinterpret_cast<_Float16*>(ws + L.off_D);
+    float* rs_g = reinterpret_cast<float*>(ws + L.off_rs);
+    float* rs_u = rs_g + p.R;
+    float* rs_act = rs_u + p.R;
     if (p.E > 512) return hipErrorInvalidValue;
 
     hipLaunchKernelGGL(prefill_plan_kernel, dim3((unsigned)((p.R + 511) / 512)), dim3(512), 0, st, p.expert_count,
                        p.E, p.R, jobs, njobs, row_expert);
     if (p.R > 0)
         hipLaunchKernelGGL(prefill_gather_kernel, dim3((unsigned)p.R), dim3(256), 0, st, p.x, p.token_sorted,
-                           row_expert, p.suh[0], p.suh[1], xg, xu, p.hidden, p.act_fn != HX_ACT_RELU2_NOGATE);
+                           row_expert, p.suh[0], p.suh[1], xg, xu, p.hidden, p.act_fn != HX_ACT_RELU2_NOGATE, rs_g, rs_u);
 
     GuArgs gu{};
     gu.jobs = jobs;
@@ -549,6 +594,9 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     gu.act = A;
     gu.g_scratch = G;
     gu.u_scratch = U;
+    gu.rs_g = rs_g;
+    gu.rs_u = rs_u;
+    gu.rs_act = rs_act;
     dim3 grid_gu(p.inter / 128, L.max_jobs);
     if (p.cb == 1) hipLaunchKernelGGL(grouped_gu_kernel<1>, grid_gu, dim3(MF_THREADS), 0, st, gu);
     else hipLaunchKernelGGL(grouped_gu_kernel<2>, grid_gu, dim3(MF_THREADS), 0, st, gu);
@@ -564,6 +612,8 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     d.K = p.inter;
     d.N = p.hidden;
     d.nproj = 1;
+    d.rs[0] = rs_act;
+    d.rs_n = p.inter / 128;
     dim3 grid_d(p.hidden / 128, L.max_jobs);
     if (p.cb == 1) hipLaunchKernelGGL(grouped_gemm_kernel<1>, grid_d, dim3(MF_THREADS), 0, st, d);
     else hipLaunchKernelGGL(grouped_gemm_kernel<2>, grid_d, dim3(MF_THREADS), 0, st, d);

@@ -59,6 +59,9 @@ def workspace(nbytes: int, device: Optional[torch.device] = None, stream=None) -
     key = (idx, _stream(stream))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("the workspace of this stream must be allocated before graph capture: run the call "
+                               "once on the capturing stream first, or pass a workspace")
         torch.cuda.synchronize(idx)
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         torch.cuda.synchronize(idx)
