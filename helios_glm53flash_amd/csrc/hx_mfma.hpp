@@ -229,7 +229,7 @@ constexpr int QT_PF = HX_QT_PF;
 #define HX_QT_ILV_MAXBITS 3  // wider words leave too few registers for two decoded quarters
 #endif
 #ifndef HX_QT_ILV
-#define HX_QT_ILV 1
+#define HX_QT_ILV 0  // measured no faster than the block decode (config-4 prefill 3.53 vs 3.54 ms)
 #endif
 
 // LDS of a kernel that uses only quarter-operand tiles: the A buffers, the epilogue staging.
@@ -248,7 +248,7 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
                                             int N, int tn0, Smem& sm, hx_f4 (&acc)[BM / 16][2],
                                             const float* rs_src = nullptr, int rs_n = 0)
 {
-    static_assert(BM == 64 || BM == 128, "row tile");
+    static_assert(BM == 32 || BM == 64 || BM == 128, "row tile");
     constexpr int RB = BM / 16;
     constexpr int NA = BM / 32;   // 16-byte A loads per thread per chunk
     constexpr int NW = 8 * BITS;

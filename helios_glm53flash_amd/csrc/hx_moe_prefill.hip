@@ -24,7 +24,7 @@ namespace hx {
 static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Job {
-    int expert, row0, rows, bm;  // bm: row tile (128, or 64 for a remainder of at most 64 rows)
+    int expert, row0, rows, bm;  // bm: row tile (128, or 64 / 32 for a remainder of at most 64 / 32 rows)
 };
 
 void MoeWs::prefill_layout(size_t o)
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(512) void prefill_plan_kernel(const int64_t* expert
     if (blockIdx.x == 0) {
         for (int k = 0; k < nj; ++k) {
             const int rows = min(MF_BM, c - k * MF_BM);
-            jobs[j0 + k] = Job{t, r0 + k * MF_BM, rows, rows <= 64 ? 64 : MF_BM};
+            jobs[j0 + k] = Job{t, r0 + k * MF_BM, rows, rows <= 32 ? 32 : rows <= 64 ? 64 : MF_BM};
         }
         if (t == 511) *njobs = joff[511];
     }
@@ -200,7 +200,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job
 #endif
     _Float16* out = g.out[proj] + (size_t)job.row0 * g.N + cg * 128;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int half = 0; half < BM / 64; ++half) {
+    for (int half = 0; half < (BM + 63) / 64; ++half) {
 #if HX_MF_Q
         qt_stage_c_half<BM>(acc, half, sm);
 #else
@@ -230,7 +230,8 @@ __global__ __launch_bounds__(MF_THREADS, HX_MFQ_OCC) void grouped_gemm_kernel(Gr
     const int bits = g.bits_tab[proj] ? g.bits_tab[proj][job.expert] : g.bits_uniform[proj];
 #define HX_GG_CASE(B)                                                                      \
     case B:                                                                                \
-        if (job.bm == 64) grouped_tile<B, CB, 64>(g, job, proj, cg, sm);                    \
+        if (job.bm == 32) grouped_tile<B, CB, 32>(g, job, proj, cg, sm);                    \
+        else if (job.bm == 64) grouped_tile<B, CB, 64>(g, job, proj, cg, sm);               \
         else grouped_tile<B, CB, MF_BM>(g, job, proj, cg, sm);                              \
         break;
     switch (bits) {
@@ -453,7 +454,8 @@ __global__ __launch_bounds__(MF_THREADS, HX_GU_OCC) void grouped_gu_kernel(GuArg
     const int job_i = blockIdx.y;
     if (job_i >= *a.njobs) return;
     const Job job = a.jobs[job_i];
-    if (job.bm == 64) gu_fused<CB, 64>(a, job, blockIdx.x, sm);
+    if (job.bm == 32) gu_fused<CB, 32>(a, job, blockIdx.x, sm);
+    else if (job.bm == 64) gu_fused<CB, 64>(a, job, blockIdx.x, sm);
     else gu_fused<CB, MF_BM>(a, job, blockIdx.x, sm);
 }
 
