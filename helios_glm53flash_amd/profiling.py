@@ -8,6 +8,9 @@
       of bench.py --profile-only
   python -m helios_glm53flash_amd.profiling counters <pmc.db> <kernel-name-part>
       mean value per dispatch of each counter collected for the matching kernels
+  python -m helios_glm53flash_amd.profiling utilisation <kernel-name-part> <pmc.db>...
+      per-dispatch utilisation of the matrix cores, VALU and LDS from the passes' counters (see
+      utilisation() for the definitions)
 """
 from __future__ import annotations
 
@@ -75,6 +78,37 @@ def counters(db: str, key: str) -> dict[str, float]:
     return {n: float(v) for n, v in rows}
 
 
+# MI355X: 8 XCDs, 256 CUs, 4 SIMDs per CU.  GRBM_GUI_ACTIVE is summed over the XCDs (cycles of one
+# XCD = value / 8); SQ_ACTIVE_INST_VALU counts in units of 4 cycles (a wave64 VALU instruction
+# issues over 4 cycles); SQ_VALU_MFMA_BUSY_CYCLES is summed over the SIMDs; the LDS counters over
+# the CUs.
+XCDS, CUS, SIMDS = 8, 256, 1024
+
+
+def utilisation(key: str, dbs: list[str]) -> dict[str, float]:
+    c: dict[str, float] = {}
+    for db in dbs:
+        for k, v in counters(db, key).items():
+            c.setdefault(k, v)
+    cyc = c["GRBM_GUI_ACTIVE"] / XCDS
+    out = {"cycles_per_xcd": cyc}
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+        out["mfma_busy"] = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc * SIMDS)
+    if "SQ_ACTIVE_INST_VALU" in c:
+        out["valu_busy"] = 4 * c["SQ_ACTIVE_INST_VALU"] / (cyc * SIMDS)
+    if "SQ_VALU_MFMA_COEXEC_CYCLES" in c:
+        out["valu_mfma_coexec"] = c["SQ_VALU_MFMA_COEXEC_CYCLES"] / (cyc * SIMDS)
+    if "SQ_LDS_IDX_ACTIVE" in c:
+        out["lds_active"] = c["SQ_LDS_IDX_ACTIVE"] / (cyc * CUS)
+    if "SQ_LDS_BANK_CONFLICT" in c:
+        out["lds_bank_conflict"] = c["SQ_LDS_BANK_CONFLICT"] / (cyc * CUS)
+    if "SQ_INSTS_VALU" in c and "SQ_INSTS_MFMA" in c:
+        out["valu_per_mfma"] = c["SQ_INSTS_VALU"] / c["SQ_INSTS_MFMA"]
+    if "SQ_INSTS_VALU_MFMA_MOPS_F16" in c:
+        out["mfma_flops"] = 512.0 * c["SQ_INSTS_VALU_MFMA_MOPS_F16"]
+    return {k: round(v, 4) if v < 100 else v for k, v in out.items()}
+
+
 def main(argv: list[str]) -> None:
     if len(argv) >= 2 and argv[0] == "stats":
         for r in kernel_stats(argv[1]):
@@ -82,6 +116,8 @@ def main(argv: list[str]) -> None:
                   f"{r['kernel'][:110]}")
     elif len(argv) >= 3 and argv[0] == "counters":
         print(json.dumps(counters(argv[1], argv[2]), indent=1))
+    elif len(argv) >= 3 and argv[0] == "utilisation":
+        print(json.dumps(utilisation(argv[1], argv[2:]), indent=1))
     elif len(argv) >= 3 and argv[0] == "traffic":
         cmd = argv[argv.index("--cmd") + 1] if "--cmd" in argv else ""
         print(json.dumps(traffic(argv[1], argv[2], cmd), indent=1))
