@@ -98,17 +98,19 @@ __global__ __launch_bounds__(512) void prefill_plan_kernel(const int64_t* expert
 
 // ------------------------------------------------------------------ gather + input transform
 
-// One workgroup per sorted row: the row's token, expert and suh pointers are loaded once; a lane
-// holds 8 consecutive values of a 128-block (16-byte loads and stores), a wave 4 blocks, the
-// workgroup 16 blocks per round.
+// One wave per sorted row (4 rows per workgroup, so that the dependent loads of the row's token,
+// expert and suh pointers of four rows overlap): a lane holds 8 consecutive values of a 128-block
+// (16-byte loads and stores), the wave 4 blocks per pass.  Also writes the rows' sums of xg and xu
+// (the codebook-2 map of the grouped GEMMs).
 __global__ __launch_bounds__(256) void prefill_gather_kernel(const _Float16* x, const int64_t* token_sorted,
                                                             const int* row_expert, const void* const* suh_g,
                                                             const void* const* suh_u, _Float16* xg, _Float16* xu,
-                                                            int hidden, bool gated, float* rs_g, float* rs_u)
+                                                            int hidden, bool gated, float* rs_g, float* rs_u, long R)
 {
-    __shared__ float red[2][4];
+    const long r = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= R) return;
+    const int lane = threadIdx.x & 63;
     float sg_sum = 0.0f, su_sum = 0.0f;
-    const long r = blockIdx.x;
     const int e = row_expert[r];
     const _Float16* xr = x + (size_t)token_sorted[r] * hidden;
     // the non-gated relu2 has no gate GEMM, so no gate input (exl3_moe_kernel.cuh:84-97)
@@ -116,7 +118,8 @@ __global__ __launch_bounds__(256) void prefill_gather_kernel(const _Float16* x, 
     const _Float16* su = static_cast<const _Float16*>(suh_u[e]);
     _Float16* og = xg + r * hidden;
     _Float16* ou = xu + r * hidden;
-    for (int c = 8 * threadIdx.x; c < hidden; c += 8 * 256) {
+#pragma unroll 2
+    for (int c = 8 * lane; c < hidden; c += 8 * 64) {
         const hx_h8 xv = *reinterpret_cast<const hx_h8*>(xr + c);
         const hx_h8 gv = *reinterpret_cast<const hx_h8*>(sg + c);
         const hx_h8 uv = *reinterpret_cast<const hx_h8*>(su + c);
@@ -142,21 +145,14 @@ __global__ __launch_bounds__(256) void prefill_gather_kernel(const _Float16* x, 
             su_sum += (float)ob[j];
         }
     }
-    // row sums of the transformed inputs (the codebook-2 map of the grouped GEMMs)
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         sg_sum += __shfl_xor(sg_sum, o, 64);
         su_sum += __shfl_xor(su_sum, o, 64);
     }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 0) {
-        red[0][wave] = sg_sum;
-        red[1][wave] = su_sum;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        if (gated) rs_g[r] = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
-        rs_u[r] = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+        if (gated) rs_g[r] = sg_sum;
+        rs_u[r] = su_sum;
     }
 }
 
@@ -572,8 +568,8 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     hipLaunchKernelGGL(prefill_plan_kernel, dim3((unsigned)((p.R + 511) / 512)), dim3(512), 0, st, p.expert_count,
                        p.E, p.R, jobs, njobs, row_expert);
     if (p.R > 0)
-        hipLaunchKernelGGL(prefill_gather_kernel, dim3((unsigned)p.R), dim3(256), 0, st, p.x, p.token_sorted,
-                           row_expert, p.suh[0], p.suh[1], xg, xu, p.hidden, p.act_fn != HX_ACT_RELU2_NOGATE, rs_g, rs_u);
+        hipLaunchKernelGGL(prefill_gather_kernel, dim3((unsigned)((p.R + 3) / 4)), dim3(256), 0, st, p.x, p.token_sorted,
+                           row_expert, p.suh[0], p.suh[1], xg, xu, p.hidden, p.act_fn != HX_ACT_RELU2_NOGATE, rs_g, rs_u, (long)p.R);
 
     GuArgs gu{};
     gu.jobs = jobs;
