@@ -40,7 +40,7 @@ void MoeWs::prefill_layout(size_t o)
     off_G = o;          o = al(o + sizeof(_Float16) * (size_t)R * inter);
     off_U = o;          o = al(o + sizeof(_Float16) * (size_t)R * inter);
     off_A = o;          o = al(o + sizeof(_Float16) * (size_t)R * inter);
-    off_rs = o;         o = al(o + sizeof(float) * (size_t)R * (2 + inter / 128));
+    off_rs = o;         o = al(o + sizeof(float) * (size_t)R * (2 * (hidden / 128) + inter / 128));
     off_D = off_xg;     // D reuses xg (xg is consumed by the gate GEMM before the down GEMM runs)
     off_sh_a = o;       o = al(o + sizeof(_Float16) * (size_t)T * kmax);
     off_sh_g = o;       o = al(o + sizeof(float) * (size_t)T * inter);
@@ -98,61 +98,110 @@ __global__ __launch_bounds__(512) void prefill_plan_kernel(const int64_t* expert
 
 // ------------------------------------------------------------------ gather + input transform
 
-// One wave per sorted row (4 rows per workgroup, so that the dependent loads of the row's token,
-// expert and suh pointers of four rows overlap): a lane holds 8 consecutive values of a 128-block
-// (16-byte loads and stores), the wave 4 blocks per pass.  Also writes the rows' sums of xg and xu
-// (the codebook-2 map of the grouped GEMMs).
-__global__ __launch_bounds__(256) void prefill_gather_kernel(const _Float16* x, const int64_t* token_sorted,
+// One wave per (16 sorted rows, 128-column block): the transform is a 16 x 128 by 128 x 128 GEMM on
+// the matrix cores, A = fp16(x[token] . suh) (one fp16 rounding, as the reference's __hmul2),
+// B = H128 generated in registers, fp32 accumulation (the products
+// are exact, so this is the reference's fp32 butterfly up to the order of the fp32 additions), one
+// fp16 rounding.  Lane l: A row l % 16, k = 32 kk + 8 (l / 16) + 0..7; B column 16 nb + l % 16 with
+// the same k; C rows 4 (l / 16) + i, column 16 nb + l % 16.  Also writes each row's sum of the 128
+// outputs (rs[row][block], the codebook-2 map of the grouped GEMMs).
+__global__ __launch_bounds__(256, 4) void prefill_gather_kernel(const _Float16* x, const int64_t* token_sorted,
                                                             const int* row_expert, const void* const* suh_g,
                                                             const void* const* suh_u, _Float16* xg, _Float16* xu,
                                                             int hidden, bool gated, float* rs_g, float* rs_u, long R)
 {
-    const long r = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (r >= R) return;
     const int lane = threadIdx.x & 63;
-    float sg_sum = 0.0f, su_sum = 0.0f;
+    const int nblk = hidden >> 7;
+    const long unit = (long)blockIdx.x * 4 + (threadIdx.x >> 6);  // (row block, column block)
+    const long rb = unit / nblk;
+    const int kb = (int)(unit % nblk);
+    if (rb * 16 >= R) return;
+    const int c = lane & 15, g = lane >> 4;
+    const long r = min(rb * 16 + c, R - 1);  // A row of this lane (rows past R repeat the last, not stored)
     const int e = row_expert[r];
-    const _Float16* xr = x + (size_t)token_sorted[r] * hidden;
-    // the non-gated relu2 has no gate GEMM, so no gate input (exl3_moe_kernel.cuh:84-97)
-    const _Float16* sg = static_cast<const _Float16*>(gated ? suh_g[e] : suh_u[e]);
-    const _Float16* su = static_cast<const _Float16*>(suh_u[e]);
-    _Float16* og = xg + r * hidden;
-    _Float16* ou = xu + r * hidden;
-#pragma unroll 2
-    for (int c = 8 * lane; c < hidden; c += 8 * 64) {
-        const hx_h8 xv = *reinterpret_cast<const hx_h8*>(xr + c);
-        const hx_h8 gv = *reinterpret_cast<const hx_h8*>(sg + c);
-        const hx_h8 uv = *reinterpret_cast<const hx_h8*>(su + c);
-        float a[8], b[8];
+    const _Float16* xr = x + (size_t)token_sorted[r] * hidden + kb * 128 + 8 * g;
+    const _Float16* sg = static_cast<const _Float16*>(gated ? suh_g[e] : suh_u[e]) + kb * 128 + 8 * g;
+    const _Float16* su = static_cast<const _Float16*>(suh_u[e]) + kb * 128 + 8 * g;
+    hx_h8 xv[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            a[j] = (float)(_Float16)(xv[j] * gv[j]);
-            b[j] = (float)(_Float16)(xv[j] * uv[j]);
+    for (int kk = 0; kk < 4; ++kk) xv[kk] = *reinterpret_cast<const hx_h8*>(xr + 32 * kk);
+    // H128 B operands: sign of (n, k) = popcount(n & k) & 1 with n = 16 nb + c, k = 32 kk + 8 g + j
+    uint32_t f[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t s0 = __builtin_popcount(c & (2 * i) & 7) & 1, s1 = __builtin_popcount(c & (2 * i + 1) & 7) & 1;
+        f[i] = (0x3c00u | (s0 << 15)) | ((0x3c00u | (s1 << 15)) << 16);
+    }
+    const uint32_t base = (uint32_t)((c >> 3) & g & 1);
+    __shared__ _Float16 stage[4][2][16][136];
+    _Float16 (*sw)[16][136] = stage[threadIdx.x >> 6];
+    float sum_g[4] = {0.f, 0.f, 0.f, 0.f}, sum_u[4] = {0.f, 0.f, 0.f, 0.f};
+    // the gate's transform, then the up's (one accumulator set at a time)
+#pragma unroll 1
+    for (int pj = gated ? 0 : 1; pj < 2; ++pj) {
+        const _Float16* sp = pj ? su : sg;
+        hx_h8 av[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) av[kk] = xv[kk] * *reinterpret_cast<const hx_h8*>(sp + 32 * kk);
+        hx_f4 y[8];
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) y[nb] = hx_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) {
+                const uint32_t sgn = base ^ ((uint32_t)(nb & 1) & (uint32_t)(g >> 1)) ^ (uint32_t)((nb >> 1) & kk & 1) ^
+                                     (uint32_t)((nb >> 2) & (kk >> 1) & 1);
+                const uint32_t m = sgn ? 0x80008000u : 0u;
+                typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+                const u4v bv = {f[0] ^ m, f[1] ^ m, f[2] ^ m, f[3] ^ m};
+                y[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[kk], __builtin_bit_cast(hx_h8, bv), y[nb], 0, 0, 0);
+            }
+        // fp16 outputs staged in LDS (16-byte row stores below); row sums: the 16 lanes of a lane
+        // group hold one row's 128 columns
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float t = 0.0f;
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) {
+                const _Float16 v = (_Float16)(y[nb][i] * HX_RSQRT128);
+                t += (float)v;
+                sw[pj][4 * g + i][16 * nb + c] = v;
+            }
+            if (pj) sum_u[i] = t;
+            else sum_g[i] = t;
         }
-        hx_had128_x8(a);
-        hx_had128_x8(b);
-        hx_h8 oa, ob;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            oa[j] = (_Float16)a[j];
-            ob[j] = (_Float16)b[j];
-        }
-        if (gated) *reinterpret_cast<hx_h8*>(og + c) = oa;
-        *reinterpret_cast<hx_h8*>(ou + c) = ob;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            sg_sum += (float)oa[j];
-            su_sum += (float)ob[j];
+    for (int q = 0; q < 4; ++q) {
+        const int row16 = 4 * q + (lane >> 4), c8 = 8 * (lane & 15);
+        const long row = rb * 16 + row16;
+        if (row < R) {
+            const size_t o = (size_t)row * hidden + kb * 128 + c8;
+            if (gated) *reinterpret_cast<hx_u4v*>(xg + o) = *reinterpret_cast<const hx_u4v*>(&sw[0][row16][c8]);
+            *reinterpret_cast<hx_u4v*>(xu + o) = *reinterpret_cast<const hx_u4v*>(&sw[1][row16][c8]);
         }
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        sg_sum += __shfl_xor(sg_sum, o, 64);
-        su_sum += __shfl_xor(su_sum, o, 64);
-    }
-    if (lane == 0) {
-        if (gated) rs_g[r] = sg_sum;
-        rs_u[r] = su_sum;
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            sum_g[i] += __shfl_xor(sum_g[i], o, 64);
+            sum_u[i] += __shfl_xor(sum_u[i], o, 64);
+        }
+    if (c < 4) {
+        float vg_ = 0.f, vu_ = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (c == i) vg_ = sum_g[i], vu_ = sum_u[i];
+        const long row = rb * 16 + 4 * g + c;
+        if (row < R) {
+            if (gated) rs_g[(size_t)row * nblk + kb] = vg_;
+            rs_u[(size_t)row * nblk + kb] = vu_;
+        }
     }
 }
 
@@ -256,7 +305,7 @@ struct GuArgs {
     _Float16* act;       // [R][inter] down-projection inputs
     _Float16* g_scratch; // [R][inter] fp16 G, then u, of the tiles in flight
     _Float16* u_scratch;
-    const float* rs_g;   // [R] row sums of xg, xu
+    const float* rs_g;   // [R][K / 128] row sums of xg, xu per 128-column block
     const float* rs_u;
     float* rs_act;       // [R][inter / 128] row sums of act per 128-column block
 };
@@ -288,7 +337,8 @@ __device__ __forceinline__ void gu_tile(const _Float16* A, int K, int rows, cons
                                         GuSmem& sm, GuAcc<BM>& acc, const float* rs)
 {
 #if HX_MF_Q
-    mfma_tile_q<BITS, CB, BM, QT_PF, true>(A, K, rows, static_cast<const uint32_t*>(tr), K, N, cg * 8, sm, acc, rs, 1);
+    mfma_tile_q<BITS, CB, BM, QT_PF, true>(A, K, rows, static_cast<const uint32_t*>(tr), K, N, cg * 8, sm, acc, rs,
+                                           K / 128);
 #else
     mfma_tile<BITS, CB, BM>(A, K, rows, static_cast<const uint32_t*>(tr), K, N, cg * 8, sm, acc);
 #endif
@@ -356,7 +406,7 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
     // gate: G = fp16(mapped sum)
     if (gated) {
         gu_tile_bits<CB, BM>(bg, a.xg + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[0][e], a.N, cg, sm, acc,
-                             a.rs_g + job.row0);
+                             a.rs_g + (size_t)job.row0 * (a.K / 128));
 #if HX_MF_Q
         qt_foreach<BM>(acc, [&](int row, int col, float v) {
             if (row < job.rows) gs[(size_t)row * a.N + col] = (_Float16)mapped(row, v);
@@ -367,7 +417,7 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
         __syncthreads();  // rowsum is reused by the up tile
     }
     gu_tile_bits<CB, BM>(bu, a.xu + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[1][e], a.N, cg, sm, acc,
-                         a.rs_u + job.row0);
+                         a.rs_u + (size_t)job.row0 * (a.K / 128));
 
     // u = fp16(H(U)) * svh_u
 #if !HX_MF_Q
@@ -561,14 +611,15 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     _Float16* A = reinterpret_cast<_Float16*>(ws + L.off_A);
     _Float16* D = reinterpret_cast<_Float16*>(ws + L.off_D);
     float* rs_g = reinterpret_cast<float*>(ws + L.off_rs);
-    float* rs_u = rs_g + p.R;
-    float* rs_act = rs_u + p.R;
+    float* rs_u = rs_g + (size_t)p.R * (p.hidden / 128);
+    float* rs_act = rs_u + (size_t)p.R * (p.hidden / 128);
     if (p.E > 512) return hipErrorInvalidValue;
 
     hipLaunchKernelGGL(prefill_plan_kernel, dim3((unsigned)((p.R + 511) / 512)), dim3(512), 0, st, p.expert_count,
                        p.E, p.R, jobs, njobs, row_expert);
     if (p.R > 0)
-        hipLaunchKernelGGL(prefill_gather_kernel, dim3((unsigned)((p.R + 3) / 4)), dim3(256), 0, st, p.x, p.token_sorted,
+        hipLaunchKernelGGL(prefill_gather_kernel, dim3((unsigned)((((long)p.R + 15) / 16 * (p.hidden / 128) + 3) / 4)),
+                           dim3(256), 0, st, p.x, p.token_sorted,
                            row_expert, p.suh[0], p.suh[1], xg, xu, p.hidden, p.act_fn != HX_ACT_RELU2_NOGATE, rs_g, rs_u, (long)p.R);
 
     GuArgs gu{};
