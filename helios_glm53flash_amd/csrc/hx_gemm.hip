@@ -1,5 +1,5 @@
 // hx_gemm.hip -- EXL3 quantized linear for M > 8 on MFMA (gfx950): input transform kernel, then
-// decode-to-LDS + MFMA tiles with the output Hadamard + svh epilogue fused.
+// quarter-operand MFMA tiles (hx_mfma.hpp) with the output Hadamard + svh epilogue fused.
 // Reference semantics: src/cuda/quant/exl3_gemm_kernel.cuh:8-80, exl3_gemm_inner.cuh:456-480.
 #include "hx_mfma.hpp"
 #include "hx_kernels.hpp"

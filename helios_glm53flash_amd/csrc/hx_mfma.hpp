@@ -1,18 +1,14 @@
-// hx_mfma.hpp -- EXL3 decode-to-LDS + MFMA tile core for gfx950 (M > 16 paths: the dense linear
-// and the grouped expert GEMM of the prefill).
+// hx_mfma.hpp -- EXL3 decode + MFMA tile core for gfx950 (M > 16 paths: the dense linear and the
+// grouped expert GEMMs of the prefill), and the Hadamard-128 transform on the matrix cores.
 //
-// Workgroup = 4 waves, output tile BM x 128 (BM = 128 or 64; 128 columns = one Hadamard block),
-// K consumed in chunks of 64, double-buffered in LDS:
-//   * while the matrix cores work on chunk c (from LDS buffer c & 1), the waves load chunk c+1:
-//     A (BM x 64 fp16, already input-transformed) with 16-byte buffer loads, and the trellis words
-//     of its 4 x 8 tiles (thread q of a tile owns positions 32q..32q+31, i.e. columns q and q+8 of
-//     all 16 k; those windows live in stream words [q*bits - 1, q*bits + bits)), then decode the
-//     words on the VALU and store B (128 x 64, [n][k]) and A into the other buffer; one barrier per
-//     chunk.
-//   * each wave computes a (BM/2) x 64 quarter with v_mfma_f32_16x16x32_f16 (fp32 accumulate).
+// Workgroup = 4 waves, output tile BM x 128 (BM = 128, 64 or 32; 128 columns = one Hadamard block),
+// K consumed in chunks of 64.  Each wave owns 32 output columns for all BM rows and decodes those
+// columns' trellis words itself, straight into MFMA B operands (mfma_tile_q below); only A (the
+// input-transformed activations) is staged in LDS, double-buffered, one barrier per chunk.  Global
+// loads of A and of the trellis words run QT_PF chunks ahead in a register ring.
 // Codebook 2 is decoded in affine form (h = 1024 + bytesum, see hx_gemv.hpp): the tile computes
-// sum_k a h, and the epilogue adds the map with the per-row input sums that the tile accumulates
-// from the staged A (v_dot2_f32_f16 against ones).
+// sum_k a h, and the epilogue adds the map with per-row input sums (accumulated from the staged A, or
+// precomputed by the caller).
 // Operand layout of v_mfma_f32_16x16x32_f16 (64 lanes): A: lane l holds row l%16,
 // k = 8*(l/16)..+7; B: column l%16, same k; C: column l%16, rows 4*(l/16)..+3.
 #pragma once
@@ -26,32 +22,24 @@ constexpr int MF_THREADS = 256;
 constexpr int MF_BM = 128;  // largest row tile
 constexpr int MF_BN = 128;
 constexpr int MF_BK = 64;
-constexpr int MF_PF = 3;  // chunks of global loads in flight
 #ifndef HX_MF_SWZ
-#define HX_MF_SWZ 1
+#define HX_MF_SWZ 2
 #endif
-// Operand rows of a chunk in LDS (A rows, then B columns, 64 halves of k each).  Swizzled layout:
-// 128-byte rows, 16-byte chunk c of row r stored at chunk c ^ f(r), f(r) = ((r >> 1) & 7) ^
-// (((r >> 4) & 1) << 2): with 16 lanes per LDS cycle, the A stores (2 rows x 8 chunks), the B stores
-// (rows 16 t + q of two tile columns) and the fragment reads (16 consecutive rows, one chunk) each
-// touch 16 different bank groups.  Unswizzled: rows padded to 72 halves.
+// Operand rows of a chunk in LDS (64 halves of k each, 128-byte rows).  Swizzled layout: 16-byte chunk
+// c of row r is stored at chunk c ^ f(r), f(r) = (r & 7) ^ ((r >> 3) & 1).  The fragment reads (16
+// consecutive rows, one chunk) then touch 8 different 16-byte bank groups in every aligned group of
+// 8 rows, and every even and every odd row of the 16 a different one, so they are conflict-free
+// whether the LDS serves 8 or 16 lanes of a 16-byte access per cycle; a row's 8 chunk stores are
+// conflict-free in any case.  (SWZ 1, f(r) = ((r >> 1) & 7) ^ (((r >> 4) & 1) << 2), suits only the
+// 16-lane case and measured 1.3 % slower in the config-4 prefill; SWZ 0 pads rows to 72 halves.)
 constexpr int MF_LDA = HX_MF_SWZ ? MF_BK : MF_BK + 8;  // halves per LDS row
 constexpr int MF_LDC = MF_BN + 4;  // floats per LDS row in the epilogue
-constexpr int MF_AB = (MF_BM + MF_BN) * MF_LDA;  // halves of one A + B buffer
-
-struct MfmaSmem {
-    union {
-        _Float16 ab[2][MF_AB];  // [buffer][A rows (MF_BM x LDA), then B columns (128 x LDA)]
-        float c[64 * MF_LDC];   // epilogue staging of 64 rows
-        _Float16 hx[2 * 128 * 136];  // matrix-core Hadamard staging: H128 and one 128 x 128 block
-    };
-    float rowsum[MF_BM];        // sum_k of each staged A row (codebook-2 map)
-};
 
 // Offset (halves) of 16-byte chunk c (8 halves of k) of LDS row r.
 HX_INLINE int mf_off(int r, int c)
 {
-    if constexpr (HX_MF_SWZ) return r * MF_LDA + 8 * (c ^ (((r >> 1) & 7) ^ (((r >> 4) & 1) << 2)));
+    if constexpr (HX_MF_SWZ == 2) return r * MF_LDA + 8 * (c ^ ((r & 7) ^ ((r >> 3) & 1)));
+    else if constexpr (HX_MF_SWZ) return r * MF_LDA + 8 * (c ^ (((r >> 1) & 7) ^ (((r >> 4) & 1) << 2)));
     else return r * MF_LDA + 8 * c;
 }
 
@@ -64,145 +52,10 @@ HX_INLINE __amdgpu_buffer_rsrc_t mf_rsrc(const void* base, size_t bytes)
                                              (int)(bytes > 0x7fffffffull ? 0x7fffffffull : bytes), 0x00020000);
 }
 
-// acc[mb][nb] (float4) for this wave's (BM/2) x 64 quarter of the BM x 128 tile; on return
-// sm.rowsum[r] = sum_k A[r][k] when CB == 2.
-//   A: `rows` rows of an fp16 row-major matrix with leading dimension lda (rows past `rows` read 0)
-//   trellis: tile words of the K x N weight; tn0 = first tile column (8 tiles = 128 columns).
-template <int BITS, int CB, int BM>
-__device__ __forceinline__ void mfma_tile(const _Float16* A, long lda, int rows, const uint32_t* trellis, int K, int N,
-                                          int tn0, MfmaSmem& sm, hx_f4 (&acc)[BM / 32][4])
-{
-    static_assert(BM == 64 || BM == 128, "row tile");
-    constexpr int WM = BM / 2, MB = WM / 16;  // wave rows, 16-row blocks per wave
-    constexpr int NA = BM / 32;               // 16-byte A loads per thread per chunk
-    constexpr int NW = 8 * BITS;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int tiles_n = N >> 4;
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = hx_f4{0.f, 0.f, 0.f, 0.f};
-
-    const __amdgpu_buffer_rsrc_t ra = mf_rsrc(A, (size_t)max(rows, 0) * lda * sizeof(_Float16));
-    const __amdgpu_buffer_rsrc_t rt = mf_rsrc(trellis, (size_t)(K >> 4) * tiles_n * NW * 4);
-    // A role: loads i = 0..NA-1 cover row (t + 256 i) / 8, halves 8 * (t % 8) .. +7 of the chunk
-    int a_voff[NA];
-#pragma unroll
-    for (int i = 0; i < NA; ++i) {
-        const int idx = t + MF_THREADS * i;
-        a_voff[i] = (int)(((idx >> 3) * lda + 8 * (idx & 7)) * sizeof(_Float16));
-    }
-    // decode role: tile (tr, tc) of the 4 x 8 chunk, quarter q
-    const int dtile = t >> 3, q = t & 7;
-    const int tr = dtile >> 3, tc = dtile & 7;
-    const int t_off = ((tr * tiles_n + tn0 + tc) * NW) * 4;
-    const int voff0 = t_off + ((q * BITS + NW - 1) % NW) * 4, voff1 = t_off + q * BITS * 4;
-    const int row_bytes = tiles_n * NW * 4;
-
-    // global loads run MF_PF chunks ahead of the LDS stores (one chunk of matrix-core work covers
-    // far less than an HBM round trip); slot s of the register ring holds chunk c with c % MF_PF == s
-    hx_u4v av[MF_PF][NA];
-    uint32_t wv[MF_PF][BITS + 1];
-    float rs[NA];
-#pragma unroll
-    for (int i = 0; i < NA; ++i) rs[i] = 0.0f;
-
-    auto load_chunk = [&](int slot, int k0) {
-#pragma unroll
-        for (int i = 0; i < NA; ++i) av[slot][i] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[i], k0 * 2, 0);
-        load_quarter_buf<BITS>(wv[slot], rt, voff0, voff1, (k0 >> 4) * row_bytes);
-    };
-    auto store_chunk = [&](int slot, int buf, bool count) {
-        _Float16* as = sm.ab[buf];
-        _Float16* bs = sm.ab[buf] + MF_BM * MF_LDA;
-#pragma unroll
-        for (int i = 0; i < NA; ++i) {
-            const int idx = t + MF_THREADS * i;
-            *reinterpret_cast<hx_u4v*>(&as[mf_off(idx >> 3, idx & 7)]) = av[slot][i];
-            if (CB == 2 && count) {
-                const hx_h2 one = {(_Float16)1.0f, (_Float16)1.0f};
-                float s = rs[i];
-                s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].x), one, s, false);
-                s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].y), one, s, false);
-                s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].z), one, s, false);
-                s = __builtin_amdgcn_fdot2(u32_as_h2(av[slot][i].w), one, s, false);
-                rs[i] = s;
-            }
-        }
-        uint32_t d[16];
-        if constexpr (CB == 2) quarter_affine<BITS>(wv[slot], d);
-        else quarter_decode<BITS, CB>(wv[slot], d);
-        const int n = 16 * tc + q;  // B column (LDS row); k chunks 2 tr, 2 tr + 1
-        *reinterpret_cast<hx_h8*>(bs + mf_off(n, 2 * tr)) = quarter_operand<0, 0>(d);
-        *reinterpret_cast<hx_h8*>(bs + mf_off(n, 2 * tr + 1)) = quarter_operand<0, 1>(d);
-        *reinterpret_cast<hx_h8*>(bs + mf_off(n + 8, 2 * tr)) = quarter_operand<1, 0>(d);
-        *reinterpret_cast<hx_h8*>(bs + mf_off(n + 8, 2 * tr + 1)) = quarter_operand<1, 1>(d);
-    };
-
-    const int nk = K / MF_BK;
-    // prologue: chunks 0 .. MF_PF-1 requested (past the end: the last chunk again, never stored)
-#pragma unroll
-    for (int s = 0; s < MF_PF; ++s) load_chunk(s, min(s, nk - 1) * MF_BK);
-    store_chunk(0, 0, true);
-    // LDS-only barriers: __syncthreads() would also wait for every global load in flight, i.e.
-    // drain the prefetch ring at each chunk
-    hx_lds_barrier();
-    // one chunk: c in LDS buffer c & 1, its registers (slot u = c % MF_PF) are free for chunk
-    // c + MF_PF; then chunk c + 1 (slot (u + 1) % MF_PF, requested MF_PF - 1 chunks ago) is stored
-    // into the other buffer
-    auto step = [&](int c, int u) {
-        load_chunk(u, min(c + MF_PF, nk - 1) * MF_BK);
-        const _Float16* as = sm.ab[c & 1];
-        const _Float16* bs = sm.ab[c & 1] + MF_BM * MF_LDA;
-#pragma unroll
-        for (int kk = 0; kk < MF_BK; kk += 32) {
-            hx_h8 af[MB], bf[4];
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-                af[mb] = *reinterpret_cast<const hx_h8*>(
-                    &as[mf_off(WM * wm + 16 * mb + (lane & 15), kk / 8 + (lane >> 4))]);
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-                bf[nb] = *reinterpret_cast<const hx_h8*>(
-                    &bs[mf_off(64 * wn + 16 * nb + (lane & 15), kk / 8 + (lane >> 4))]);
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-                for (int nb = 0; nb < 4; ++nb)
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mb], bf[nb], acc[mb][nb], 0, 0, 0);
-        }
-        store_chunk((u + 1) % MF_PF, (c + 1) & 1, c + 1 < nk);
-        hx_lds_barrier();
-    };
-    // whole groups of MF_PF chunks without exits (an exit inside the group makes the compiler wait
-    // for every load in flight where the paths join), then the remaining chunks
-    const int nmain = nk - nk % MF_PF;
-    for (int c0 = 0; c0 < nmain; c0 += MF_PF) {
-#pragma unroll
-        for (int u = 0; u < MF_PF; ++u) step(c0 + u, u);
-    }
-#pragma unroll
-    for (int u = 0; u < MF_PF - 1; ++u)
-        if (nmain + u < nk) step(nmain + u, u);
-    if constexpr (CB == 2) {
-        // the 8 threads of a row are consecutive lanes
-#pragma unroll
-        for (int i = 0; i < NA; ++i) {
-            float s = rs[i];
-            s += __shfl_xor(s, 1, 64);
-            s += __shfl_xor(s, 2, 64);
-            s += __shfl_xor(s, 4, 64);
-            if ((t & 7) == 0) sm.rowsum[(t + MF_THREADS * i) >> 3] = s;
-        }
-        __syncthreads();
-    }
-}
-
 // ---- quarter-operand tile: the decoded weights never leave the registers
 //
-// Same BM x 128 output tile and LDS-staged A as mfma_tile, but each wave owns 32 columns (tile
-// columns 2w, 2w+1) for all BM rows and decodes its own B: lane l = 16g + 8t + q decodes quarter
+// Each wave owns 32 columns (tile columns 2w, 2w+1) of the BM x 128 tile for all BM rows and
+// decodes its own B: lane l = 16g + 8t + q decodes quarter
 // q of the tile in row g (of the chunk's 4 tile rows) and column 2w + t, and the 32 decoded values
 // are four MFMA B operands directly (quarter_operand<nh, kh>: column 8nh + q of tile t, k = 16g +
 // 8kh + 0..7 of the chunk), as in the GEMV core.  The A fragment of operand (rb, kh) is therefore
@@ -222,15 +75,6 @@ HX_INLINE void qt_rowcol(int rb, int nh, int i, int& row, int& col)
 #define HX_QT_PF 2
 #endif
 constexpr int QT_PF = HX_QT_PF;
-#ifndef HX_QT_SCHED
-#define HX_QT_SCHED 0
-#endif
-#ifndef HX_QT_ILV_MAXBITS
-#define HX_QT_ILV_MAXBITS 3  // wider words leave too few registers for two decoded quarters
-#endif
-#ifndef HX_QT_ILV
-#define HX_QT_ILV 0  // measured no faster than the block decode (config-4 prefill 3.53 vs 3.54 ms)
-#endif
 
 // LDS of a kernel that uses only quarter-operand tiles: the A buffers, the epilogue staging.
 struct MfmaSmemQ {
@@ -322,51 +166,6 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
     uint32_t d[16];
     decode(0, d);
     hx_lds_barrier();
-#if HX_QT_ILV
-    if constexpr (CB == 2 && PF % 2 == 0 && BITS <= HX_QT_ILV_MAXBITS) {
-        // Codebook 2: the next quarter's decode is spread between this chunk's MFMAs in program
-        // order (2 of its 16 pairs after each 16-row block for BM = 128), so the wave issues VALU
-        // work while its matrix-core ops run instead of parking it behind the last MFMA (issue is in
-        // order).  The decoded quarters alternate between d and dn (PF even: chunk parity = slot
-        // parity).
-        uint32_t dn[16];
-        auto step2 = [&](int c, int u, uint32_t* dc, uint32_t* dx) {
-            load_chunk(u, min(c + PF, nk - 1) * MF_BK);
-            const _Float16* as = sm.ab[c & 1];
-            const hx_h8 b00 = quarter_operand<0, 0>(dc), b01 = quarter_operand<0, 1>(dc);
-            const hx_h8 b10 = quarter_operand<1, 0>(dc), b11 = quarter_operand<1, 1>(dc);
-            const uint32_t* wn = wv[(u + 1) % PF];
-            uint32_t M[BITS + 1];
-#pragma unroll
-            for (int j = 1; j <= BITS; ++j) M[j] = __builtin_amdgcn_alignbit(wn[j - 1], wn[j], 16);
-            auto block = [&](auto rbc) {
-                constexpr int rb = decltype(rbc)::value;
-                const int r = 16 * rb + (lane & 15);
-                const hx_h8 a0 = *reinterpret_cast<const hx_h8*>(&as[mf_off(r, 2 * g)]);
-                const hx_h8 a1 = *reinterpret_cast<const hx_h8*>(&as[mf_off(r, 2 * g + 1)]);
-                acc[rb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b00, acc[rb][0], 0, 0, 0);
-                acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b10, acc[rb][1], 0, 0, 0);
-                acc[rb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b01, acc[rb][0], 0, 0, 0);
-                acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b11, acc[rb][1], 0, 0, 0);
-                quarter_affine_range<BITS, 32 * rb / RB, 32 * (rb + 1) / RB>(wn, M, dx);
-            };
-            [&]<int... I>(std::integer_sequence<int, I...>) {
-                (block(std::integral_constant<int, I>{}), ...);
-            }(std::make_integer_sequence<int, RB>{});
-            store_a((u + 1) % PF, (c + 1) & 1, c + 1 < nk);
-            hx_lds_barrier();
-        };
-        const int nmain = nk - nk % PF;
-        for (int c0 = 0; c0 < nmain; c0 += PF) {
-#pragma unroll
-            for (int u = 0; u < PF; ++u) step2(c0 + u, u, (u & 1) ? dn : d, (u & 1) ? d : dn);
-        }
-#pragma unroll
-        for (int u = 0; u < PF - 1; ++u)
-            if (nmain + u < nk) step2(nmain + u, u, (u & 1) ? dn : d, (u & 1) ? d : dn);
-    } else
-#endif
-    {
     auto step = [&](int c, int u) {
         load_chunk(u, min(c + PF, nk - 1) * MF_BK);
         const _Float16* as = sm.ab[c & 1];
@@ -383,23 +182,6 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
             acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b11, acc[rb][1], 0, 0, 0);
         }
         decode((u + 1) % PF, d);
-#if HX_QT_SCHED
-        // issue order: the next quarter's decode interleaved between this chunk's MFMAs, so that the
-        // wave issues VALU work while its matrix-core ops run (in-order issue would otherwise park
-        // the decode behind the last MFMA)
-        {
-            constexpr int NV = HX_QT_SCHED * (BM == 128 ? 1 : 2);
-#pragma unroll
-            for (int i = 0; i < RB; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
-                }
-            }
-        }
-#endif
         store_a((u + 1) % PF, (c + 1) & 1, c + 1 < nk);
         hx_lds_barrier();
     };
@@ -411,7 +193,6 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
 #pragma unroll
     for (int u = 0; u < PF - 1; ++u)
         if (nmain + u < nk) step(nmain + u, u);
-    }
     if constexpr (CB == 2 && EXT_RS) {
         if (t < BM) sm.rowsum[t] = rs_ext;
         __syncthreads();
@@ -463,27 +244,6 @@ HX_INLINE void qt_stage_c_half(const hx_f4 (&acc)[BM / 16][2], int half, Smem& s
     }
 }
 
-// Stage rows [64*half, 64*half + 64) of the accumulated tile to LDS (sm.c[row - 64*half][col]).
-template <int BM>
-HX_INLINE void stage_c_half(const hx_f4 (&acc)[BM / 32][4], int half, MfmaSmem& sm)
-{
-    constexpr int WM = BM / 2, MB = WM / 16;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-        const int row0 = WM * wm + 16 * mb;  // tile row of this block
-        if (row0 >= 64 * half && row0 < 64 * half + 64) {
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    sm.c[(row0 - 64 * half + 4 * (lane >> 4) + r) * MF_LDC + 64 * wn + 16 * nb + (lane & 15)] =
-                        acc[mb][nb][r];
-        }
-    }
-}
-
 // Staged value of tile row r (within the half) and column c, with the codebook-2 map applied.
 template <int CB, class Smem>
 HX_INLINE float staged_value(const Smem& sm, int half, int r, int c)
@@ -505,17 +265,6 @@ namespace hx {
 // the fp32 additions.  The result lands in the GEMM's accumulator layout (wave (wm, wn) holds rows
 // BM/2*wm + 16*mb + 4*(lane/16) + i, columns 64*wn + 16*nb + lane%16).
 constexpr int MF_LDA2 = 128 + 8;  // halves per row of a staged 128-column block
-static_assert(sizeof(MfmaSmem::hx) == 2 * 128 * MF_LDA2 * sizeof(_Float16), "Hadamard staging size");
-
-// H128 as a B operand block ([n][k], leading dimension MF_LDA2).
-HX_INLINE void h128_to_lds(_Float16* h)
-{
-    for (int i = threadIdx.x; i < 128 * 64; i += MF_THREADS) {
-        const int n = i >> 6, k = 2 * (i & 63);
-        const uint32_t s0 = __builtin_popcount(n & k) & 1, s1 = __builtin_popcount(n & (k + 1)) & 1;
-        *reinterpret_cast<uint32_t*>(&h[n * MF_LDA2 + k]) = (0x3c00u | (s0 << 15)) | ((0x3c00u | (s1 << 15)) << 16);
-    }
-}
 
 // fp16 of a float accumulator tile into X (row-major, MF_LDA2): X[row][col] = fp16(f(row, col, v)).
 template <int BM, class F>
@@ -535,38 +284,7 @@ HX_INLINE void acc_to_lds_f16(const hx_f4 (&acc)[BM / 32][4], _Float16* x, F f)
             }
 }
 
-template <int BM>
-HX_INLINE void hadamard_mfma(const _Float16* x, const _Float16* h, hx_f4 (&y)[BM / 32][4])
-{
-    constexpr int WM = BM / 2, MB = WM / 16;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) y[mb][nb] = hx_f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < 128; kk += 32) {
-        hx_h8 af[MB], bf[4];
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-            af[mb] = *reinterpret_cast<const hx_h8*>(&x[(WM * wm + 16 * mb + (lane & 15)) * MF_LDA2 + kk + 8 * (lane >> 4)]);
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-            bf[nb] = *reinterpret_cast<const hx_h8*>(&h[(64 * wn + 16 * nb + (lane & 15)) * MF_LDA2 + kk + 8 * (lane >> 4)]);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-                y[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mb], bf[nb], y[mb][nb], 0, 0, 0);
-    }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) y[mb][nb] = y[mb][nb] * HX_RSQRT128;
-}
-
-// The same transform with H128 generated in registers instead of read from LDS.  For B operand
+// H128 is generated in registers: for B operand
 // (nb, kk) lane l holds n = 64wn + 16nb + c (c = l % 16) and k = kk + 8g + j (g = l / 16, j < 8),
 // so popcount(n & k) mod 2 = popcount(c & j & 7) + (c3 g0) + (nb0 g1) + (nb1 kk5) + (wn kk6): a fixed
 // per-lane fragment F (the j-dependent part) times a per-lane sign for each (nb, kk), applied as an

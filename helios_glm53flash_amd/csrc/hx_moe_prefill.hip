@@ -2,11 +2,12 @@
 // token-by-expert permutation).
 //
 // Flow (all stream-ordered, no host synchronisation):
-//   plan       expert_count -> per-row expert id and 128-row tile jobs per expert
-//   gather     xg[r] = fp16(H(x[token_sorted[r]] . suh_g[e])), xu[r] likewise  (one wave per 128 block)
-//   gate/up    G = xg . W_g[e], U = xu . W_u[e] (decode-to-LDS + MFMA), then in the same workgroup
-//              act[r] = fp16(H((silu(g) * u) . suh_d)), g = fp16(H(G)) . svh_g ... (fp16 chain,
-//              transforms on the matrix cores)
+//   plan       expert_count -> per-row expert id and 128/64/32-row tile jobs per expert
+//   gather     xg[r] = fp16(H(x[token_sorted[r]] . suh_g[e])), xu[r] likewise (H on the matrix
+//              cores), and their row sums per 128-column block
+//   gate/up    G = xg . W_g[e], U = xu . W_u[e] (quarter-operand MFMA tiles), then in the same
+//              workgroup act[r] = fp16(H((act(g) * u) . suh_d)), g = fp16(H(G)) . svh_g ... (fp16
+//              chain, transforms on the matrix cores), and the row sums of act
 //   gemm d     D = act . W_d[e]                    (fp16 output)
 //   combine    y[t] = fp16(sum_j H(D[r_j]) * w_j / sqrt(128) . svh_d[e_j]  + shared[t])
 // Reference semantics: src/cuda/quant/exl3_moe_kernel.cuh:57-262, hadamard_inner.cuh:284-481,
@@ -14,10 +15,6 @@
 #include "hx_mfma.hpp"
 #include "hx_kernels.hpp"
 #include "hx_moe.hpp"
-
-#ifndef HX_MF_Q
-#define HX_MF_Q 1
-#endif
 
 namespace hx {
 
@@ -220,37 +217,18 @@ struct GroupedGemmArgs {
     int rs_n;
 };
 
-#if HX_MF_Q
-typedef MfmaSmemQ GemmSmem;
-#ifndef HX_MFQ_OCC
-#define HX_MFQ_OCC 3
-#endif
-#else
-typedef MfmaSmem GemmSmem;
-#define HX_MFQ_OCC 2
-#endif
-
 template <int BITS, int CB, int BM>
-__device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job& job, int proj, int cg, GemmSmem& sm)
+__device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job& job, int proj, int cg, MfmaSmemQ& sm)
 {
     const _Float16* A = g.A[proj] + (size_t)job.row0 * g.K;
     const uint32_t* tr = static_cast<const uint32_t*>(g.tr[proj][job.expert]);
-#if HX_MF_Q
     hx_f4 acc[BM / 16][2];
     mfma_tile_q<BITS, CB, BM, QT_PF, true>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc,
                                             g.rs[proj] + (size_t)job.row0 * g.rs_n, g.rs_n);
-#else
-    hx_f4 acc[BM / 32][4];
-    mfma_tile<BITS, CB, BM>(A, g.K, job.rows, tr, g.K, g.N, cg * 8, sm, acc);
-#endif
     _Float16* out = g.out[proj] + (size_t)job.row0 * g.N + cg * 128;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int half = 0; half < (BM + 63) / 64; ++half) {
-#if HX_MF_Q
         qt_stage_c_half<BM>(acc, half, sm);
-#else
-        stage_c_half<BM>(acc, half, sm);
-#endif
         __syncthreads();
         for (int r = wave; r < 64; r += 4) {
             const int row = 64 * half + r;
@@ -263,9 +241,9 @@ __device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job
 }
 
 template <int CB>
-__global__ __launch_bounds__(MF_THREADS, HX_MFQ_OCC) void grouped_gemm_kernel(GroupedGemmArgs g)
+__global__ __launch_bounds__(MF_THREADS, 3) void grouped_gemm_kernel(GroupedGemmArgs g)
 {
-    __shared__ GemmSmem sm;
+    __shared__ MfmaSmemQ sm;
     const int job_i = blockIdx.y;
     if (job_i >= *g.njobs) return;
     const Job job = g.jobs[job_i];
@@ -310,7 +288,6 @@ struct GuArgs {
     float* rs_act;       // [R][inter / 128] row sums of act per 128-column block
 };
 
-#if HX_MF_Q
 // accumulator of the gate/up tiles (quarter-operand layout); LDS: the tile's A buffers, reused as the
 // staging block of the matrix-core Hadamard transforms (H128 itself is generated in registers)
 template <int BM>
@@ -322,26 +299,13 @@ struct GuSmem {
     };
     float rowsum[MF_BM];
 };
-#ifndef HX_GU_OCC
-#define HX_GU_OCC 3
-#endif
-#else
-template <int BM>
-using GuAcc = hx_f4[BM / 32][4];
-typedef MfmaSmem GuSmem;
-#define HX_GU_OCC 2
-#endif
 
 template <int BITS, int CB, int BM>
 __device__ __forceinline__ void gu_tile(const _Float16* A, int K, int rows, const void* tr, int N, int cg,
                                         GuSmem& sm, GuAcc<BM>& acc, const float* rs)
 {
-#if HX_MF_Q
     mfma_tile_q<BITS, CB, BM, QT_PF, true>(A, K, rows, static_cast<const uint32_t*>(tr), K, N, cg * 8, sm, acc, rs,
                                            K / 128);
-#else
-    mfma_tile<BITS, CB, BM>(A, K, rows, static_cast<const uint32_t*>(tr), K, N, cg * 8, sm, acc);
-#endif
 }
 
 template <int CB, int BM>
@@ -372,14 +336,7 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
     const int e = job.expert;
     const int bg = a.bits_tab[0] ? a.bits_tab[0][e] : a.bits_uniform[0];
     const int bu = a.bits_tab[1] ? a.bits_tab[1][e] : a.bits_uniform[1];
-#if HX_MF_Q
     _Float16* X = sm.hx;
-#define HX_HAD(dst) hadamard_mfma_reg<BM>(X, dst)
-#else
-    _Float16* H = sm.hx;
-    _Float16* X = sm.hx + 128 * MF_LDA2;
-#define HX_HAD(dst) hadamard_mfma<BM>(X, H, dst)
-#endif
     auto mapped = [&](int row, float v) -> float {
         if constexpr (CB == 2) return fmaf(v, CB2_SCALE, CB2_BIAS * sm.rowsum[row]);
         else return v;
@@ -407,29 +364,18 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
     if (gated) {
         gu_tile_bits<CB, BM>(bg, a.xg + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[0][e], a.N, cg, sm, acc,
                              a.rs_g + (size_t)job.row0 * (a.K / 128));
-#if HX_MF_Q
         qt_foreach<BM>(acc, [&](int row, int col, float v) {
             if (row < job.rows) gs[(size_t)row * a.N + col] = (_Float16)mapped(row, v);
         });
-#else
-        frag_store(gs, [&](int row, int, float v) { return (_Float16)mapped(row, v); });
-#endif
         __syncthreads();  // rowsum is reused by the up tile
     }
     gu_tile_bits<CB, BM>(bu, a.xu + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[1][e], a.N, cg, sm, acc,
                          a.rs_u + (size_t)job.row0 * (a.K / 128));
 
     // u = fp16(H(U)) * svh_u
-#if !HX_MF_Q
-    h128_to_lds(H);
-#endif
-#if HX_MF_Q
     qt_foreach<BM>(acc, [&](int row, int col, float v) { X[row * MF_LDA2 + col] = (_Float16)mapped(row, v); });
-#else
-    acc_to_lds_f16<BM>(acc, X, [&](int row, int, float v) { return mapped(row, v); });
-#endif
     __syncthreads();
-    HX_HAD(hacc);
+    hadamard_mfma_reg<BM>(X, hacc);
     const _Float16* svg = gated ? static_cast<const _Float16*>(a.svh[0][e]) + cg * 128 : nullptr;
     const _Float16* svu = static_cast<const _Float16*>(a.svh[1][e]) + cg * 128;
     const _Float16* sud = static_cast<const _Float16*>(a.suh_d[e]) + cg * 128;
@@ -444,7 +390,7 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
             *reinterpret_cast<hx_u4v*>(&X[row * MF_LDA2 + c8]) = v;
         }
         __syncthreads();
-        HX_HAD(hacc);
+        hadamard_mfma_reg<BM>(X, hacc);
     }
     const float L = a.act_limit;
     const _Float16 Lh = (_Float16)L, nLh = (_Float16)(-L);
@@ -470,7 +416,7 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
     }
     __syncthreads();
     // act = fp16(H(p)), staged back to LDS for row-wise stores
-    HX_HAD(hacc);
+    hadamard_mfma_reg<BM>(X, hacc);
     __syncthreads();
     acc_to_lds_f16<BM>(hacc, X, [](int, int, float v) { return v; });
     __syncthreads();
@@ -491,10 +437,9 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
         if ((i & 15) == 0 && row < job.rows) a.rs_act[(size_t)(job.row0 + row) * nblk + cg] = sum;
     }
 }
-#undef HX_HAD
 
 template <int CB>
-__global__ __launch_bounds__(MF_THREADS, HX_GU_OCC) void grouped_gu_kernel(GuArgs a)
+__global__ __launch_bounds__(MF_THREADS, 3) void grouped_gu_kernel(GuArgs a)
 {
     __shared__ GuSmem sm;
     const int job_i = blockIdx.y;
