@@ -201,3 +201,10 @@ def test_moe_grouped_activations(hx, act, T):
     got = y.cpu().numpy()
     assert np.isfinite(got).all()
     assert_close(got, ref, what=f"act={act} T={T}")
+
+
+@pytest.mark.parametrize("topk", [1, 2, 6, 16])
+def test_moe_prefill_topk_variants(hx, topk):
+    """The matrix-core combine serves topk dividing 16 (1, 2, 16 here, besides 4 and 8 above), the
+    per-token combine any other topk (6)."""
+    _run_layer(hx, E=32, hidden=256, inter=256, topk=topk, T=20, bits=2, shared_bits=2, seed=950 + topk)

@@ -574,3 +574,18 @@ def test_moe_rows_relu2_nogate(L):
         xh = (x.view(np.float16) * np.float16(0.5)).view(np.uint16)
         yh, _ = O.moe_rows(xh, hidden, inter, idx, w, np.arange(T), ex, None, 0.0, act=2)
         assert np.abs(4 * yh - yr).max() <= 2e-2 * scale
+
+
+def test_h128_register_sign_pattern():
+    """The sign rule the matrix-core Hadamard kernels use to build H128 B operands in registers: for
+    n = 16 nb + c and k = 32 kk + 8 g + j (c < 16, g < 4, j < 8), popcount(n & k) is odd exactly when
+    popcount(c & j & 7) + (c3 & g0) + (nb0 & g1) + (nb1 & kk0) + (nb2 & kk1) is odd -- checked against
+    scipy's Sylvester matrix over all 128 x 128 entries."""
+    H = scipy.linalg.hadamard(128)
+    for n in range(128):
+        nb, c = n >> 4, n & 15
+        for k in range(128):
+            kk, g, j = k >> 5, (k >> 3) & 3, k & 7
+            par = (bin(c & j & 7).count("1") + ((c >> 3) & g & 1) + ((nb & 1) & (g >> 1)) + ((nb >> 1) & kk & 1)
+                   + ((nb >> 2) & (kk >> 1) & 1)) & 1
+            assert H[k, n] == (-1 if par else 1)
