@@ -398,7 +398,8 @@ __device__ __forceinline__ float* gemv_lds()
 //
 // before_input() runs after the tile prefetch is issued and before a pre-transformed input is read
 // (a consumer waits there for its producer); after_input() runs once the input is in LDS.
-template <int BITS, int CB, int MT, int KS = 1, class Before = NoHook, class After = NoHook>
+// PF4: steps of tile words in flight per wave for bit widths up to 4 (wider words: 4).
+template <int BITS, int CB, int MT, int KS = 1, int PF4 = 8, class Before = NoHook, class After = NoHook>
 __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, int kc, uint32_t* a_lds, float* colsum,
                                            Before before_input = Before(), After after_input = After())
 {
@@ -428,7 +429,7 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     // consumes one ring slot and refills it PF steps ahead (past the end the load repeats the range's
     // last tile row, so the number of loads in flight is the same at every step and each wait is a
     // static count).
-    constexpr int PF = BITS <= 4 ? 8 : 4;
+    constexpr int PF = BITS <= 4 ? PF4 : 4;
     uint32_t buf[PF][BITS + 1];
     // byte offsets: lane part (tile row gq of the step, tile column tn, quarter q) and step part
     // (tile rows (k0 + step_k) / 16); the tensor is (K/16) x (N/16) tiles

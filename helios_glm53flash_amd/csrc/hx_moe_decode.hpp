@@ -18,6 +18,15 @@
 #pragma once
 #include "hx_gemv.hpp"
 
+// Table entries of every expert loaded with the scores (1) or the slot's entries after the ranking (0).
+#ifndef HX_DEC_PFTAB
+#define HX_DEC_PFTAB 1
+#endif
+// ... and the epilogue tables of every expert with the scores (1), or the slot's after the plan (0).
+#ifndef HX_DEC_PFEP
+#define HX_DEC_PFEP 1
+#endif
+
 namespace hx {
 
 constexpr int DEC_MAX_R = 64;  // T * topk rows handled by the few-token path
@@ -322,7 +331,7 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
         // loads trellis and suh (parked after its selection, which then waits for the scores only,
         // as loads complete in order), wave 1 the epilogue tables.  The owning lane of the slot's
         // expert takes trellis and suh after the ranking, thread 0 the rest after the plan barrier.
-        const bool pf_tab = my_slot >= 0 && a.E <= TAB_MAX_E;
+        const bool pf_tab = my_slot >= 0 && HX_DEC_PFTAB && a.E <= TAB_MAX_E;
         auto load_tabs = [&](int q0, int q1, uint64_t (*v)[TPL]) {
 #pragma unroll
             for (int q = q0; q < q1; ++q) {
@@ -341,7 +350,7 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
         auto prefetch = [&]() {
             if (pf_tab && wave == 0) load_tabs(0, 2, v_main);
         };
-        if (pf_tab && wave == 1) {
+        if (pf_tab && HX_DEC_PFEP && wave == 1) {
             uint64_t v_ep[DEC_TABS - 2][TPL];
             load_tabs(2, DEC_TABS, v_ep);
             park_tabs(2, DEC_TABS, v_ep);
@@ -462,10 +471,17 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
     }
     __syncthreads();
     // the slot's epilogue tables (the epilogues read them after later barriers)
-    if (a.scores && threadIdx.x == 0 && my_slot >= 0 && my_slot < p.n && a.E <= TAB_MAX_E) {
+    if (a.scores && threadIdx.x == 0 && my_slot >= 0 && my_slot < p.n && HX_DEC_PFTAB && a.E <= TAB_MAX_E) {
         const int e = p.expert[my_slot];
 #pragma unroll
-        for (int q = 2; q < DEC_TABS; ++q) set_tab(p.tab, q, bits_ptr(tab_lds[q][e]));
+        for (int q = 2; q < DEC_TABS; ++q) {
+            if constexpr (HX_DEC_PFEP) {
+                set_tab(p.tab, q, bits_ptr(tab_lds[q][e]));
+            } else {
+                const void* const* b = tab_base(a, q, proj);
+                set_tab(p.tab, q, b ? b[e] : nullptr);
+            }
+        }
     }
 }
 
@@ -652,6 +668,14 @@ __device__ __forceinline__ void combine_columns(const MoeDecodeArgs& a, const De
 #define HX_DEC_KS 1
 #endif
 constexpr int DEC_KS = HX_DEC_KS;
+// Tile-word steps in flight per wave in the layer kernel (up to 4 bits).  Every resident unit's ring
+// is in flight at once, and the queue that builds up in the memory system delays each unit's own
+// dependent loads (scores, inputs, flags, partial sums): measured at config 3, 8 steps 54.2 us,
+// 4 steps 52.8 us, 3 steps 52.0 us, 2 steps 53.1 us.  (The dense GEMV keeps 8: it streams alone.)
+#ifndef HX_DEC_PF
+#define HX_DEC_PF 3
+#endif
+constexpr int DEC_PF = HX_DEC_PF;
 constexpr int DEC_THREADS = 256 * DEC_KS;
 
 // Bounded wait of thread 0 for *flag >= target (the producers are resident workgroups that do not
@@ -760,7 +784,7 @@ __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodeP
     g.K = a.hidden;
     g.N = a.inter;
     g.pre_transformed = false;
-    gemv_range<BITS, CB, MT, DEC_KS>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
+    gemv_range<BITS, CB, MT, DEC_KS, DEC_PF>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
 
     // partial of segment i of (slot, proj, cg): partial_{g,u}[((slot*gg + cg) * (KB + 1) + i) * 8 + m][128]
     float* pbase = (proj == 0 ? a.partial_g : a.partial_u) + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
@@ -792,7 +816,7 @@ __device__ __forceinline__ void d_segment(const MoeDecodeArgs& a, const DecodePl
             for (int kb = kb0; kb < kb1; ++kb) wait_flag(&a.ready[slot * gg + kb], 1, a.status);
         hx_lds_barrier();
     };
-    gemv_range<BITS, CB, MT, DEC_KS>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs, wait_inputs);
+    gemv_range<BITS, CB, MT, DEC_KS, DEC_PF>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs, wait_inputs);
 
     const int count = sp.count(c);
     float* pbase = a.partial_d + (size_t)(slot * gd + cg) * (KB + 1) * 8 * 128;
