@@ -22,6 +22,17 @@
 
 namespace hx {
 
+// Tile-word steps in flight per wave in the dense linear, up to 4 bits / wider.  Fewer steps in
+// flight shorten the memory queue that every workgroup's dependent loads (inputs, partial sums,
+// arrival counters) wait behind: config 2 (4096 -> 12288, 4-bit) at M = 1 measured 15.6 us with
+// 8 steps, 13.9 with 4, 13.4 with 2; the 5-bit lm_head is flat between 2 and 4.
+#ifndef HX_LIN_PF
+#define HX_LIN_PF 2
+#endif
+#ifndef HX_LIN_PFW
+#define HX_LIN_PFW 4
+#endif
+
 constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_WAVES = 4;
 
@@ -398,8 +409,8 @@ __device__ __forceinline__ float* gemv_lds()
 //
 // before_input() runs after the tile prefetch is issued and before a pre-transformed input is read
 // (a consumer waits there for its producer); after_input() runs once the input is in LDS.
-// PF4: steps of tile words in flight per wave for bit widths up to 4 (wider words: 4).
-template <int BITS, int CB, int MT, int KS = 1, int PF4 = 8, class Before = NoHook, class After = NoHook>
+// PF4 / PFW: steps of tile words in flight per wave for bit widths up to 4 / wider.
+template <int BITS, int CB, int MT, int KS = 1, int PF4 = 8, int PFW = 4, class Before = NoHook, class After = NoHook>
 __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, int kc, uint32_t* a_lds, float* colsum,
                                            Before before_input = Before(), After after_input = After())
 {
@@ -429,7 +440,7 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     // consumes one ring slot and refills it PF steps ahead (past the end the load repeats the range's
     // last tile row, so the number of loads in flight is the same at every step and each wait is a
     // static count).
-    constexpr int PF = BITS <= 4 ? PF4 : 4;
+    constexpr int PF = BITS <= 4 ? PF4 : PFW;
     uint32_t buf[PF][BITS + 1];
     // byte offsets: lane part (tile row gq of the step, tile column tn, quarter q) and step part
     // (tile rows (k0 + step_k) / 16); the tensor is (K/16) x (N/16) tiles
@@ -554,7 +565,8 @@ __device__ __forceinline__ void gemv_split_sum(const GemvArgs& g, int cg, int s,
                                                Before before_input = Before(), After after_input = After())
 {
     const int k0 = s * g.kc;
-    gemv_range<BITS, CB, MT>(g, cg, k0, min(g.kc, g.K - k0), a_lds, colsum, before_input, after_input);
+    gemv_range<BITS, CB, MT, 1, HX_LIN_PF, HX_LIN_PFW>(g, cg, k0, min(g.kc, g.K - k0), a_lds, colsum, before_input,
+                                                   after_input);
 }
 
 // Cross-workgroup handoff of split-K partials.  An agent-scope release/acquire fence pair would
