@@ -19,6 +19,7 @@
 // The counter is reset by that workgroup, so the workspace stays reusable without clearing.
 #pragma once
 #include "hx_device.hpp"
+#include <type_traits>
 
 namespace hx {
 
@@ -102,6 +103,10 @@ HX_INLINE uint32_t quarter_reg(const uint32_t* r)
     else return __builtin_amdgcn_alignbit(r[j - 1], r[j], 32 - rr);
 }
 
+// Register slot of decoded pair i of a quarter (positions 2i, 2i+1): operand-major, so that the
+// four pairs of each MFMA B operand (quarter_operand) sit in consecutive registers.
+HX_INLINE constexpr int qpos(int i) { return 4 * (i & 3) + (i >> 2); }
+
 // x = window * 0x83DCD12D mod 2^32 for four 16-bit windows: the low and high halves of ra and rb
 // (hi = true) or the low halves of ra, rb, rc, rd (hi = false).  Each product is one
 // v_pk_mul_lo_u16 making (w * 0x83DC) << 16 and one v_mad_u32_u16 adding w * 0xD12D (both full-rate
@@ -181,7 +186,7 @@ template <int BITS, int CB, int P = 0>
 HX_INLINE void quarter_decode_generic(const uint32_t* r, uint32_t* out)
 {
     if constexpr (P < 32) {
-        out[P / 2] = h2_as_u32(hx_decode2<CB>(quarter_reg<(P + 1) * BITS + 32>(r) & 0xffffu,
+        out[qpos(P / 2)] = h2_as_u32(hx_decode2<CB>(quarter_reg<(P + 1) * BITS + 32>(r) & 0xffffu,
                                               quarter_reg<(P + 2) * BITS + 32>(r) & 0xffffu));
         quarter_decode_generic<BITS, CB, P + 2>(r, out);
     }
@@ -205,7 +210,7 @@ HX_INLINE void mul1_dec4(const uint32_t* x, uint32_t& d0, uint32_t& d1, uint32_t
     d3 = h2_as_u32(__builtin_elementwise_fma(u32_as_h2(h[3]), c1, c0));
 }
 
-// Decoded fp16 pairs of a quarter: out[i] = positions (2i, 2i+1) = (k, k+1) of one column.
+// Decoded fp16 pairs of a quarter: out[qpos(i)] = positions (2i, 2i+1) = (k, k+1) of one column.
 template <int BITS, int CB>
 HX_INLINE void quarter_decode(const uint32_t* r, uint32_t* out)
 {
@@ -216,7 +221,7 @@ HX_INLINE void quarter_decode(const uint32_t* r, uint32_t* out)
         for (int o = 0; o < 4; ++o) {  // the pairs of MFMA operand o: pair indices o, o+4, o+8, o+12
             const uint32_t xs[8] = {x[2 * o], x[2 * o + 1], x[2 * o + 8], x[2 * o + 9],
                                     x[2 * o + 16], x[2 * o + 17], x[2 * o + 24], x[2 * o + 25]};
-            mul1_dec4(xs, out[o], out[o + 4], out[o + 8], out[o + 12]);
+            mul1_dec4(xs, out[4 * o], out[4 * o + 1], out[4 * o + 2], out[4 * o + 3]);
         }
     } else {
         quarter_decode_generic<BITS, CB>(r, out);
@@ -253,7 +258,7 @@ HX_INLINE void quarter_affine_pairs(const uint32_t* r, const uint32_t* M, uint32
     if constexpr (P < 32) {
         const uint32_t x0 = quarter_window<BITS, P>(r, M) * 0x83DCD12Du;
         const uint32_t x1 = quarter_window<BITS, P + 1>(r, M) * 0x83DCD12Du;
-        out[P / 2] = __builtin_amdgcn_sad_hi_u8(x1, 0u, __builtin_amdgcn_sad_u8(x0, 0u, 0x64006400u));
+        out[qpos(P / 2)] = __builtin_amdgcn_sad_hi_u8(x1, 0u, __builtin_amdgcn_sad_u8(x0, 0u, 0x64006400u));
         quarter_affine_pairs<BITS, P + 2>(r, M, out);
     }
 }
@@ -265,12 +270,12 @@ HX_INLINE void quarter_affine_range(const uint32_t* r, const uint32_t* M, uint32
     if constexpr (P0 < P1) {
         const uint32_t x0 = quarter_window<BITS, P0>(r, M) * 0x83DCD12Du;
         const uint32_t x1 = quarter_window<BITS, P0 + 1>(r, M) * 0x83DCD12Du;
-        out[P0 / 2] = __builtin_amdgcn_sad_hi_u8(x1, 0u, __builtin_amdgcn_sad_u8(x0, 0u, 0x64006400u));
+        out[qpos(P0 / 2)] = __builtin_amdgcn_sad_hi_u8(x1, 0u, __builtin_amdgcn_sad_u8(x0, 0u, 0x64006400u));
         quarter_affine_range<BITS, P0 + 2, P1>(r, M, out);
     }
 }
 
-// h of a quarter as fp16 pairs: out[i] = positions (2i, 2i+1) = (k, k+1) of one column.
+// h of a quarter as fp16 pairs: out[qpos(i)] = positions (2i, 2i+1) = (k, k+1) of one column.
 template <int BITS>
 HX_INLINE void quarter_affine(const uint32_t* r, uint32_t* out)
 {
@@ -281,17 +286,18 @@ HX_INLINE void quarter_affine(const uint32_t* r, uint32_t* out)
 }
 
 // MFMA B operand (nh, kh) of a decoded quarter: column 8nh+q, k = 8kh + 0..7, i.e. local positions
-// 2kh + 4nh + 8j + {0, 1} for j = 0..3.
+// 2kh + 4nh + 8j + {0, 1} for j = 0..3: pairs I0 + 4j, I0 = kh + 2nh, stored at out[4 I0 + j] (qpos),
+// so an operand is four consecutive registers and needs no moves.
 template <int NH, int KH>
 HX_INLINE hx_h8 quarter_operand(const uint32_t* d)
 {
-    constexpr int I0 = KH + 2 * NH;  // pair index of positions 2kh + 4nh
+    constexpr int I0 = KH + 2 * NH;
     typedef uint32_t u4v __attribute__((ext_vector_type(4)));
     u4v v;
-    v.x = d[I0];
-    v.y = d[I0 + 4];
-    v.z = d[I0 + 8];
-    v.w = d[I0 + 12];
+    v.x = d[4 * I0];
+    v.y = d[4 * I0 + 1];
+    v.z = d[4 * I0 + 2];
+    v.w = d[4 * I0 + 3];
     return __builtin_bit_cast(hx_h8, v);
 }
 
@@ -482,7 +488,9 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     hx_f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
     const int am = min(lane & 15, g.M - 1);  // A row of this lane (rows >= M repeat the last row)
     const _Float16* arow = reinterpret_cast<const _Float16*>(a_lds) + (size_t)am * kc;
-    for (int st0 = 0; st0 < steps; st0 += PF) {
+    // one group of PF steps; GUARD: the group runs past the range (only the last group can)
+    auto group = [&](int st0, auto guard) {
+        constexpr bool GUARD = decltype(guard)::value;
 #pragma unroll
         for (int j = 0; j < PF; ++j) {
             const int st = st0 + j;
@@ -498,13 +506,14 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
             // steps would otherwise decode the repeated last row); every refill is issued (past the
             // range it repeats the last row, an L2 hit), so that the count of loads in flight, and
             // so every wait, is the same at every step
+            const bool live = !GUARD || st < steps;
             uint32_t d[16];
-            if (st < steps) {
+            if (live) {
                 if constexpr (AFFINE) quarter_affine<BITS>(buf[j], d);
                 else quarter_decode<BITS, CB>(buf[j], d);
             }
             load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff(st + PF));
-            if (st < steps) {
+            if (live) {
                 const int kl = step_k(st) + 16 * gq;
                 const hx_h8 a0 = *reinterpret_cast<const hx_h8*>(arow + kl);
                 const hx_h8 a1 = *reinterpret_cast<const hx_h8*>(arow + kl + 8);
@@ -513,8 +522,16 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
                 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, quarter_operand<1, 0>(d), acc1, 0, 0, 0);
                 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, quarter_operand<1, 1>(d), acc1, 0, 0, 0);
             }
+            // keeps each step's decode after the previous step's refill: the scheduler does not see
+            // the memory wait a decode implies, and one hoisted into an earlier step waits there for
+            // every load in flight
+            if (j + 1 < PF) __builtin_amdgcn_sched_barrier(0);
         }
-    }
+    };
+    // whole groups run without per-step branches, so each group is one block
+    int st0 = 0;
+    for (; st0 + PF <= steps; st0 += PF) group(st0, std::false_type{});
+    if (st0 < steps) group(st0, std::true_type{});
 
     HX_SETPRIO(3);  // the split-K handoff and epilogues are on the critical path
     // C: lane holds rows 4*(lane/16) + i of column label lane%16 = 8t + q; label -> column
