@@ -670,10 +670,11 @@ __device__ __forceinline__ void combine_columns(const MoeDecodeArgs& a, const De
 constexpr int DEC_KS = HX_DEC_KS;
 // Tile-word steps in flight per wave in the layer kernel (up to 4 bits).  Every resident unit's ring
 // is in flight at once, and the queue that builds up in the memory system delays each unit's own
-// dependent loads (scores, inputs, flags, partial sums): measured at config 3, 8 steps 54.2 us,
-// 4 steps 52.8 us, 3 steps 52.0 us, 2 steps 53.1 us.  (The dense GEMV keeps 8: it streams alone.)
+// dependent loads (scores, inputs, flags, partial sums): measured at config 3 (layer time), 8 steps
+// 51.1 us, 6 steps 49.8 us, 5 steps 49.6 us, 4 steps 49.4 us, 3 steps 50.5 us, 2 steps 51.7 us.
+// (The linear GEMV keeps its own ring depth: it streams alone.)
 #ifndef HX_DEC_PF
-#define HX_DEC_PF 3
+#define HX_DEC_PF 4
 #endif
 constexpr int DEC_PF = HX_DEC_PF;
 constexpr int DEC_THREADS = 256 * DEC_KS;
