@@ -35,13 +35,17 @@ constexpr int MF_BK = 64;
 constexpr int MF_LDA = HX_MF_SWZ ? MF_BK : MF_BK + 8;  // halves per LDS row
 constexpr int MF_LDC = MF_BN + 4;  // floats per LDS row in the epilogue
 
-// Offset (halves) of 16-byte chunk c (8 halves of k) of LDS row r.
-HX_INLINE int mf_off(int r, int c)
+// Chunk permutation of LDS row r (an XOR, so it is its own inverse: slot c of row r holds chunk
+// c ^ mf_swz(r)).
+HX_INLINE int mf_swz(int r)
 {
-    if constexpr (HX_MF_SWZ == 2) return r * MF_LDA + 8 * (c ^ ((r & 7) ^ ((r >> 3) & 1)));
-    else if constexpr (HX_MF_SWZ) return r * MF_LDA + 8 * (c ^ (((r >> 1) & 7) ^ (((r >> 4) & 1) << 2)));
-    else return r * MF_LDA + 8 * c;
+    if constexpr (HX_MF_SWZ == 2) return (r & 7) ^ ((r >> 3) & 1);
+    else if constexpr (HX_MF_SWZ) return ((r >> 1) & 7) ^ (((r >> 4) & 1) << 2);
+    else return 0;
 }
+
+// Offset (halves) of 16-byte chunk c (8 halves of k) of LDS row r.
+HX_INLINE int mf_off(int r, int c) { return r * MF_LDA + 8 * (c ^ mf_swz(r)); }
 
 HX_INLINE __amdgpu_buffer_rsrc_t mf_rsrc(const void* base, size_t bytes)
 {
@@ -70,16 +74,42 @@ HX_INLINE void qt_rowcol(int rb, int nh, int i, int& row, int& col)
     col = 32 * wave + 16 * ((lane >> 3) & 1) + 8 * nh + (lane & 7);
 }
 
-// Chunks of global loads in flight for the quarter-operand tile (2 keeps it at 3 workgroups per CU).
+// Chunks of global loads in flight for the quarter-operand tile (2 keeps it at 3 workgroups per CU):
+// A chunks (QT_PF) and trellis-word chunks (QT_PT).
 #ifndef HX_QT_PF
 #define HX_QT_PF 2
 #endif
+#ifndef HX_QT_PT
+#define HX_QT_PT 2
+#endif
+#ifndef HX_QT_IL
+#define HX_QT_IL 1
+#endif
+// workgroups per CU the MFMA-tile kernels are compiled for (their register budget)
+#ifndef HX_QT_OCC
+#define HX_QT_OCC 3
+#endif
 constexpr int QT_PF = HX_QT_PF;
+constexpr int QT_PT = HX_QT_PT;
+// LDS A buffers: with A loaded straight into LDS, the chunks in flight and the one being read
+constexpr int QT_NB = QT_PF + 1;
+// s_waitcnt immediate that waits until at most n vector-memory instructions are outstanding
+// (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their no-wait maxima)
+constexpr int qt_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+#ifndef HX_QT_DMA
+#define HX_QT_DMA 1
+#endif
+constexpr int qt_lcm(int a, int b)
+{
+    int x = a, y = b;
+    while (y) { const int r = x % y; x = y; y = r; }
+    return a / x * b;
+}
 
 // LDS of a kernel that uses only quarter-operand tiles: the A buffers, the epilogue staging.
 struct MfmaSmemQ {
     union {
-        _Float16 ab[2][MF_BM * MF_LDA];
+        _Float16 ab[QT_NB][MF_BM * MF_LDA];
         float c[64 * MF_LDC];
     };
     float rowsum[MF_BM];
@@ -114,15 +144,39 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
     const int voff0 = t_off + ((q * BITS + NW - 1) % NW) * 4, voff1 = t_off + q * BITS * 4;
     const int row_bytes = tiles_n * NW * 4;
 
-    hx_u4v av[PF][NA];
-    uint32_t wv[PF][BITS + 1];
+    // A and the trellis words have rings of their own: PF chunks of A (16 VGPRs per chunk at BM 128),
+    // PT chunks of trellis words (BITS + 1 VGPRs per chunk)
+    constexpr int PT = QT_PT;
+    // A through LDS by DMA, unless the tile sums A's rows itself (that reads A in registers)
+    constexpr bool DMA = HX_QT_DMA && (EXT_RS || CB != 2);
+    static_assert(!DMA || (MF_LDA == MF_BK && PF + 1 <= QT_NB), "A ring in LDS");
+    hx_u4v av[DMA ? 1 : PF][NA];
+    uint32_t wv[PT][BITS + 1];
     float rs[NA];
 #pragma unroll
     for (int i = 0; i < NA; ++i) rs[i] = 0.0f;
-    auto load_chunk = [&](int slot, int k0) {
+    auto load_a = [&](int slot, int k0) {
 #pragma unroll
         for (int i = 0; i < NA; ++i) av[slot][i] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[i], k0 * 2, 0);
-        load_quarter_buf<BITS>(wv[slot], rt, voff0, voff1, (k0 >> 4) * row_bytes);
+    };
+    auto load_t = [&](int slot, int k0) { load_quarter_buf<BITS>(wv[slot], rt, voff0, voff1, (k0 >> 4) * row_bytes); };
+    // A straight into LDS (buffer loads with an LDS destination): instruction i of wave w fills rows
+    // 32i + 8w .. +7 of the buffer, lane l 16 bytes at slot l % 8 of row 32i + 8w + l / 8, so the lane
+    // fetches the chunk that the swizzle puts in that slot.  Rows past the tile's end read zeros (the
+    // buffer resource's range).  The loads use no registers, so with DMA A has QT_NB LDS buffers and
+    // no register ring.
+    int a_voff_lds[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int r = 32 * i + 8 * wave + (lane >> 3);
+        a_voff_lds[i] = (int)(((size_t)r * lda + 8 * ((lane & 7) ^ mf_swz(r))) * sizeof(_Float16));
+    }
+    auto load_a_lds = [&](int buf, int k0) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void*)(&sm.ab[buf][(32 * i + 8 * wave) * MF_LDA]), 16,
+                a_voff_lds[i], k0 * 2, 0, 0);
     };
     auto store_a = [&](int slot, int buf, bool count) {
         _Float16* as = sm.ab[buf];
@@ -159,40 +213,101 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
             }
     }
 #pragma unroll
-    for (int s = 0; s < PF; ++s) load_chunk(s, min(s, nk - 1) * MF_BK);
-    store_a(0, 0, true);
-    // d holds the decoded quarter of the chunk being multiplied; the next chunk's quarter is decoded
-    // while the matrix cores work on this one
-    uint32_t d[16];
-    decode(0, d);
+    for (int s = 0; s < (PF > PT ? PF : PT); ++s) {
+        if (s < PF) {
+            if constexpr (DMA) load_a_lds(s, min(s, nk - 1) * MF_BK);
+            else load_a(s, min(s, nk - 1) * MF_BK);
+        }
+        if (s < PT) load_t(s, min(s, nk - 1) * MF_BK);
+    }
+    // VMEM instructions per chunk: A (DMA) and trellis words; chunk c + 1's A is complete once at
+    // most the loads of the PF - 1 later chunks are outstanding (their order within a step is left
+    // to the compiler, so the count takes whole chunks)
+    constexpr int NT = 1 + (BITS + 3) / 4;
+    constexpr int A_WAIT = (PF - 1) * (NA + NT);
+    static_assert(!DMA || A_WAIT < 64, "vmcnt range");
+    // chunk 0: the prologue issued at most the other chunks' loads after it
+    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(qt_vmcnt((PF - 1) * NA + (PT - 1) * NT));
+    else store_a(0, 0, true);
+    // d[c & 1] holds the decoded quarter of chunk c; the next chunk's quarter is decoded into the
+    // other half while the matrix cores work on this one, interleaved with the MFMAs in one block
+    uint32_t d[2][16];
+    decode(0, d[0]);
     hx_lds_barrier();
-    auto step = [&](int c, int u) {
-        load_chunk(u, min(c + PF, nk - 1) * MF_BK);
-        const _Float16* as = sm.ab[c & 1];
-        const hx_h8 b00 = quarter_operand<0, 0>(d), b01 = quarter_operand<0, 1>(d);
-        const hx_h8 b10 = quarter_operand<1, 0>(d), b11 = quarter_operand<1, 1>(d);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
+    // step c: ua = c % PF, ut = c % PT, par = c & 1, all compile-time in the unrolled loops
+    auto step = [&](int c, auto ua_, auto ut_, auto par_) {
+        constexpr int ua = decltype(ua_)::value, ut = decltype(ut_)::value, par = decltype(par_)::value;
+        if constexpr (DMA) load_a_lds((c + PF) % QT_NB, min(c + PF, nk - 1) * MF_BK);
+        else load_a(ua, min(c + PF, nk - 1) * MF_BK);
+        load_t(ut, min(c + PT, nk - 1) * MF_BK);
+        const _Float16* as = sm.ab[DMA ? c % QT_NB : c & 1];
+        const uint32_t* dc = d[par];
+        uint32_t* dn = d[par ^ 1];
+        const hx_h8 b00 = quarter_operand<0, 0>(dc), b01 = quarter_operand<0, 1>(dc);
+        const hx_h8 b10 = quarter_operand<1, 0>(dc), b11 = quarter_operand<1, 1>(dc);
+        auto read_a = [&](int rb, hx_h8& a0, hx_h8& a1) {
             const int r = 16 * rb + (lane & 15);
-            const hx_h8 a0 = *reinterpret_cast<const hx_h8*>(&as[mf_off(r, 2 * g)]);
-            const hx_h8 a1 = *reinterpret_cast<const hx_h8*>(&as[mf_off(r, 2 * g + 1)]);
+            a0 = *reinterpret_cast<const hx_h8*>(&as[mf_off(r, 2 * g)]);
+            a1 = *reinterpret_cast<const hx_h8*>(&as[mf_off(r, 2 * g + 1)]);
+        };
+        auto mfma_ab = [&](int rb, const hx_h8& a0, const hx_h8& a1) {
             acc[rb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b00, acc[rb][0], 0, 0, 0);
             acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b10, acc[rb][1], 0, 0, 0);
             acc[rb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b01, acc[rb][0], 0, 0, 0);
             acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b11, acc[rb][1], 0, 0, 0);
+        };
+        auto mfma_rb = [&](int rb) {
+            hx_h8 a0, a1;
+            read_a(rb, a0, a1);
+            mfma_ab(rb, a0, a1);
+        };
+        if constexpr (CB == 2 && HX_QT_IL) {
+            // the next chunk's decode is cut into RB slices, one per row block: piece R reads the A
+            // fragments of row block R + 1, decodes slice R and issues row block R's MFMAs, so the
+            // slice's VALU work runs while the previous MFMAs execute and the LDS reads have a
+            // whole piece to land.  The fences keep that order (left alone, the scheduler gathers
+            // all MFMAs in one run and the decode in another).
+            const uint32_t* wn = wv[(ut + 1) % PT];
+            uint32_t M[BITS + 1];
+#pragma unroll
+            for (int j = 1; j <= BITS; ++j) M[j] = __builtin_amdgcn_alignbit(wn[j - 1], wn[j], 16);
+            constexpr int PS = 32 / RB;
+            hx_h8 fa[2][2];
+            read_a(0, fa[0][0], fa[0][1]);
+            [&]<int... R>(std::integer_sequence<int, R...>) {
+                (((R + 1 < RB ? read_a(R + 1, fa[(R + 1) & 1][0], fa[(R + 1) & 1][1]) : void()),
+                  quarter_affine_range<BITS, R * PS, (R + 1) * PS>(wn, M, dn), mfma_ab(R, fa[R & 1][0], fa[R & 1][1]),
+                  __builtin_amdgcn_sched_barrier(0)),
+                 ...);
+            }(std::make_integer_sequence<int, RB>{});
+        } else {
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) mfma_rb(rb);
+            decode((ut + 1) % PT, dn);
         }
-        decode((u + 1) % PF, d);
-        store_a((u + 1) % PF, (c + 1) & 1, c + 1 < nk);
+        if constexpr (DMA) __builtin_amdgcn_s_waitcnt(qt_vmcnt(A_WAIT));
+        else store_a((ua + 1) % PF, (c + 1) & 1, c + 1 < nk);
         hx_lds_barrier();
     };
-    const int nmain = nk - nk % PF;
-    for (int c0 = 0; c0 < nmain; c0 += PF) {
-#pragma unroll
-        for (int u = 0; u < PF; ++u) step(c0 + u, u);
+    // unrolled period: every ring position and the parity are compile-time constants
+    constexpr int PER = qt_lcm(qt_lcm(PF, PT), 2);
+    const int nmain = nk - nk % PER;
+    for (int c0 = 0; c0 < nmain; c0 += PER) {
+        [&]<int... U>(std::integer_sequence<int, U...>) {
+            (step(c0 + U, std::integral_constant<int, U % PF>{}, std::integral_constant<int, U % PT>{},
+                  std::integral_constant<int, U & 1>{}), ...);
+        }(std::make_integer_sequence<int, PER>{});
     }
-#pragma unroll
-    for (int u = 0; u < PF - 1; ++u)
-        if (nmain + u < nk) step(nmain + u, u);
+    [&]<int... U>(std::integer_sequence<int, U...>) {
+        ((nmain + U < nk ? step(nmain + U, std::integral_constant<int, U % PF>{},
+                                std::integral_constant<int, U % PT>{}, std::integral_constant<int, U & 1>{})
+                         : void()), ...);
+    }(std::make_integer_sequence<int, PER - 1>{});
+    if constexpr (DMA) {
+        // the clamped loads past the last chunk still write LDS: drain them before it is reused
+        __builtin_amdgcn_s_waitcnt(qt_vmcnt(0));
+        hx_lds_barrier();
+    }
     if constexpr (CB == 2 && EXT_RS) {
         if (t < BM) sm.rowsum[t] = rs_ext;
         __syncthreads();

@@ -241,7 +241,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job
 }
 
 template <int CB>
-__global__ __launch_bounds__(MF_THREADS, 3) void grouped_gemm_kernel(GroupedGemmArgs g)
+__global__ __launch_bounds__(MF_THREADS, HX_QT_OCC) void grouped_gemm_kernel(GroupedGemmArgs g)
 {
     __shared__ MfmaSmemQ sm;
     const int job_i = blockIdx.y;
@@ -294,7 +294,7 @@ template <int BM>
 using GuAcc = hx_f4[BM / 16][2];
 struct GuSmem {
     union {
-        _Float16 ab[2][MF_BM * MF_LDA];
+        _Float16 ab[QT_NB][MF_BM * MF_LDA];
         _Float16 hx[128 * MF_LDA2];
     };
     float rowsum[MF_BM];
@@ -439,7 +439,7 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
 }
 
 template <int CB>
-__global__ __launch_bounds__(MF_THREADS, 3) void grouped_gu_kernel(GuArgs a)
+__global__ __launch_bounds__(MF_THREADS, HX_QT_OCC) void grouped_gu_kernel(GuArgs a)
 {
     __shared__ GuSmem sm;
     const int job_i = blockIdx.y;
