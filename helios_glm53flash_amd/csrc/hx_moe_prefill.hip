@@ -240,16 +240,41 @@ __device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job
     }
 }
 
+// (column block, job) of this workgroup, in an XCD-aware order.  Workgroups are dispatched to the 8
+// XCDs round-robin by linear id; the real work (the first njobs x gridDim.x ids) is renumbered so
+// that all column blocks of a job run on one XCD, at the same time, and read the job's A rows
+// through one L2 (A is re-read by every column block), while the jobs themselves still go round the
+// XCDs in order, so each XCD gets the same mix of large and small row tiles.
+#ifndef HX_XCD_REMAP
+#define HX_XCD_REMAP 1
+#endif
+HX_INLINE bool grouped_tile_index(int njobs, int& bx, int& job)
+{
+    const int nx = gridDim.x;
+    const int i = blockIdx.x + blockIdx.y * nx;
+    const int total = njobs * nx;
+    if (i >= total) return false;
+    int l = i;
+    constexpr int NXCD = 8;
+    if (HX_XCD_REMAP && i < njobs / NXCD * NXCD * nx) {  // whole rounds of 8 jobs; the rest as issued
+        const int x = i % NXCD, k = i / NXCD;  // k-th workgroup on XCD x: job x + 8 (k / nx)
+        l = ((k / nx) * NXCD + x) * nx + k % nx;
+    }
+    bx = l % nx;
+    job = l / nx;
+    return true;
+}
+
 template <int CB>
 __global__ __launch_bounds__(MF_THREADS, HX_QT_OCC) void grouped_gemm_kernel(GroupedGemmArgs g)
 {
     __shared__ MfmaSmemQ sm;
-    const int job_i = blockIdx.y;
-    if (job_i >= *g.njobs) return;
+    int bx, job_i;
+    if (!grouped_tile_index(*g.njobs, bx, job_i)) return;
     const Job job = g.jobs[job_i];
     const int ntiles = g.N / 128;
-    const int proj = blockIdx.x / ntiles;
-    const int cg = blockIdx.x % ntiles;
+    const int proj = bx / ntiles;
+    const int cg = bx % ntiles;
     const int bits = g.bits_tab[proj] ? g.bits_tab[proj][job.expert] : g.bits_uniform[proj];
 #define HX_GG_CASE(B)                                                                      \
     case B:                                                                                \
@@ -442,12 +467,12 @@ template <int CB>
 __global__ __launch_bounds__(MF_THREADS, HX_QT_OCC) void grouped_gu_kernel(GuArgs a)
 {
     __shared__ GuSmem sm;
-    const int job_i = blockIdx.y;
-    if (job_i >= *a.njobs) return;
+    int cg, job_i;
+    if (!grouped_tile_index(*a.njobs, cg, job_i)) return;
     const Job job = a.jobs[job_i];
-    if (job.bm == 32) gu_fused<CB, 32>(a, job, blockIdx.x, sm);
-    else if (job.bm == 64) gu_fused<CB, 64>(a, job, blockIdx.x, sm);
-    else gu_fused<CB, MF_BM>(a, job, blockIdx.x, sm);
+    if (job.bm == 32) gu_fused<CB, 32>(a, job, cg, sm);
+    else if (job.bm == 64) gu_fused<CB, 64>(a, job, cg, sm);
+    else gu_fused<CB, MF_BM>(a, job, cg, sm);
 }
 
 // ------------------------------------------------------------------ combine
