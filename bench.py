@@ -171,7 +171,7 @@ def graph_time_us(torch, fn, reps: int = 20, inner: int = 20) -> float:
     return a.elapsed_time(b) / (reps * inner) * 1e3
 
 
-def bench_linears(torch, moe, exl3):
+def bench_linears(torch, moe, exl3, only: str = ""):
     """BASELINE configs 1, 2 and 5a: single EXL3 linears (weight GB/s at M <= 16, TFLOP/s on MFMA)."""
     g = torch.Generator(device="cuda")
     g.manual_seed(11)
@@ -181,8 +181,13 @@ def bench_linears(torch, moe, exl3):
              ("config2_K4096_N12288_4bit_M4", 4096, 12288, 4, 4),
              ("config2_K4096_N12288_4bit_M8", 4096, 12288, 4, 8),
              ("config5a_lmhead_K4096_N151552_5bit_M1", 4096, 151552, 5, 1),
-             ("config5a_lmhead_K4096_N151552_5bit_M512", 4096, 151552, 5, 512)]
+             ("config5a_lmhead_K4096_N151552_5bit_M512", 4096, 151552, 5, 512),
+             # not a BASELINE config: a long dense 2-bit stream through the same decode core, the
+             # steady-state decode rate that bounds the MoE decode layer's streaming phases
+             ("stream_K16384_N32768_2bit_M1", 16384, 32768, 2, 1)]
     for name, K, N, bits, M in cases:
+        if only not in name:
+            continue
         copies = 4 if K * N * bits // 8 < 256 << 20 else 1   # rotate copies so the 256 MB MALL does not hold them
         ws_ = [exl3.GroupWords(*moe.synthetic_linear(K, N, bits, g), exl3.MUL1) for _ in range(copies)]
         x = torch.randn((M, K), generator=g, device="cuda").half()
@@ -196,7 +201,8 @@ def bench_linears(torch, moe, exl3):
         wbytes = K * N * bits / 8 + 2 * K + 2 * N
         out[name] = {"us": round(us, 2), "weight_gbs": round(wbytes / us / 1e3, 1),
                      "pct_hbm": round(100 * wbytes / us / 1e3 / HBM_PEAK_GBS, 2),
-                     "tflops": round(2.0 * M * K * N / us / 1e6, 2)}
+                     "tflops": round(2.0 * M * K * N / us / 1e6, 2),
+                     "tera_weights_per_s": round(K * N / us / 1e6, 2)}
         del ws_
     return out
 
@@ -397,6 +403,8 @@ def main():
     ap.add_argument("--skip-extra", action="store_true", help="skip the linear and 42-layer sweep configs")
     ap.add_argument("--profile-only", action="store_true",
                     help="counter-collection driver: a 256 MiB device copy (calibration), then eager decode steps")
+    ap.add_argument("--linears-only", default=None, metavar="SUBSTR",
+                    help="run only the linear cases whose name contains SUBSTR and print their results")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (one GPU holds every expert); "
@@ -412,6 +420,9 @@ def main():
         profile_only(torch, moe)
         return
     from helios_glm53flash_amd import exl3
+    if args.linears_only is not None:
+        print(json.dumps(bench_linears(torch, moe, exl3, args.linears_only)))
+        return
     dec = bench_decode(args, torch, moe, lib)
     pre = None if args.skip_prefill else bench_prefill(args, torch, moe)
     lin = None if args.skip_extra else bench_linears(torch, moe, exl3)
