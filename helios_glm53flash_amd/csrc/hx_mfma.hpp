@@ -82,8 +82,11 @@ HX_INLINE void qt_rowcol(int rb, int nh, int i, int& row, int& col)
 #ifndef HX_QT_PT
 #define HX_QT_PT 2
 #endif
+// 1: the next chunk's decode sliced between the row blocks' MFMAs (one wave overlaps its own VALU and
+// matrix work); 0: decode after the chunk's MFMAs.  Measured equal on the config-4 prefill (3.14 ms
+// either way; the co-resident waves of a SIMD already overlap the two), so the simpler schedule.
 #ifndef HX_QT_IL
-#define HX_QT_IL 1
+#define HX_QT_IL 0
 #endif
 // workgroups per CU the MFMA-tile kernels are compiled for (their register budget)
 #ifndef HX_QT_OCC
