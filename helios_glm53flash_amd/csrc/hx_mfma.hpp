@@ -4,8 +4,9 @@
 // Workgroup = 4 waves, output tile BM x 128 (BM = 128, 64 or 32; 128 columns = one Hadamard block),
 // K consumed in chunks of 64.  Each wave owns 32 output columns for all BM rows and decodes those
 // columns' trellis words itself, straight into MFMA B operands (mfma_tile_q below); only A (the
-// input-transformed activations) is staged in LDS, double-buffered, one barrier per chunk.  Global
-// loads of A and of the trellis words run QT_PF chunks ahead in a register ring.
+// input-transformed activations) goes through LDS, one barrier per chunk: QT_PF chunks ahead, by
+// buffer loads that write LDS directly (a ring of QT_NB buffers), or through registers where the
+// tile sums A's rows itself.  The trellis words run QT_PT chunks ahead in a register ring.
 // Codebook 2 is decoded in affine form (h = 1024 + bytesum, see hx_gemv.hpp): the tile computes
 // sum_k a h, and the epilogue adds the map with per-row input sums (accumulated from the staged A, or
 // precomputed by the caller).
