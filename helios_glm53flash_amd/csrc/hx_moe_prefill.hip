@@ -549,8 +549,8 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const _Float16* D,
 // order), multiplied by H128 (generated in registers) with fp32 accumulation; the results are staged
 // in LDS and each lane then adds its columns over the routes in rank order (the order of
 // prefill_combine_kernel and the reference's ordered reduction).
-template <int TOPK>
-__global__ __launch_bounds__(256, 4) void prefill_combine_mfma_kernel(const _Float16* D, const int64_t* r2s,
+template <int TOPK, int KBC>
+__global__ __launch_bounds__(256, 3) void prefill_combine_mfma_kernel(const _Float16* D, const int64_t* r2s,
                                                                       const int* row_expert, const _Float16* w_sorted,
                                                                       const void* const* svh_d, int T, int hidden,
                                                                       float* contrib, const float* shared_rows,
@@ -559,29 +559,42 @@ __global__ __launch_bounds__(256, 4) void prefill_combine_mfma_kernel(const _Flo
     constexpr int TPW = 16 / TOPK;       // tokens per wave
     constexpr int LPT = 64 / TPW;        // lanes per token in the reduction
     constexpr int CPL = 128 / LPT;       // columns per lane in the reduction
+    constexpr int SVW = CPL / 2;         // svh words per route and lane
     __shared__ float st[4][16][132];
     __shared__ long srow[4][16];
     __shared__ float sw_[4][16];
     __shared__ const _Float16* ssv[4][16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nblk = hidden >> 7;
+    const int nblk = hidden >> 7, nchunk = (nblk + KBC - 1) / KBC;
     const long unit = (long)blockIdx.x * 4 + wave;
-    const long tg = unit / nblk;
-    const int kb = (int)(unit % nblk);
+    const long tg = unit / nchunk;
+    const int kb0 = (int)(unit % nchunk) * KBC;
     const long t0 = tg * TPW;
     if (t0 >= T) return;
     const int c = lane & 15, g = lane >> 4;
     const long t = min(t0 + c / TOPK, (long)T - 1);
     const long r = r2s[(size_t)t * TOPK + c % TOPK];
+    // the routes' rows, weights and svh rows: looked up once for the wave's KBC column blocks
     if (g == 0) {
         srow[wave][c] = r;
         sw_[wave][c] = (float)w_sorted[r];
         ssv[wave][c] = static_cast<const _Float16*>(svh_d[row_expert[r]]);
     }
-    const _Float16* dr = D + (size_t)r * hidden + kb * 128 + 8 * g;
-    hx_h8 av[4];
+    const _Float16* dr = D + (size_t)r * hidden + 8 * g;
+    auto load_d = [&](int kb, hx_h8 (&av)[4]) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) av[kk] = *reinterpret_cast<const hx_h8*>(dr + 32 * kk);
+        for (int kk = 0; kk < 4; ++kk) av[kk] = *reinterpret_cast<const hx_h8*>(dr + kb * 128 + 32 * kk);
+    };
+    const int tl = lane / LPT, col = (lane % LPT) * CPL;
+    const long tok = t0 + tl;
+    auto load_sv = [&](int kb, uint32_t (&sv)[TOPK][SVW]) {
+#pragma unroll
+        for (int j = 0; j < TOPK; ++j) {
+            const uint32_t* p = reinterpret_cast<const uint32_t*>(ssv[wave][tl * TOPK + j] + kb * 128 + col);
+#pragma unroll
+            for (int w = 0; w < SVW; ++w) sv[j][w] = p[w];
+        }
+    };
     uint32_t f[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -589,73 +602,82 @@ __global__ __launch_bounds__(256, 4) void prefill_combine_mfma_kernel(const _Flo
         f[i] = (0x3c00u | (s0 << 15)) | ((0x3c00u | (s1 << 15)) << 16);
     }
     const uint32_t base = (uint32_t)((c >> 3) & g & 1);
-    hx_f4 yv[8];
+    auto wave_sync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // D and svh of the next column block are requested before this one is transformed and reduced
+    hx_h8 av[2][4];
+    uint32_t sv[2][TOPK][SVW];
+    load_d(kb0, av[0]);
+    wave_sync();  // the route tables in LDS
+    load_sv(kb0, sv[0]);
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) yv[nb] = hx_f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) {
-            const uint32_t sgn = base ^ ((uint32_t)(nb & 1) & (uint32_t)(g >> 1)) ^ (uint32_t)((nb >> 1) & kk & 1) ^
-                                 (uint32_t)((nb >> 2) & (kk >> 1) & 1);
-            const uint32_t m = sgn ? 0x80008000u : 0u;
-            typedef uint32_t u4v __attribute__((ext_vector_type(4)));
-            const u4v bv = {f[0] ^ m, f[1] ^ m, f[2] ^ m, f[3] ^ m};
-            yv[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[kk], __builtin_bit_cast(hx_h8, bv), yv[nb], 0, 0, 0);
+    for (int i = 0; i < KBC; ++i) {
+        const int kb = kb0 + i;
+        if (kb >= nblk) break;
+        if (i + 1 < KBC && kb + 1 < nblk) {
+            load_d(kb + 1, av[(i + 1) & 1]);
+            load_sv(kb + 1, sv[(i + 1) & 1]);
         }
+        hx_f4 yv[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int nb = 0; nb < 8; ++nb) yv[nb] = hx_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) st[wave][4 * g + i][16 * nb + c] = yv[nb][i] * HX_RSQRT128;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int tl = lane / LPT, col = (lane % LPT) * CPL;
-    const long tok = t0 + tl;
-    if (tok >= T) return;
-    float acc[CPL];
+        for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-    for (int k = 0; k < CPL; ++k) acc[k] = 0.0f;
+            for (int nb = 0; nb < 8; ++nb) {
+                const uint32_t sgn = base ^ ((uint32_t)(nb & 1) & (uint32_t)(g >> 1)) ^
+                                     (uint32_t)((nb >> 1) & kk & 1) ^ (uint32_t)((nb >> 2) & (kk >> 1) & 1);
+                const uint32_t m = sgn ? 0x80008000u : 0u;
+                typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+                const u4v bv = {f[0] ^ m, f[1] ^ m, f[2] ^ m, f[3] ^ m};
+                yv[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i & 1][kk], __builtin_bit_cast(hx_h8, bv), yv[nb],
+                                                                0, 0, 0);
+            }
+        if (i > 0) wave_sync();  // the previous block's reads of st are done
 #pragma unroll
-    for (int j = 0; j < TOPK; ++j) {
-        const int row = tl * TOPK + j;
-        const float w = sw_[wave][row];
-        const _Float16* sv = ssv[wave][row] + kb * 128 + col;
-        float d[CPL];
-        if constexpr (CPL == 4) {
-            const hx_h4 s4 = *reinterpret_cast<const hx_h4*>(sv);
-            const float4 v4 = *reinterpret_cast<const float4*>(&st[wave][row][col]);
-            d[0] = v4.x * w * (float)s4[0];
-            d[1] = v4.y * w * (float)s4[1];
-            d[2] = v4.z * w * (float)s4[2];
-            d[3] = v4.w * w * (float)s4[3];
-        } else {
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
-            for (int k = 0; k < CPL; ++k) d[k] = st[wave][row][col + k] * w * (float)sv[k];
-        }
-        if (contrib) {
-            float* cp = contrib + (size_t)srow[wave][row] * hidden + kb * 128 + col;
+            for (int nb = 0; nb < 8; ++nb) st[wave][4 * g + q][16 * nb + c] = yv[nb][q] * HX_RSQRT128;
+        wave_sync();
+        if (tok < T) {
+            float acc[CPL];
 #pragma unroll
-            for (int k = 0; k < CPL; ++k) cp[k] = d[k];
-        }
+            for (int k = 0; k < CPL; ++k) acc[k] = 0.0f;
 #pragma unroll
-        for (int k = 0; k < CPL; ++k) acc[k] += d[k];
-    }
-    const size_t o = (size_t)tok * hidden + kb * 128 + col;
-    if (y_routed) {
-        float* yr = y_routed + o;
+            for (int j = 0; j < TOPK; ++j) {
+                const int row = tl * TOPK + j;
+                const float w = sw_[wave][row];
+                float d[CPL];
 #pragma unroll
-        for (int k = 0; k < CPL; ++k) yr[k] = accumulate ? yr[k] + acc[k] : acc[k];
-    }
-    if (y) {
-        if constexpr (CPL == 4) {
-            hx_h4 out;
+                for (int k = 0; k < CPL; ++k) {
+                    const hx_h2 s2 = u32_as_h2(sv[i & 1][j][k >> 1]);
+                    d[k] = st[wave][row][col + k] * w * (float)s2[k & 1];
+                }
+                if (contrib) {
+                    float* cp = contrib + (size_t)srow[wave][row] * hidden + kb * 128 + col;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) out[k] = (_Float16)(shared_rows ? acc[k] + shared_rows[o + k] : acc[k]);
-            *reinterpret_cast<hx_h4*>(y + o) = out;
-        } else {
+                    for (int k = 0; k < CPL; ++k) cp[k] = d[k];
+                }
 #pragma unroll
-            for (int k = 0; k < CPL; ++k) y[o + k] = (_Float16)(shared_rows ? acc[k] + shared_rows[o + k] : acc[k]);
+                for (int k = 0; k < CPL; ++k) acc[k] += d[k];
+            }
+            const size_t o = (size_t)tok * hidden + kb * 128 + col;
+            if (y_routed) {
+                float* yr = y_routed + o;
+#pragma unroll
+                for (int k = 0; k < CPL; ++k) yr[k] = accumulate ? yr[k] + acc[k] : acc[k];
+            }
+            if (y) {
+                _Float16 out[CPL];
+#pragma unroll
+                for (int k = 0; k < CPL; ++k) out[k] = (_Float16)(shared_rows ? acc[k] + shared_rows[o + k] : acc[k]);
+#pragma unroll
+                for (int w = 0; w < SVW; ++w)
+                    reinterpret_cast<uint32_t*>(y + o)[w] = h2_as_u32(hx_h2{out[2 * w], out[2 * w + 1]});
+            }
         }
     }
 }
@@ -764,11 +786,15 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     if (!p.r2s) return hipErrorInvalidValue;
     if (p.topk > 64) return hipErrorInvalidValue;
     if (p.T > 0 && (p.topk == 1 || p.topk == 2 || p.topk == 4 || p.topk == 8 || p.topk == 16)) {
-        const long units = ((long)p.T * p.topk + 15) / 16 * (p.hidden / 128);
+#ifndef HX_CMB_KBC
+#define HX_CMB_KBC 4
+#endif
+        constexpr int KBC = HX_CMB_KBC;  // 128-column blocks per wave (the route lookups are paid once for them)
+        const long units = ((long)p.T * p.topk + 15) / 16 * ((p.hidden / 128 + KBC - 1) / KBC);
         const dim3 grid((unsigned)((units + 3) / 4));
 #define HX_CMB(K)                                                                                             \
     case K:                                                                                                   \
-        hipLaunchKernelGGL(prefill_combine_mfma_kernel<K>, grid, dim3(256), 0, st, D, p.r2s, row_expert,      \
+        hipLaunchKernelGGL((prefill_combine_mfma_kernel<K, KBC>), grid, dim3(256), 0, st, D, p.r2s, row_expert, \
                            p.weight_sorted, p.svh[2], p.T, p.hidden, contrib, shared_rows, y, y_routed, accumulate); \
         break;
         switch (p.topk) { HX_CMB(1) HX_CMB(2) HX_CMB(4) HX_CMB(8) HX_CMB(16) }
