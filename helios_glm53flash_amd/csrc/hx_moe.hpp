@@ -18,7 +18,7 @@ struct MoeWs {
     size_t off_pg = 0, off_pu = 0, off_pd = 0, off_act = 0, off_contrib = 0;
     // prefill path
     int max_jobs = 0;
-    size_t off_perm = 0, off_jobs = 0, off_njobs = 0, off_row_expert = 0, off_xg = 0, off_xu = 0, off_G = 0, off_U = 0,
+    size_t off_perm = 0, off_jobs = 0, off_njobs = 0, off_row_expert = 0, off_xg = 0, off_xu = 0, off_G = 0,
            off_A = 0, off_rs = 0, off_D = 0, off_sh_a = 0, off_sh_g = 0, off_sh_u = 0, off_sh_act = 0, off_sh_d = 0;
     size_t prefill_end = 0;
     size_t total = 0;

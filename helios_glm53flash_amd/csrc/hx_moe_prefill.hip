@@ -35,7 +35,6 @@ void MoeWs::prefill_layout(size_t o)
     off_xg = o;         o = al(o + sizeof(_Float16) * (size_t)R * hidden);
     off_xu = o;         o = al(o + sizeof(_Float16) * (size_t)R * hidden);
     off_G = o;          o = al(o + sizeof(_Float16) * (size_t)R * inter);
-    off_U = o;          o = al(o + sizeof(_Float16) * (size_t)R * inter);
     off_A = o;          o = al(o + sizeof(_Float16) * (size_t)R * inter);
     off_rs = o;         o = al(o + sizeof(float) * (size_t)R * (2 * (hidden / 128) + inter / 128));
     off_D = off_xg;     // D reuses xg (xg is consumed by the gate GEMM before the down GEMM runs)
@@ -306,8 +305,7 @@ struct GuArgs {
     float act_limit;
     int act_fn;          // HX_ACT_SILU, HX_ACT_GELU or HX_ACT_RELU2_NOGATE (no gate GEMM)
     _Float16* act;       // [R][inter] down-projection inputs
-    _Float16* g_scratch; // [R][inter] fp16 G, then u, of the tiles in flight
-    _Float16* u_scratch;
+    _Float16* g_scratch; // [R][inter] fp16 g of the tiles in flight (lane-grouped columns)
     const float* rs_g;   // [R][K / 128] row sums of xg, xu per 128-column block
     const float* rs_u;
     float* rs_act;       // [R][inter / 128] row sums of act per 128-column block
@@ -369,68 +367,68 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
 
     GuAcc<BM> acc;
     hx_f4 hacc[MB][4];  // Hadamard results (the matrix-core transform's layout)
-    // The fp16 tiles G and then u wait in global scratch (this workgroup's rows and columns only; they
-    // stay in L2) instead of registers, which would halve the waves per SIMD of the main loops.
+    const _Float16* svg = (a.act_fn != HX_ACT_RELU2_NOGATE) ? static_cast<const _Float16*>(a.svh[0][e]) + cg * 128 : nullptr;
+    const _Float16* svu = static_cast<const _Float16*>(a.svh[1][e]) + cg * 128;
+    const _Float16* sud = static_cast<const _Float16*>(a.suh_d[e]) + cg * 128;
+    // g = fp16(H(G)) * svh_g is formed right after the gate tile and waits in global scratch (this
+    // workgroup's rows and columns only; it stays in L2) while the up tile runs, which needs the
+    // registers.  Scratch layout within a row's 128 columns: a lane's 4 values of the row
+    // (columns 64 wn + 16 nb + c, nb = 0..3) sit together at 64 wn + 4 c, one 8-byte access each.
     _Float16* gs = a.g_scratch + (size_t)job.row0 * a.N + cg * 128;
-    _Float16* us = a.u_scratch + (size_t)job.row0 * a.N + cg * 128;
-    auto frag_store = [&](_Float16* dst, auto f) {  // fragment (row, col) -> dst[row][col], rows < job.rows
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int row = WM * wm + 16 * mb + 4 * (lane >> 4) + r, col = 64 * wn + 16 * nb + (lane & 15);
-                    if (row < job.rows) dst[(size_t)row * a.N + col] = f(row, col, hacc[mb][nb][r]);
-                }
-    };
-    const bool gated = a.act_fn != HX_ACT_RELU2_NOGATE;
-    // gate: G = fp16(mapped sum)
+    auto gs_at = [&](int row) { return gs + (size_t)row * a.N + 64 * wn + 4 * (lane & 15); };
+    const bool gated = (a.act_fn != HX_ACT_RELU2_NOGATE);
     if (gated) {
         gu_tile_bits<CB, BM>(bg, a.xg + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[0][e], a.N, cg, sm, acc,
                              a.rs_g + (size_t)job.row0 * (a.K / 128));
-        qt_foreach<BM>(acc, [&](int row, int col, float v) {
-            if (row < job.rows) gs[(size_t)row * a.N + col] = (_Float16)mapped(row, v);
-        });
-        __syncthreads();  // rowsum is reused by the up tile
+        // G = fp16(mapped sum), staged for the transform (the A buffers are free between tiles)
+        qt_foreach<BM>(acc, [&](int row, int col, float v) { X[row * MF_LDA2 + col] = (_Float16)mapped(row, v); });
+        __syncthreads();
+        hadamard_mfma_reg<BM>(X, hacc);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = WM * wm + 16 * mb + 4 * (lane >> 4) + r;
+                hx_h4 v;
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb) v[nb] = (_Float16)hacc[mb][nb][r] * svg[64 * wn + 16 * nb + (lane & 15)];
+                if (row < job.rows) *reinterpret_cast<hx_h4*>(gs_at(row)) = v;
+            }
+        // the stores are complete before this workgroup reads them back, and X is free for the
+        // up tile's A buffers
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
     }
     gu_tile_bits<CB, BM>(bu, a.xu + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[1][e], a.N, cg, sm, acc,
                          a.rs_u + (size_t)job.row0 * (a.K / 128));
-
-    // u = fp16(H(U)) * svh_u
+    // g back from scratch, requested before the up tile's transform
+    hx_h4 gv[MB][4];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = WM * wm + 16 * mb + 4 * (lane >> 4) + r;
+            gv[mb][r] = hx_h4{(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+            if (gated && row < job.rows) gv[mb][r] = *reinterpret_cast<const hx_h4*>(gs_at(row));
+        }
+    // u = fp16(H(U)) * svh_u, kept in registers
     qt_foreach<BM>(acc, [&](int row, int col, float v) { X[row * MF_LDA2 + col] = (_Float16)mapped(row, v); });
     __syncthreads();
     hadamard_mfma_reg<BM>(X, hacc);
-    const _Float16* svg = gated ? static_cast<const _Float16*>(a.svh[0][e]) + cg * 128 : nullptr;
-    const _Float16* svu = static_cast<const _Float16*>(a.svh[1][e]) + cg * 128;
-    const _Float16* sud = static_cast<const _Float16*>(a.suh_d[e]) + cg * 128;
-    frag_store(us, [&](int, int col, float v) { return (_Float16)((_Float16)v * svu[col]); });
-    __syncthreads();  // G and u stores done (workgroup scope), X free
-    // g = fp16(H(G)) * svh_g
-    if (gated) {
-        for (int i = threadIdx.x; i < BM * 16; i += MF_THREADS) {
-            const int row = i >> 4, c8 = (i & 15) * 8;
-            hx_u4v v = {0u, 0u, 0u, 0u};
-            if (row < job.rows) v = *reinterpret_cast<const hx_u4v*>(gs + (size_t)row * a.N + c8);
-            *reinterpret_cast<hx_u4v*>(&X[row * MF_LDA2 + c8]) = v;
-        }
-        __syncthreads();
-        hadamard_mfma_reg<BM>(X, hacc);
-    }
     const float L = a.act_limit;
     const _Float16 Lh = (_Float16)L, nLh = (_Float16)(-L);
     __syncthreads();
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
         const int col = 64 * wn + 16 * nb + (lane & 15);
-        const _Float16 sg = gated ? svg[col] : (_Float16)0.0f, sd = sud[col];
+        const _Float16 su = svu[col], sd = sud[col];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = WM * wm + 16 * mb + 4 * (lane >> 4) + r;
-                _Float16 g = gated ? (_Float16)hacc[mb][nb][r] * sg : (_Float16)0.0f;
-                _Float16 uu = row < job.rows ? us[(size_t)row * a.N + col] : (_Float16)0.0f;
+                _Float16 g = gv[mb][r][nb];
+                _Float16 uu = row < job.rows ? (_Float16)((_Float16)hacc[mb][nb][r] * su) : (_Float16)0.0f;
                 g = hx_gate_act(a.act_fn, g, uu);
                 if (L != 0.0f) {
                     uu = uu < nLh ? nLh : (uu > Lh ? Lh : uu);
@@ -715,7 +713,6 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     _Float16* xg = reinterpret_cast<_Float16*>(ws + L.off_xg);
     _Float16* xu = reinterpret_cast<_Float16*>(ws + L.off_xu);
     _Float16* G = reinterpret_cast<_Float16*>(ws + L.off_G);
-    _Float16* U = reinterpret_cast<_Float16*>(ws + L.off_U);
     _Float16* A = reinterpret_cast<_Float16*>(ws + L.off_A);
     _Float16* D = reinterpret_cast<_Float16*>(ws + L.off_D);
     float* rs_g = reinterpret_cast<float*>(ws + L.off_rs);
@@ -750,7 +747,6 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     gu.act_fn = p.act_fn;
     gu.act = A;
     gu.g_scratch = G;
-    gu.u_scratch = U;
     gu.rs_g = rs_g;
     gu.rs_u = rs_u;
     gu.rs_act = rs_act;
