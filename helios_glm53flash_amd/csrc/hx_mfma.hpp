@@ -205,17 +205,6 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
     };
 
     const int nk = K / MF_BK;
-    float rs_ext = 0.0f;  // row t's precomputed sum (requested before the tile streams)
-    if constexpr (CB == 2 && EXT_RS) {
-        if (t < BM && t < rows)
-            for (int b0 = 0; b0 < rs_n; b0 += 16) {  // 16 independent loads per round trip
-                float v[16];
-#pragma unroll
-                for (int j = 0; j < 16; ++j) v[j] = b0 + j < rs_n ? rs_src[(size_t)t * rs_n + b0 + j] : 0.0f;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) rs_ext += v[j];
-            }
-    }
 #pragma unroll
     for (int s = 0; s < (PF > PT ? PF : PT); ++s) {
         if (s < PF) {
@@ -223,6 +212,19 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
             else load_a(s, min(s, nk - 1) * MF_BK);
         }
         if (s < PT) load_t(s, min(s, nk - 1) * MF_BK);
+    }
+    // row t's precomputed sum, requested while the first chunks are in flight (32 independent
+    // loads per round trip: one round trip for K up to 4096)
+    float rs_ext = 0.0f;
+    if constexpr (CB == 2 && EXT_RS) {
+        if (t < BM && t < rows)
+            for (int b0 = 0; b0 < rs_n; b0 += 32) {
+                float v[32];
+#pragma unroll
+                for (int j = 0; j < 32; ++j) v[j] = b0 + j < rs_n ? rs_src[(size_t)t * rs_n + b0 + j] : 0.0f;
+#pragma unroll
+                for (int j = 0; j < 32; ++j) rs_ext += v[j];
+            }
     }
     // VMEM instructions per chunk: A (DMA) and trellis words; chunk c + 1's A is complete once at
     // most the loads of the PF - 1 later chunks are outstanding (their order within a step is left

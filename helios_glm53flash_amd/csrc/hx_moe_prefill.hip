@@ -394,9 +394,8 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
                 for (int nb = 0; nb < 4; ++nb) v[nb] = (_Float16)hacc[mb][nb][r] * svg[64 * wn + 16 * nb + (lane & 15)];
                 if (row < job.rows) *reinterpret_cast<hx_h4*>(gs_at(row)) = v;
             }
-        // the stores are complete before this workgroup reads them back, and X is free for the
-        // up tile's A buffers
-        __builtin_amdgcn_s_waitcnt(0);
+        // X is free for the up tile's A buffers (the lanes read back only what they stored
+        // themselves, in program order)
         __syncthreads();
     }
     gu_tile_bits<CB, BM>(bu, a.xu + (size_t)job.row0 * a.K, a.K, job.rows, a.tr[1][e], a.N, cg, sm, acc,
