@@ -61,8 +61,11 @@ __global__ __launch_bounds__(MF_THREADS, HX_QT_OCC) void linear_mfma_kernel(cons
                                                                 bool y_fp32)
 {
     __shared__ MfmaSmemQ sm;
-    const int cg = blockIdx.x;
-    const int m0 = blockIdx.y * MF_BM;
+    // the row tiles of a column group on one XCD: its trellis words come from memory once and the
+    // other row tiles read them from that XCD's L2
+    int mt, cg;
+    xcd_group_index(blockIdx.x + blockIdx.y * gridDim.x, gridDim.y, gridDim.x, mt, cg);
+    const int m0 = mt * MF_BM;
     const int rows = min(MF_BM, M - m0);
     hx_f4 acc[MF_BM / 16][2];
     mfma_tile_q<BITS, CB, MF_BM>(a + (size_t)m0 * K, K, rows, trellis, K, N, cg * 8, sm, acc);

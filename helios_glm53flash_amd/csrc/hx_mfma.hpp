@@ -119,6 +119,30 @@ struct MfmaSmemQ {
     float rowsum[MF_BM];
 };
 
+// XCD-aware renumbering of a grid of ngroups groups of nx workgroups (linear id i, groups of
+// consecutive ids).  Workgroups are dispatched to the 8 XCDs round-robin by linear id; the
+// renumbering gives all nx members of a group to one XCD, where they run at the same time and share
+// that XCD's L2 for what they all read, while the groups still go round the XCDs in order (whole
+// rounds of 8 groups; the rest as issued), so every XCD gets the same mix of groups.  Returns false
+// for ids past the ngroups * nx real workgroups.
+#ifndef HX_XCD_REMAP
+#define HX_XCD_REMAP 1
+#endif
+HX_INLINE bool xcd_group_index(int i, int nx, int ngroups, int& member, int& group)
+{
+    const int total = ngroups * nx;
+    if (i >= total) return false;
+    int l = i;
+    constexpr int NXCD = 8;
+    if (HX_XCD_REMAP && i < ngroups / NXCD * NXCD * nx) {
+        const int x = i % NXCD, k = i / NXCD;  // k-th workgroup on XCD x: group x + 8 (k / nx)
+        l = ((k / nx) * NXCD + x) * nx + k % nx;
+    }
+    member = l % nx;
+    group = l / nx;
+    return true;
+}
+
 // With rs_src (codebook 2), the row sums of A come precomputed as rs_n fp32 partial sums per row
 // (rs_src[r * rs_n + b]) instead of being accumulated from the staged A.
 template <int BITS, int CB, int BM, int PF = QT_PF, bool EXT_RS = false, class Smem>

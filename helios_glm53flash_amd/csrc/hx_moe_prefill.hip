@@ -239,29 +239,11 @@ __device__ __forceinline__ void grouped_tile(const GroupedGemmArgs& g, const Job
     }
 }
 
-// (column block, job) of this workgroup, in an XCD-aware order.  Workgroups are dispatched to the 8
-// XCDs round-robin by linear id; the real work (the first njobs x gridDim.x ids) is renumbered so
-// that all column blocks of a job run on one XCD, at the same time, and read the job's A rows
-// through one L2 (A is re-read by every column block), while the jobs themselves still go round the
-// XCDs in order, so each XCD gets the same mix of large and small row tiles.
-#ifndef HX_XCD_REMAP
-#define HX_XCD_REMAP 1
-#endif
+// (column block, job) of this workgroup, in the XCD-aware order of xcd_group_index: all column
+// blocks of a job on one XCD (they all read the job's A rows), the jobs round the XCDs in order.
 HX_INLINE bool grouped_tile_index(int njobs, int& bx, int& job)
 {
-    const int nx = gridDim.x;
-    const int i = blockIdx.x + blockIdx.y * nx;
-    const int total = njobs * nx;
-    if (i >= total) return false;
-    int l = i;
-    constexpr int NXCD = 8;
-    if (HX_XCD_REMAP && i < njobs / NXCD * NXCD * nx) {  // whole rounds of 8 jobs; the rest as issued
-        const int x = i % NXCD, k = i / NXCD;  // k-th workgroup on XCD x: job x + 8 (k / nx)
-        l = ((k / nx) * NXCD + x) * nx + k % nx;
-    }
-    bx = l % nx;
-    job = l / nx;
-    return true;
+    return xcd_group_index(blockIdx.x + blockIdx.y * gridDim.x, gridDim.x, njobs, bx, job);
 }
 
 template <int CB>
