@@ -261,7 +261,9 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
     else store_a(0, 0, true);
     // d[c & 1] holds the decoded quarter of chunk c; the next chunk's quarter is decoded into the
     // other half while the matrix cores work on this one, interleaved with the MFMAs in one block
-    uint32_t d[2][16];
+    // (with the decode after the chunk's MFMAs one buffer serves: the B operands are read first)
+    constexpr int ND = HX_QT_IL ? 2 : 1;
+    uint32_t d[ND][16];
     decode(0, d[0]);
     hx_lds_barrier();
     // step c: ua = c % PF, ut = c % PT, par = c & 1, all compile-time in the unrolled loops
@@ -271,8 +273,8 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
         else load_a(ua, min(c + PF, nk - 1) * MF_BK);
         load_t(ut, min(c + PT, nk - 1) * MF_BK);
         const _Float16* as = sm.ab[DMA ? c % QT_NB : c & 1];
-        const uint32_t* dc = d[par];
-        uint32_t* dn = d[par ^ 1];
+        const uint32_t* dc = d[par % ND];
+        uint32_t* dn = d[(par + 1) % ND];
         const hx_h8 b00 = quarter_operand<0, 0>(dc), b01 = quarter_operand<0, 1>(dc);
         const hx_h8 b10 = quarter_operand<1, 0>(dc), b11 = quarter_operand<1, 1>(dc);
         auto read_a = [&](int rb, hx_h8& a0, hx_h8& a1) {
