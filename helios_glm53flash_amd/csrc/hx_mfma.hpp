@@ -100,6 +100,8 @@ constexpr int QT_NB = QT_PF + 1;
 // s_waitcnt immediate that waits until at most n vector-memory instructions are outstanding
 // (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their no-wait maxima)
 constexpr int qt_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+// 1: A by buffer loads that write LDS directly wherever the tile does not sum A's rows itself (those
+// read A in registers); 0: always through registers and ds_write (measured 2 % slower, 32 more VGPRs)
 #ifndef HX_QT_DMA
 #define HX_QT_DMA 1
 #endif
