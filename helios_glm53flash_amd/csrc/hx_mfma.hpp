@@ -201,11 +201,14 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
         const int r = 32 * i + 8 * wave + (lane >> 3);
         a_voff_lds[i] = (int)(((size_t)r * lda + 8 * ((lane & 7) ^ mf_swz(r))) * sizeof(_Float16));
     }
+    // the LDS destination is wave-uniform (it goes to M0): derived from a scalar wave index, it is
+    // computed on the scalar unit instead of a v_readfirstlane per load
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
     auto load_a_lds = [&](int buf, int k0) {
 #pragma unroll
         for (int i = 0; i < NA; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ra, (__attribute__((address_space(3))) void*)(&sm.ab[buf][(32 * i + 8 * wave) * MF_LDA]), 16,
+                ra, (__attribute__((address_space(3))) void*)(&sm.ab[buf][(32 * i + 8 * wave_s) * MF_LDA]), 16,
                 a_voff_lds[i], k0 * 2, 0, 0);
     };
     auto store_a = [&](int slot, int buf, bool count) {
