@@ -175,8 +175,11 @@ size_t decode_lds_pad(const void* kernel, size_t lds, int max_per_cu)
 // U / C or U / C + 1 units (equal k ranges within it, one segment each).  Measured (config-3 layer,
 // 1024 resident, 4-step ring): 1024 + 1024 units (3 or 4 per column group, every CU holds 4
 // gate/up workgroups) 46.3 us; 864 + 864 (3 per column group, so 96 CUs hold 4 and the others 3)
-// 48.3 us; 960 + 1024 47.7 us; 1024 + 1280 48.4 us; 576 + 864 49.1 us.  (With the earlier
-// ring, whose waits drained every load in flight once per group, 864 + 864 was the faster one.)
+// 48.3 us; 960 + 1024 47.7 us; 1024 + 1280 48.4 us; 576 + 864 49.1 us; and for the down phase
+// alone (1024 gate/up): 1024 46.1-46.5 us, 992 45.9, 960 45.8, 928 46.1, 832 47.3 us, so the down
+// phase takes 15/16 of the resident count (its units, a little longer, gather fewer partials).
+// (With the earlier ring, whose waits drained every load in flight once per group, 864 + 864 was
+// the faster one.)
 // A fused variant (workgroup w runs gate/up unit w then down unit w, reusing its plan) took 60 us.
 // HX_MOE_UNITS="g,d" sets the two counts as fractions of the resident count (tuning).  Returns the
 // longest unit's k extent.
@@ -186,7 +189,7 @@ int decode_units(MoeDecodeArgs& a, int resident)
     const long cg_gu = slots * 2 * (a.inter / 128), kb_gu = a.hidden / 128;
     const long cg_d = slots * (a.hidden / 128), kb_d = a.inter / 128;
     auto clampu = [](long u, long c, long kb) { return u < c ? c : (u > c * kb ? c * kb : u); };
-    long ug = clampu(resident, cg_gu, kb_gu), ud = clampu(resident, cg_d, kb_d);
+    long ug = clampu(resident, cg_gu, kb_gu), ud = clampu(resident - resident / 16, cg_d, kb_d);
     if (const char* v = getenv("HX_MOE_UNITS")) {  // fractions of the resident count, for sweeps
         double fg = 1.0, fd = 1.0;
         sscanf(v, "%lf,%lf", &fg, &fd);
