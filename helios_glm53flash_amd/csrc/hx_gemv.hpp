@@ -356,6 +356,64 @@ HX_INLINE uint32_t input_transform(uint32_t xv, uint32_t sv, bool pre_transforme
     return h2_as_u32(r);
 }
 
+// The input transform of up to 16 rows at once on the matrix cores: per 128-k block, the rows'
+// fp16(x . suh) (rows >= M zero) times H128 as one 16 x 128 by 128 x 128 product, H generated in
+// registers (sign of (n, k) = popcount(n & k) & 1: a fixed per-lane fragment times one sign per
+// operand), fp32 accumulation of the exact +-products, one fp16 rounding after the 1/sqrt(128)
+// scale.  The same values as the butterfly (hx_had128_wave) up to the order of the fp32 additions;
+// for several rows it replaces a wave-wide butterfly per row and block with 32 MFMAs per block.
+// Lane l: A row l % 16, k = 32 kk + 8 (l / 16) + 0..7; C rows 4 (l / 16) + i, column 16 nb + l % 16.
+HX_INLINE void input_mfma(uint32_t* a_lds, const _Float16* x, const int* rows, const _Float16* suh, int M, int K,
+                          int k0, int kc)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = lane & 15, g = lane >> 4;
+    const int blocks = kc >> 7;
+    uint32_t f[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t s0 = __builtin_popcount(c & (2 * i) & 7) & 1, s1 = __builtin_popcount(c & (2 * i + 1) & 7) & 1;
+        f[i] = (0x3c00u | (s0 << 15)) | ((0x3c00u | (s1 << 15)) << 16);
+    }
+    const uint32_t base = (uint32_t)((c >> 3) & g & 1);
+    const bool live = c < M;
+    const _Float16* xr = x + (live ? (rows ? (size_t)rows[c] : (size_t)c) : 0) * K + 8 * g;
+    _Float16* al = reinterpret_cast<_Float16*>(a_lds);
+    for (int b = wave; b < blocks; b += hx_nwaves()) {
+        const int kb = k0 + b * 128;
+        hx_h8 av[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const hx_h8 sv = *reinterpret_cast<const hx_h8*>(suh + kb + 32 * kk + 8 * g);
+            hx_h8 xv = {};
+            if (live) xv = *reinterpret_cast<const hx_h8*>(xr + kb + 32 * kk);
+            av[kk] = xv * sv;
+        }
+        hx_f4 y[8];
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) y[nb] = hx_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) {
+                const uint32_t sgn = base ^ ((uint32_t)(nb & 1) & (uint32_t)(g >> 1)) ^ (uint32_t)((nb >> 1) & kk & 1) ^
+                                     (uint32_t)((nb >> 2) & (kk >> 1) & 1);
+                const uint32_t m = sgn ? 0x80008000u : 0u;
+                typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+                const u4v bv = {f[0] ^ m, f[1] ^ m, f[2] ^ m, f[3] ^ m};
+                y[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[kk], __builtin_bit_cast(hx_h8, bv), y[nb], 0, 0, 0);
+            }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * g + i;
+            if (m < M) {
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb) al[m * kc + b * 128 + 16 * nb + c] = (_Float16)(y[nb][i] * HX_RSQRT128);
+            }
+        }
+    }
+}
+
 // Transform and store all jobs: the first IN_PRE per wave from r, the rest loaded here.
 HX_INLINE void input_finish(uint32_t* a_lds, const InputRegs& r, const _Float16* x, const int* rows,
                             const _Float16* suh, int M, int K, int k0, int kc, bool pre_transformed)
@@ -463,7 +521,9 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     const int row_bytes = tiles_n * NW * 4;
     auto soff = [&](int st) { return ((k0 + step_k(min(st, steps - 1))) >> 4) * row_bytes; };
     InputRegs in;
-    if (!g.pre_transformed) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, false);
+    // several rows: the transform on the matrix cores (its loads are issued there)
+    constexpr bool MF_IN = MT >= 4;
+    if (!g.pre_transformed && !MF_IN) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, false);
     if (steps > 0) {
 #pragma unroll
         for (int j = 0; j < PF; ++j) load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff(j));
@@ -471,7 +531,8 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
 
     before_input();
     if (g.pre_transformed) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, true);
-    input_finish(a_lds, in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, g.pre_transformed);
+    if (MF_IN && !g.pre_transformed) input_mfma(a_lds, g.x, g.rows, g.suh, g.M, g.K, k0, kc);
+    else input_finish(a_lds, in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, g.pre_transformed);
     hx_lds_barrier();
     after_input();
     if constexpr (AFFINE) {
