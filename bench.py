@@ -208,10 +208,12 @@ def bench_linears(torch, moe, exl3, only: str = ""):
 
 
 def bench_sweep(torch, moe, layers_n: int = 42):
-    """BASELINE config 5b: 42 resident MoE layers (288 x 2-bit experts each), 1 token, independent
-    seeded routing per layer; one step = the 42 layers back to back."""
+    """BASELINE config 5b: 42 resident MoE layers (288 routed x 2-bit experts + one 2-bit shared
+    expert each), 1 token, independent seeded routing per layer; one step = the 42 layers back to
+    back.  Bytes per layer: the 8 routed and the shared expert's compressed weights."""
     E, hidden, inter = 288, 4096, 2048
-    layers = [moe.MoeLayer(moe.ExpertSet.synthetic(E, hidden, inter, 2, seed=20000 + i), None, topk=8)
+    layers = [moe.MoeLayer(moe.ExpertSet.synthetic(E, hidden, inter, 2, seed=20000 + i),
+                           moe.synthetic_dense_mlp(hidden, inter, 2, seed=30000 + i), topk=8)
               for i in range(layers_n)]
     g = torch.Generator(device="cuda")
     g.manual_seed(5)
@@ -224,12 +226,15 @@ def bench_sweep(torch, moe, layers_n: int = 42):
         for i in range(layers_n):
             layers[i](x, scores[i], y=ys[i], ws=ws)
     us = graph_time_us(torch, run, reps=10, inner=2)
-    step_bytes = layers_n * 8 * layers[0].experts.weight_bytes([0])
+    moe.check_status(ws)
+    step_bytes = layers_n * 9 * layers[0].experts.weight_bytes([0])
+    assert step_bytes == layers_n * 56954880
     del layers
     return {"layers": layers_n, "us_per_step": round(us, 1), "us_per_layer": round(us / layers_n, 2),
             "weight_gbs": round(step_bytes / us / 1e3, 1),
-            "pct_hbm": round(100 * step_bytes / us / 1e3 / HBM_PEAK_GBS, 2),
-            "note": "routed experts only (8 per layer); weights of all 42 layers resident (~71 GiB)"}
+            "pct_hbm": round(100 * step_bytes / us / 1e3 / HBM_PEAK_GBS, 2), "bytes_per_step": step_bytes,
+            "note": "8 routed + 1 shared expert per layer (42 x 56,954,880 B); weights of all 42 layers "
+                    "resident (~72 GiB)"}
 
 
 def cpu_baseline(layers, budget_s: float):

@@ -155,7 +155,9 @@ int hx_moe_check_status(void* workspace, hx_stream_t stream)
                    "hx_moe_check_status");
     if (r == 0) r = hip_status(hipStreamSynchronize((hipStream_t)stream), "hx_moe_check_status");
     if (r != 0) return r;
-    return fail(HX_ERR_TIMEOUT, "hx_moe_check_status: a bounded wait of the few-token MoE layer gave up");
+    if (v & hx::DEC_STATUS_TIMEOUT)
+        return fail(HX_ERR_TIMEOUT, "hx_moe_check_status: a bounded wait of the few-token MoE layer gave up");
+    return fail(HX_ERR_UNSUPPORTED, "hx_moe_check_status: a per-expert bit table holds a width outside 1..8");
 }
 
 // Debug option: with HX_MOE_SYNC_CHECK=1 in the environment, every few-token MoE call synchronizes
@@ -322,13 +324,30 @@ int hx_exl3_unpack_trellis(void* unpacked, const void* packed, int rows, int col
 }
 
 int hx_had_r_128(const void* input, void* output, const void* pre_scale, const void* post_scale, int64_t rows,
-                 int cols, float r_scale, hx_stream_t stream)
+                 int cols, int dtype, float scale, hx_stream_t stream)
 {
-    if (!input || !output || rows < 0 || cols <= 0 || cols % 128) return fail(HX_ERR_INVALID, "hx_had_r_128: bad arguments");
-    return hip_status(hx::launch_had_r_128(static_cast<const _Float16*>(input), static_cast<_Float16*>(output),
-                                           static_cast<const _Float16*>(pre_scale),
-                                           static_cast<const _Float16*>(post_scale), (long)rows, cols, r_scale,
-                                           (hipStream_t)stream),
+    return hx_had_r_128_dual(input, output, pre_scale, post_scale, nullptr, nullptr, nullptr, nullptr, rows, cols, dtype,
+                             scale, stream);
+}
+
+int hx_had_r_128_dual(const void* input1, void* output1, const void* pre_scale1, const void* post_scale1,
+                      const void* input2, void* output2, const void* pre_scale2, const void* post_scale2,
+                      int64_t rows, int cols, int dtype, float scale, hx_stream_t stream)
+{
+    const bool dual = input2 != nullptr || output2 != nullptr;
+    if (!input1 || !output1 || (dual && (!input2 || !output2)) || rows < 0 || cols <= 0 || cols % 128)
+        return fail(HX_ERR_INVALID, "hx_had_r_128: bad arguments (cols must be a positive multiple of 128)");
+    if (dtype != HX_DTYPE_HALF && dtype != HX_DTYPE_FLOAT)
+        return fail(HX_ERR_INVALID, "hx_had_r_128: dtype must be HX_DTYPE_HALF or HX_DTYPE_FLOAT");
+    if ((pre_scale1 && post_scale1) || (pre_scale2 && post_scale2))
+        return fail(HX_ERR_INVALID, "hx_had_r_128: pre_scale and post_scale are exclusive");
+    if (dual && (!pre_scale1 != !pre_scale2 || !post_scale1 != !post_scale2))
+        return fail(HX_ERR_INVALID, "hx_had_r_128_dual: both tensors need the same scaling mode");
+    const int mode = pre_scale1 ? 1 : post_scale1 ? 2 : 0;
+    const void* s1 = pre_scale1 ? pre_scale1 : post_scale1;
+    const void* s2 = pre_scale2 ? pre_scale2 : post_scale2;
+    return hip_status(hx::launch_had_r_128(input1, output1, s1, input2, output2, s2, mode, (long)rows, cols,
+                                           dtype == HX_DTYPE_FLOAT, scale * HX_HAD_RSQRT128, (hipStream_t)stream),
                       "hx_had_r_128");
 }
 

@@ -15,6 +15,7 @@
 // them; every width 1..8 (within the shape rule) is accepted here.
 #include <hip/hip_runtime.h>
 
+#include <errno.h>
 #include <fcntl.h>
 #include <stdio.h>
 #include <string.h>
@@ -180,20 +181,38 @@ struct JsonParser {
             return v;
         }
         if (lit("null")) return v;
-        // number: integers exactly (offsets exceed 2^53 only past 8 PB), others as double
+        // number (RFC 8259 grammar): integers exactly (offsets exceed 2^53 only past 8 PB), others as double
         const char* s = p;
-        if (p < end && (*p == '-' || *p == '+')) ++p;
+        if (p < end && *p == '-') ++p;
+        const char* digits = p;
+        while (p < end && *p >= '0' && *p <= '9') ++p;
+        if (p == digits) bad("unexpected character");
         bool integral = true;
-        while (p < end && ((*p >= '0' && *p <= '9') || *p == '.' || *p == 'e' || *p == 'E' || *p == '-' || *p == '+')) {
-            if (*p == '.' || *p == 'e' || *p == 'E') integral = false;
-            ++p;
+        if (p < end && *p == '.') {
+            integral = false;
+            const char* f = ++p;
+            while (p < end && *p >= '0' && *p <= '9') ++p;
+            if (p == f) bad("malformed number");
         }
-        if (p == s) bad("unexpected character");
+        if (p < end && (*p == 'e' || *p == 'E')) {
+            integral = false;
+            ++p;
+            if (p < end && (*p == '-' || *p == '+')) ++p;
+            const char* x = p;
+            while (p < end && *p >= '0' && *p <= '9') ++p;
+            if (p == x) bad("malformed number");
+        }
         const std::string t(s, p);
         v.kind = Json::NUM;
-        v.num = strtod(t.c_str(), nullptr);
+        char* stop = nullptr;
+        v.num = strtod(t.c_str(), &stop);
+        if (stop != t.c_str() + t.size()) bad("malformed number");
         v.is_int = integral;
-        if (integral) v.inum = strtoll(t.c_str(), nullptr, 10);
+        if (integral) {
+            errno = 0;
+            v.inum = strtoll(t.c_str(), &stop, 10);
+            if (errno == ERANGE || stop != t.c_str() + t.size()) bad("integer out of range");
+        }
         return v;
     }
 };
@@ -274,6 +293,7 @@ std::vector<std::string> shard_paths(const std::string& dir)
         size_t n;
         while ((n = fread(buf, 1, sizeof(buf), f)) > 0) text.append(buf, n);
         fclose(f);
+        std::string bad_shard;
         try {
             JsonParser jp{text.data(), text.data() + text.size()};
             const Json j = jp.value(0);
@@ -283,11 +303,18 @@ std::vector<std::string> shard_paths(const std::string& dir)
                     if (kv.second.kind == Json::STR) files.push_back(kv.second.str);
                 std::sort(files.begin(), files.end());
                 files.erase(std::unique(files.begin(), files.end()), files.end());
-                for (const auto& fn : files) out.push_back(dir + "/" + fn);
+                for (const auto& fn : files) {
+                    // a shard is a file of the checkpoint directory itself: no separators, no parent
+                    if (fn.empty() || fn.find('/') != std::string::npos || fn.find("..") != std::string::npos)
+                        bad_shard = fn;
+                    out.push_back(dir + "/" + fn);
+                }
             }
         } catch (const std::exception&) {
             out.clear();  // an unreadable index falls back to the directory scan, as the reference does
         }
+        if (!bad_shard.empty())
+            throw std::runtime_error("index names a shard outside the checkpoint directory: " + bad_shard);
     }
     if (out.empty()) {
         DIR* d = opendir(dir.c_str());
@@ -361,6 +388,65 @@ int fail(int code, const std::string& msg)
 
 // ------------------------------------------------------------------ C ABI
 
+namespace {
+
+// ---- routed-expert tensors of a layer
+//
+// Each projection of an expert is four tensors named model.language_model.layers.<l>.mlp.experts.<e>.
+// <proj>.<kind>; their form follows from the projection's in/out features and bit width.
+enum PieceKind { TRELLIS = 0, SUH = 1, SVH = 2, MUL1 = 3 };
+struct PieceSpec {
+    const char* leaf;
+    Dt dtype;
+};
+const PieceSpec kPieces[4] = {{"trellis", I16}, {"suh", F16}, {"svh", F16}, {"mul1", I32}};
+const char* const kProjNames[3] = {"gate_proj", "up_proj", "down_proj"};
+constexpr uint32_t kMul1Codebook = 0x83DCD12Du;
+
+std::string expert_tensor_name(int layer, int expert, int proj, PieceKind k)
+{
+    char buf[160];
+    snprintf(buf, sizeof(buf), "model.language_model.layers.%d.mlp.experts.%d.%s.%s", layer, expert,
+             kProjNames[proj], kPieces[k].leaf);
+    return buf;
+}
+
+// Shapes and byte sizes of the four tensors of a projection: gate/up map hidden -> intermediate,
+// down maps intermediate -> hidden.
+struct ProjForm {
+    int in, out;
+    std::vector<int64_t> shape[4];
+    uint64_t bytes[4];
+};
+ProjForm proj_form(int proj, int hidden, int intermediate, int bits)
+{
+    ProjForm f;
+    f.in = proj == 2 ? intermediate : hidden;
+    f.out = proj == 2 ? hidden : intermediate;
+    f.shape[TRELLIS] = {f.in / 16, f.out / 16, 16 * bits};
+    f.shape[SUH] = {f.in};
+    f.shape[SVH] = {f.out};
+    f.shape[MUL1] = {};
+    f.bytes[TRELLIS] = (uint64_t)f.in * f.out * bits / 8;
+    f.bytes[SUH] = 2ull * f.in;
+    f.bytes[SVH] = 2ull * f.out;
+    f.bytes[MUL1] = 4;
+    return f;
+}
+
+// Bit width of a trellis tensor of the projection's tile grid (third dimension 16 * bits, bits 2..8),
+// or -1 when it is not one.
+int trellis_width(const Tensor& t, const ProjForm& f)
+{
+    if (t.shape.size() != 3 || t.shape[0] != f.in / 16 || t.shape[1] != f.out / 16) return -1;
+    const int64_t d = t.shape[2];
+    return (d % 16 == 0 && d >= 32 && d <= 128) ? (int)(d / 16) : -1;
+}
+
+uint64_t round_up64(uint64_t v) { return (v + 63) / 64 * 64; }
+
+}  // namespace
+
 extern "C" {
 
 int hx_ckpt_open(const char* dir, hx_ckpt** out)
@@ -409,56 +495,74 @@ int hx_ckpt_read(const hx_ckpt* c, const char* name, void* host_dst, uint64_t by
     return 0;
 }
 
+
 int hx_ckpt_expert_layout(const hx_ckpt* c, int layer, int experts, int hidden, int intermediate,
                           hx_expert_layout* out)
 {
     if (!c || !out || experts < 1 || hidden < 16 || intermediate < 16 || hidden % 16 || intermediate % 16)
         return fail(HX_ERR_INVALID, "hx_ckpt_expert_layout: bad arguments");
-    static const char* proj[] = {"gate_proj", "up_proj", "down_proj"};
-    static const char* suffix[] = {".trellis", ".suh", ".svh", ".mul1"};
+    // The bit width of each projection is read off expert 0's trellis; every other tensor of every
+    // expert must then have exactly the form that width implies (one width per projection, as the
+    // slab has one stride).
+    int bits[3];
+    for (int p = 0; p < 3; ++p) {
+        const ProjForm f0 = proj_form(p, hidden, intermediate, 0);
+        const std::string tn = expert_tensor_name(layer, 0, p, TRELLIS);
+        const Tensor* tr = c->find(tn);
+        if (!tr) return fail(HX_ERR_INVALID, "hx_ckpt_expert_layout: no tensor " + tn);
+        const int w = trellis_width(*tr, f0);
+        if (w < 0)
+            return fail(HX_ERR_INVALID, "hx_ckpt_expert_layout: " + tn + " is not a (" + std::to_string(f0.in / 16) +
+                                            ", " + std::to_string(f0.out / 16) + ", 16*bits) trellis, bits 2..8");
+        bits[p] = w;
+    }
+    for (int e = 0; e < experts; ++e)
+        for (int p = 0; p < 3; ++p) {
+            const ProjForm f = proj_form(p, hidden, intermediate, bits[p]);
+            for (int k = 0; k < 4; ++k) {
+                const std::string tn = expert_tensor_name(layer, e, p, (PieceKind)k);
+                const Tensor* t = c->find(tn);
+                if (!t) return fail(HX_ERR_INVALID, "hx_ckpt_expert_layout: no tensor " + tn);
+                if (k == TRELLIS && e > 0 && trellis_width(*t, f) >= 0 && trellis_width(*t, f) != bits[p])
+                    return fail(HX_ERR_INVALID, "hx_ckpt_expert_layout: " + tn + " has " +
+                                                    std::to_string(trellis_width(*t, f)) + " bits, expert 0 has " +
+                                                    std::to_string(bits[p]) + " (one width per projection)");
+                const char* why = nullptr;
+                if (t->dtype != kPieces[k].dtype) why = "dtype";
+                else if (t->shape != f.shape[k]) why = "shape";
+                else if (t->bytes != f.bytes[k]) why = "byte size";
+                if (why)
+                    return fail(HX_ERR_INVALID, std::string("hx_ckpt_expert_layout: ") + tn + ": unexpected " + why +
+                                                    " for a " + std::to_string(f.in) + "->" + std::to_string(f.out) +
+                                                    " projection at " + std::to_string(bits[p]) + " bits");
+            }
+            // codebook 2 is the only codebook of the fused expert kernels
+            uint32_t mul = 0;
+            const std::string mn = expert_tensor_name(layer, e, p, MUL1);
+            try {
+                c->read(*c->find(mn), &mul);
+            } catch (const std::exception& ex) {
+                return fail(HX_ERR_INVALID, "hx_ckpt_expert_layout: " + mn + ": " + ex.what());
+            }
+            if (mul != kMul1Codebook)
+                return fail(HX_ERR_INVALID, "hx_ckpt_expert_layout: " + mn + " selects another codebook than mul1");
+        }
+    // Slab placement: the pieces in kind order, projection after projection, each projection's block
+    // padded to the 64-byte alignment the loaders keep.
     hx_expert_layout L;
     memset(&L, 0, sizeof(L));
-    try {
-        for (int e = 0; e < experts; ++e)
-            for (int p = 0; p < 3; ++p) {
-                const std::string base = "model.language_model.layers." + std::to_string(layer) + ".mlp.experts." +
-                                         std::to_string(e) + "." + proj[p];
-                const Tensor* t[4];
-                for (int q = 0; q < 4; ++q) {
-                    t[q] = c->find(base + suffix[q]);
-                    if (!t[q]) throw std::runtime_error("missing expert tensor " + base + suffix[q]);
-                }
-                const int in = p == 2 ? intermediate : hidden;
-                const int outn = p == 2 ? hidden : intermediate;
-                const auto& sh = t[0]->shape;
-                if (sh.size() != 3 || sh[0] != in / 16 || sh[1] != outn / 16 || sh[2] % 16 || sh[2] < 32 || sh[2] > 128)
-                    throw std::runtime_error("unsupported expert trellis shape: " + base);
-                const int bits = (int)(sh[2] / 16);
-                const uint64_t bytes[4] = {(uint64_t)in * outn * bits / 8, (uint64_t)in * 2, (uint64_t)outn * 2, 4};
-                const Dt types[4] = {I16, F16, F16, I32};
-                if (t[1]->shape != std::vector<int64_t>{in} || t[2]->shape != std::vector<int64_t>{outn} ||
-                    !t[3]->shape.empty())
-                    throw std::runtime_error("invalid expert scales/multiplier shape: " + base);
-                for (int q = 0; q < 4; ++q) {
-                    if (t[q]->bytes != bytes[q] || t[q]->dtype != types[q])
-                        throw std::runtime_error("invalid expert tensor size/dtype: " + base + suffix[q]);
-                    if (e == 0) L.piece[4 * p + q] = bytes[q];
-                    else if (L.piece[4 * p + q] != bytes[q])
-                        throw std::runtime_error("mixed expert bit widths within a layer: " + base);
-                }
-                uint32_t mul = 0;
-                c->read(*t[3], &mul);
-                if (mul != 0x83DCD12Du) throw std::runtime_error("unsupported expert mul1 codebook: " + base);
-                L.bits[p] = bits;
-            }
-    } catch (const std::exception& ex) {
-        return fail(HX_ERR_INVALID, std::string("hx_ckpt_expert_layout: ") + ex.what());
+    uint64_t at = 0;
+    for (int p = 0; p < 3; ++p) {
+        const ProjForm f = proj_form(p, hidden, intermediate, bits[p]);
+        for (int k = 0; k < 4; ++k) {
+            L.off[4 * p + k] = at;
+            L.piece[4 * p + k] = f.bytes[k];
+            at += f.bytes[k];
+        }
+        at = round_up64(at);
+        L.bits[p] = bits[p];
     }
-    for (int q = 0; q < 12; ++q) {
-        L.off[q] = L.stride;
-        L.stride += L.piece[q];
-        if (q % 4 == 3) L.stride = (L.stride + 63) & ~(uint64_t)63;
-    }
+    L.stride = at;
     *out = L;
     return 0;
 }
@@ -469,14 +573,11 @@ int hx_ckpt_load_experts(const hx_ckpt* c, int layer, int experts, const hx_expe
     if (!c || !L || !slab || experts < 1) return fail(HX_ERR_INVALID, "hx_ckpt_load_experts: bad arguments");
     if ((uint64_t)experts * L->stride > slab_bytes)
         return fail(HX_ERR_WORKSPACE, "hx_ckpt_load_experts: slab smaller than experts * layout.stride");
-    static const char* proj[] = {"gate_proj", "up_proj", "down_proj"};
-    static const char* suffix[] = {".trellis", ".suh", ".svh", ".mul1"};
     // the 12 tensors of every expert, found before anything is read
     std::vector<const Tensor*> t((size_t)experts * 12);
     for (int e = 0; e < experts; ++e)
         for (int q = 0; q < 12; ++q) {
-            const std::string n = "model.language_model.layers." + std::to_string(layer) + ".mlp.experts." +
-                                  std::to_string(e) + "." + proj[q / 4] + suffix[q % 4];
+            const std::string n = expert_tensor_name(layer, e, q / 4, (PieceKind)(q % 4));
             t[(size_t)e * 12 + q] = c->find(n);
             if (!t[(size_t)e * 12 + q] || t[(size_t)e * 12 + q]->bytes != L->piece[q])
                 return fail(HX_ERR_INVALID, "hx_ckpt_load_experts: tensor missing or not as in the layout: " + n);

@@ -87,6 +87,13 @@ HX_INLINE void buf_words(uint32_t* r, __amdgpu_buffer_rsrc_t rs, int voff, int s
     }
 }
 
+// VMEM instructions that load_quarter_buf issues: one dword for the wrapped first word, then the
+// BITS words in 16-byte pieces (buf_words).  Waits that count loads in flight (the MFMA tile's
+// s_waitcnt on its LDS-DMA ring) take their per-chunk count from here.  Each piece is its own
+// buffer-load builtin with its own offset register, so the compiler cannot merge pieces into fewer
+// instructions (which would make a counted wait too short).
+constexpr int quarter_buf_vmem(int bits) { return 1 + (bits + 3) / 4; }
+
 template <int BITS>
 HX_INLINE void load_quarter_buf(uint32_t* r, __amdgpu_buffer_rsrc_t rs, int voff0, int voff1, int soff)
 {

@@ -28,8 +28,9 @@ hipError_t launch_linear_mfma(const _Float16* a_had, const uint16_t* trellis, co
 // utilities (hx_misc.hip)
 hipError_t launch_reconstruct(_Float16* out, const uint16_t* packed, int packed_rows, int packed_cols,
                               int unpacked_cols, int bits, int cb, long n_offset, hipStream_t st);
-hipError_t launch_had_r_128(const _Float16* in, _Float16* out, const _Float16* pre, const _Float16* post,
-                            long rows, int cols, float r_scale, hipStream_t st);
+hipError_t launch_had_r_128(const void* in1, void* out1, const void* scale1, const void* in2, void* out2,
+                            const void* scale2, int scale_mode, long rows, int cols, bool fp32, float r_scale,
+                            hipStream_t st);
 hipError_t launch_routing(const _Float16* scores, const _Float16* bias, int64_t* idx, _Float16* w, int bsz, int E,
                           int K, float scale, hipStream_t st, bool use_topk = true, int act_fn = 0);
 hipError_t launch_permute(const int64_t* ids, const _Float16* w, int M, int topk, int E, int64_t* expert_count,

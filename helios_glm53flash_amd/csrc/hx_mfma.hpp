@@ -258,7 +258,7 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
     // VMEM instructions per chunk: A (DMA) and trellis words; chunk c + 1's A is complete once at
     // most the loads of the PF - 1 later chunks are outstanding (their order within a step is left
     // to the compiler, so the count takes whole chunks)
-    constexpr int NT = 1 + (BITS + 3) / 4;
+    constexpr int NT = quarter_buf_vmem(BITS);  // load_t = one load_quarter_buf
     constexpr int A_WAIT = (PF - 1) * (NA + NT);
     static_assert(!DMA || A_WAIT < 64, "vmcnt range");
     // chunk 0: the prologue issued at most the other chunks' loads after it

@@ -1,6 +1,7 @@
 // hx_misc.hip -- trellis reconstruct, standalone Hadamard-128, sigmoid top-k router, deterministic
 // MoE permutation, ordered reduction and swiglu for gfx950.
 #include "hx_device.hpp"
+#include <type_traits>
 #include "hx_kernels.hpp"
 
 namespace hx {
@@ -49,35 +50,70 @@ hipError_t launch_reconstruct(_Float16* out, const uint16_t* packed, int packed_
 
 // ------------------------------------------------------------------ had_r_128
 
-// Row-wise Hadamard-128 with optional fp16 pre/post scales (reference hadamard.cu had_r_128:
-// pre-scale by fp16 multiply, transform in fp32, times r_scale, round to fp16, post-scale by
-// fp16 multiply).  One wave per 128-element block.
-__global__ __launch_bounds__(256) void had_r_128_kernel(const _Float16* in, _Float16* out, const _Float16* pre,
-                                                        const _Float16* post, long blocks, int cols, float r_scale)
+// Row-wise Hadamard-128 with an optional fp16 scale per column, applied before (SCALE 1) or after
+// (SCALE 2) the transform, on one or two tensors of rows x cols (reference hadamard.cu had_r_128 /
+// had_r_128_dual, hadamard_inner.cuh:93-225).  fp16 data: pre-scale by an fp16 multiply, transform
+// in fp32, times r_scale, round to fp16, post-scale by an fp16 multiply.  fp32 data: the scales are
+// widened and every step stays in fp32.  One wave per 128-element block, two elements per lane;
+// blocks past the first tensor's belong to the second.
+struct HadPair {
+    const void* in[2];
+    void* out[2];
+    const _Float16* scale[2];
+};
+
+template <typename T, int SCALE>
+__global__ __launch_bounds__(256) void had_r_128_kernel(HadPair job, long blocks, int cols, float r_scale)
 {
     const int lane = threadIdx.x & 63;
-    const long b = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (b >= blocks) return;
+    long b = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= 2 * blocks || (b >= blocks && !job.in[1])) return;
+    const int which = b >= blocks;
+    b -= which * blocks;
     const long row = b / (cols / 128);
     const int c = (int)(b % (cols / 128)) * 128 + 2 * lane;
-    hx_h2 v = *reinterpret_cast<const hx_h2*>(in + row * cols + c);
-    if (pre) v = v * *reinterpret_cast<const hx_h2*>(pre + c);
-    float v0 = (float)v.x, v1 = (float)v.y;
-    hx_had128_wave(v0, v1);
-    const float rs = r_scale / HX_RSQRT128;  // hx_had128_wave already applied 1/sqrt(128)
-    hx_h2 o = {(_Float16)(v0 * rs), (_Float16)(v1 * rs)};
-    if (post) o = o * *reinterpret_cast<const hx_h2*>(post + c);
-    *reinterpret_cast<hx_h2*>(out + row * cols + c) = o;
+    const T* in = static_cast<const T*>(job.in[which]) + row * cols + c;
+    T* out = static_cast<T*>(job.out[which]) + row * cols + c;
+    const _Float16* sc = job.scale[which];
+    const float rs = r_scale / HX_RSQRT128;  // hx_had128_wave already applies 1/sqrt(128)
+    if constexpr (std::is_same<T, float>::value) {
+        float v0 = in[0], v1 = in[1];
+        if (SCALE == 1) v0 *= (float)sc[c], v1 *= (float)sc[c + 1];
+        hx_had128_wave(v0, v1);
+        v0 *= rs, v1 *= rs;
+        if (SCALE == 2) v0 *= (float)sc[c], v1 *= (float)sc[c + 1];
+        out[0] = v0, out[1] = v1;
+    } else {
+        hx_h2 v = *reinterpret_cast<const hx_h2*>(in);
+        if (SCALE == 1) v = v * *reinterpret_cast<const hx_h2*>(sc + c);
+        float v0 = (float)v.x, v1 = (float)v.y;
+        hx_had128_wave(v0, v1);
+        hx_h2 o = {(_Float16)(v0 * rs), (_Float16)(v1 * rs)};
+        if (SCALE == 2) o = o * *reinterpret_cast<const hx_h2*>(sc + c);
+        *reinterpret_cast<hx_h2*>(out) = o;
+    }
 }
 
-hipError_t launch_had_r_128(const _Float16* in, _Float16* out, const _Float16* pre, const _Float16* post,
-                            long rows, int cols, float r_scale, hipStream_t st)
+template <typename T>
+static void had_launch(const HadPair& job, int scale_mode, long blocks, int cols, float r_scale, hipStream_t st)
+{
+    const long total = (job.in[1] ? 2 : 1) * blocks;
+    const dim3 grid((unsigned)((total + 3) / 4));
+    if (scale_mode == 1) hipLaunchKernelGGL((had_r_128_kernel<T, 1>), grid, dim3(256), 0, st, job, blocks, cols, r_scale);
+    else if (scale_mode == 2) hipLaunchKernelGGL((had_r_128_kernel<T, 2>), grid, dim3(256), 0, st, job, blocks, cols, r_scale);
+    else hipLaunchKernelGGL((had_r_128_kernel<T, 0>), grid, dim3(256), 0, st, job, blocks, cols, r_scale);
+}
+
+hipError_t launch_had_r_128(const void* in1, void* out1, const void* scale1, const void* in2, void* out2,
+                            const void* scale2, int scale_mode, long rows, int cols, bool fp32, float r_scale,
+                            hipStream_t st)
 {
     if (cols % 128) return hipErrorInvalidValue;
-    long blocks = rows * (cols / 128);
+    const long blocks = rows * (cols / 128);
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(had_r_128_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, st, in, out, pre, post,
-                       blocks, cols, r_scale);
+    HadPair job{{in1, in2}, {out1, out2}, {(const _Float16*)scale1, (const _Float16*)scale2}};
+    if (fp32) had_launch<float>(job, scale_mode, blocks, cols, r_scale, st);
+    else had_launch<_Float16>(job, scale_mode, blocks, cols, r_scale, st);
     return hipGetLastError();
 }
 

@@ -32,6 +32,8 @@ namespace hx {
 constexpr int DEC_MAX_R = 64;  // T * topk rows handled by the few-token path
 constexpr int DEC_SHARED = -2;  // build_plan: the workgroup's slot is the shared expert
 constexpr int DEC_STATUS_INT = 10242;  // int index of the wait-status word in the counter area
+constexpr int DEC_STATUS_TIMEOUT = 1;  // status bits: a bounded wait gave up
+constexpr int DEC_STATUS_BAD_BITS = 2; // a per-expert bit table held a width outside 1..8
 
 // Routing plan of one call: sorted rows and active-expert slots.
 // Tables of a workgroup's slot's expert (or of the shared expert) that its unit uses: trellis and
@@ -92,8 +94,8 @@ struct MoeDecodeArgs {
     int* exit_count;               // workgroups that finished (zero between calls)
     int units_gu, units_d;         // workgroups of the gate/up and down phases (grid = their sum)
     int* ready;                    // [slots][inter/128] 1 once the guad epilogue stored that block
-    int* status;                   // set to 1 when a bounded wait gave up (never expected); read and
-                                   // cleared by hx_moe_check_status
+    int* status;                   // DEC_STATUS_* bits (never expected to be set); read and cleared by
+                                   // hx_moe_check_status
     // outputs
     int64_t* out_idx;              // optional router outputs [T][topk]
     _Float16* out_w;
@@ -691,10 +693,11 @@ HX_INLINE void wait_flag(const int* flag, int target, int* status)
         if (spins < 4) __builtin_amdgcn_s_sleep(4);
         else if (spins < 16) __builtin_amdgcn_s_sleep(16);
         else __builtin_amdgcn_s_sleep(64);
-        if ((++spins & 1023) == 0 && __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+        if ((++spins & 1023) == 0 &&
+            (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & DEC_STATUS_TIMEOUT))
             break;  // another wait already gave up: do not add its bound to every later wait
         if (spins > (1 << 22)) {
-            __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_or(status, DEC_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
     }
@@ -818,7 +821,17 @@ __device__ __forceinline__ void d_segment(const MoeDecodeArgs& a, const DecodePl
         hx_lds_barrier();
     };
     gemv_range<BITS, CB, MT, DEC_KS, DEC_PF>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs, wait_inputs);
+}
 
+// Split-K handoff of a down unit: publish, arrive; the last unit of the column group runs the down
+// epilogue and, as the last slot of the column, the combine.
+template <int MT>
+__device__ __forceinline__ void d_finish(const MoeDecodeArgs& a, const DecodePlan& plan, const Split& sp, long c,
+                                         int j, int slot, float* cs)
+{
+    const int gd = a.hidden >> 7, KB = a.inter >> 7;
+    const int cg = (int)(c % gd);
+    const SlotInfo si = slot_info(a, plan, slot);
     const int count = sp.count(c);
     float* pbase = a.partial_d + (size_t)(slot * gd + cg) * (KB + 1) * 8 * 128;
     publish_partial<MT>(pbase, si.count, 128, 0, j, cs);
@@ -864,10 +877,17 @@ __device__ __forceinline__ void run_unit(const MoeDecodeArgs& a, const DecodePla
             HX_SEG_CASE(1) HX_SEG_CASE(2) HX_SEG_CASE(3) HX_SEG_CASE(4)
             HX_SEG_CASE(5) HX_SEG_CASE(6) HX_SEG_CASE(7) HX_SEG_CASE(8)
 #undef HX_SEG_CASE
-            default: break;
+            default:
+                // a per-expert width outside 1..8 in the device bit tables: flagged for
+                // hx_moe_check_status; the unit still takes part in its handoff below, so no
+                // consumer waits for it and every counter returns to zero
+                if (threadIdx.x == 0)
+                    __hip_atomic_fetch_or(a.status, DEC_STATUS_BAD_BITS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
         }
     }
     if (gu) gu_finish<MT, BITS == 0>(a, plan, sp, c, slot, cs_g, cs_u);
+    else d_finish<MT>(a, plan, sp, c, j, slot, cs_g);
 }
 
 // BITS = 0 dispatches each segment on its projection's bit width at run time (mixed-bit layers, and

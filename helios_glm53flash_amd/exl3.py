@@ -184,13 +184,32 @@ def unpack_trellis(unpacked: torch.Tensor, packed: torch.Tensor, rows: int, cols
           "hx_exl3_unpack_trellis")
 
 
+_HAD_DTYPES = {torch.float16: 0, torch.float32: 1}
+
+
+def _had_dtype(*ts: torch.Tensor) -> int:
+    if ts[0].dtype not in _HAD_DTYPES or any(t.dtype != ts[0].dtype for t in ts):
+        raise TypeError("had_r_128: inputs and outputs must all be float16 or all float32")
+    return _HAD_DTYPES[ts[0].dtype]
+
+
 def had_r_128(input: torch.Tensor, output: torch.Tensor, pre_scale: Optional[torch.Tensor],
-              post_scale: Optional[torch.Tensor], rows: int, cols: int, r_scale: float = 0.088388347648,
-              stream=None) -> None:
-    _need(input, "input", (torch.float16,))
-    _need(output, "output", (torch.float16,))
-    check(lib.hx_had_r_128(input.data_ptr(), output.data_ptr(), _ptr(pre_scale), _ptr(post_scale), rows, cols,
-                           r_scale, _stream(stream)), "hx_had_r_128")
+              post_scale: Optional[torch.Tensor], rows: int, cols: int, scale: float = 1.0, stream=None) -> None:
+    """y = H128(x) * scale / sqrt(128) per 128-element group, fp16 or fp32 data (the dtype of `input`),
+    optional fp16 per-column scale before or after the transform (reference hadamard.cuh:14-25)."""
+    dt = _had_dtype(input, output)
+    check(lib.hx_had_r_128(input.data_ptr(), output.data_ptr(), _ptr(pre_scale), _ptr(post_scale), rows, cols, dt,
+                           scale, _stream(stream)), "hx_had_r_128")
+
+
+def had_r_128_dual(input1: torch.Tensor, output1: torch.Tensor, pre_scale1, post_scale1, input2: torch.Tensor,
+                   output2: torch.Tensor, pre_scale2, post_scale2, rows: int, cols: int, scale: float = 1.0,
+                   stream=None) -> None:
+    """had_r_128 on two tensors of one shape in one launch (reference hadamard.cuh:27-43)."""
+    dt = _had_dtype(input1, output1, input2, output2)
+    check(lib.hx_had_r_128_dual(input1.data_ptr(), output1.data_ptr(), _ptr(pre_scale1), _ptr(post_scale1),
+                                input2.data_ptr(), output2.data_ptr(), _ptr(pre_scale2), _ptr(post_scale2), rows,
+                                cols, dt, scale, _stream(stream)), "hx_had_r_128_dual")
 
 
 def routing_ds3_nogroup(scores: torch.Tensor, bias: Optional[torch.Tensor], topk_indices: torch.Tensor,
@@ -270,6 +289,6 @@ def gemm_nt_f16(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor, M: int, N: in
                              _stream(stream)), "hx_gemm_nt_f16")
 
 
-__all__ = ["GroupWords", "gemm", "gemm_nt_f16", "reconstruct_had_slice", "pack_trellis", "unpack_trellis", "gemv", "reconstruct", "reconstruct_slice", "had_r_128", "routing_ds3_nogroup",
+__all__ = ["GroupWords", "gemm", "gemm_nt_f16", "reconstruct_had_slice", "pack_trellis", "unpack_trellis", "gemv", "reconstruct", "reconstruct_slice", "had_r_128", "had_r_128_dual", "routing_ds3_nogroup",
            "moe_permute", "moe_reduce_sorted", "swiglu_clamp", "workspace", "MUL1", "HxError",
            "HX_GEMM_PATH_GEMV", "HX_GEMM_PATH_MFMA"]

@@ -3,8 +3,8 @@
 // (src/engine/runner.cpp) compile unchanged against libhx_exl3.so.
 //
 // Differences a caller sees: errors throw helios::exl3::Error (the reference aborts); the fused
-// kernels need a workspace, which this layer keeps per device (allocated on first use, zeroed once,
-// never freed while the process runs) unless the caller installs one with set_workspace().
+// kernels need a workspace, which this layer keeps per (device, stream) (allocated on first use, zeroed
+// once, never freed while the process runs) unless the caller installs one with set_workspace().
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -13,7 +13,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
-#include <unordered_map>
+#include <map>
 
 #include "../hx/exl3.h"
 
@@ -22,6 +22,9 @@ namespace helios {
 using Stream = hipStream_t;
 
 namespace exl3 {
+
+// reference: src/cuda/quant/helios_shim.cuh:120-124
+enum class DType : int { Half = HX_DTYPE_HALF, Float = HX_DTYPE_FLOAT };
 
 struct Error : std::runtime_error {
     explicit Error(const std::string& s) : std::runtime_error(s) {}
@@ -33,56 +36,68 @@ inline int check(int code, const char* what)
     return code;
 }
 
-// Per-device workspace (the reference keeps its lock buffer in a per-device singleton,
-// src/cuda/quant/exl3_devctx.cu:60-71).
+// Workspace of one (device, stream) pair (the reference keeps one lock buffer per device,
+// src/cuda/quant/exl3_devctx.cu:60-71, and is unsafe across streams).  Calls on different streams get
+// different buffers, so their arrival counters and ready flags never meet.  A buffer that must grow is
+// replaced after a device-wide synchronisation, since kernels queued on any stream may still use it.
+// Grow outside graph capture: run each call shape once on the capturing stream first.
 class Workspace {
 public:
+    struct View {
+        void* ptr;
+        size_t bytes;
+    };
     static Workspace& get()
     {
         static Workspace w;
         return w;
     }
-    void* acquire(size_t bytes, Stream s)
+    View acquire(size_t bytes, Stream s)
     {
         std::lock_guard<std::mutex> g(mu_);
         int dev = 0;
         (void)hipGetDevice(&dev);
-        Slot& slot = slots_[dev];
+        auto it = installed_.find(dev);
+        if (it != installed_.end()) {
+            if (it->second.bytes < bytes) throw Error("installed workspace is smaller than the call needs");
+            return View{it->second.ptr, it->second.bytes};
+        }
+        Slot& slot = slots_[Key{dev, s}];
         if (slot.bytes < bytes) {
-            if (slot.ptr && slot.owned) {
-                (void)hipStreamSynchronize(s);
+            if (slot.ptr) {
+                if (hipDeviceSynchronize() != hipSuccess) throw Error("device synchronisation failed");
                 (void)hipFree(slot.ptr);
+                slot = Slot{};
             }
             if (hipMalloc(&slot.ptr, bytes) != hipSuccess) throw Error("workspace allocation failed");
-            check(hx_workspace_init(slot.ptr, bytes, (hx_stream_t)s), "hx_workspace_init");
             slot.bytes = bytes;
-            slot.owned = true;
+            check(hx_workspace_init(slot.ptr, bytes, (hx_stream_t)s), "hx_workspace_init");
         }
-        return slot.ptr;
+        return View{slot.ptr, slot.bytes};
     }
-    size_t size()
-    {
-        int dev = 0;
-        (void)hipGetDevice(&dev);
-        return slots_[dev].bytes;
-    }
-    // Install a caller-owned, zero-filled workspace for the current device.
+    // Install a caller-owned, zero-filled workspace for every call on the current device; the caller
+    // then keeps calls on different streams from overlapping.
     void set(void* ptr, size_t bytes)
     {
         std::lock_guard<std::mutex> g(mu_);
         int dev = 0;
         (void)hipGetDevice(&dev);
-        slots_[dev] = Slot{ptr, bytes, false};
+        installed_[dev] = Slot{ptr, bytes};
     }
 
 private:
     struct Slot {
         void* ptr = nullptr;
         size_t bytes = 0;
-        bool owned = false;
+    };
+    struct Key {
+        int dev;
+        Stream stream;
+        bool operator<(const Key& o) const { return dev != o.dev ? dev < o.dev : stream < o.stream; }
     };
     std::mutex mu_;
-    std::unordered_map<int, Slot> slots_;
+    std::map<Key, Slot> slots_;
+    std::map<int, Slot> installed_;
 };
 
 inline void set_workspace(void* ptr, size_t bytes) { Workspace::get().set(ptr, bytes); }
@@ -104,9 +119,9 @@ inline int gemm(void* y, const void* x, const GroupWords& w, int M, int N, int K
     (void)force_num_sms;
     const hx_group_words g{w.trellis, w.suh, w.svh, w.mul1};
     const size_t ws_bytes = hx_exl3_gemm_workspace_size(M, N, K);
-    void* ws = Workspace::get().acquire(ws_bytes, s);
-    return check(hx_exl3_gemm(y, x, &g, M, N, K, bits, y_fp32, (hx_stream_t)s, a_had, mcg, ws,
-                              Workspace::get().size()),
+    const Workspace::View ws = Workspace::get().acquire(ws_bytes, s);
+    return check(hx_exl3_gemm(y, x, &g, M, N, K, bits, y_fp32, (hx_stream_t)s, a_had, mcg, ws.ptr,
+                              ws.bytes),
                  "helios::exl3::gemm");
 }
 
@@ -188,12 +203,12 @@ inline void moe_grouped(const void* x, void* y, const int64_t* expert_count, con
                              reinterpret_cast<const void* const*>(tables.down_svh),
                              nullptr, nullptr, nullptr, 0u};
     const size_t ws_bytes = hx_moe_workspace_size(tokens, hidden_dim, intermediate_dim, num_experts, topk);
-    void* ws = Workspace::get().acquire(ws_bytes, s);
+    const Workspace::View ws = Workspace::get().acquire(ws_bytes, s);
     check(hx_moe_grouped(x, static_cast<float*>(y), expert_count, token_sorted, weight_sorted, temp_state_g,
                          temp_state_u, temp_intermediate_g, temp_intermediate_u, &t, tokens, hidden_dim,
                          intermediate_dim, num_experts, topk, max_tokens_per_expert, concurrency, K_gate, K_up, K_down,
                          mcg, mul1, act_limit, act_function, num_active, (hx_stream_t)s, sorted_contributions,
-                         route_to_sorted, ws, Workspace::get().size()),
+                         route_to_sorted, ws.ptr, ws.bytes),
           "helios::exl3::moe_grouped");
 }
 
@@ -220,19 +235,30 @@ inline void moe_layer(void* y, float* y_routed, const void* x, const void* score
     if (shared)
         for (int i = 0; i < 3; ++i) sh[i] = hx_group_words{shared[i].trellis, shared[i].suh, shared[i].svh, shared[i].mul1};
     const size_t ws_bytes = hx_moe_workspace_size(tokens, hidden_dim, intermediate_dim, num_experts, topk);
-    void* ws = Workspace::get().acquire(ws_bytes, s);
+    const Workspace::View ws = Workspace::get().acquire(ws_bytes, s);
     check(hx_moe_layer(y, y_routed, x, scores, bias, &t, shared ? sh : nullptr, shared_bits, tokens, hidden_dim,
                        intermediate_dim, num_experts, topk, K_gate, K_up, K_down, routed_scale, act_limit, mcg, mul1,
-                       ws, Workspace::get().size(), (hx_stream_t)s),
+                       ws.ptr, ws.bytes, (hx_stream_t)s),
           "helios::exl3::moe_layer");
 }
 
-// reference: src/cuda/quant/hadamard.cuh:14-43 (fp16)
-inline void had_r_128(const void* input, void* output, const void* pre_scale, const void* post_scale, int64_t rows,
-                      int cols, float r_scale = 0.088388347648f, Stream s = 0)
+// reference: src/cuda/quant/hadamard.cuh:14-25 (the kernel multiplies by scale / sqrt(128); fp16 or fp32
+// data; pre_scale and post_scale are exclusive)
+inline void had_r_128(const void* input, void* output, const void* pre_scale, const void* post_scale, int rows,
+                      int cols, DType dt, float scale, Stream s = 0)
 {
-    check(hx_had_r_128(input, output, pre_scale, post_scale, rows, cols, r_scale, (hx_stream_t)s),
+    check(hx_had_r_128(input, output, pre_scale, post_scale, rows, cols, (int)dt, scale, (hx_stream_t)s),
           "helios::exl3::had_r_128");
+}
+
+// reference: src/cuda/quant/hadamard.cuh:27-43
+inline void had_r_128_dual(const void* input1, void* output1, const void* pre_scale1, const void* post_scale1,
+                           const void* input2, void* output2, const void* pre_scale2, const void* post_scale2, int rows,
+                           int cols, DType dt, float scale, Stream s = 0)
+{
+    check(hx_had_r_128_dual(input1, output1, pre_scale1, post_scale1, input2, output2, pre_scale2, post_scale2, rows,
+                            cols, (int)dt, scale, (hx_stream_t)s),
+          "helios::exl3::had_r_128_dual");
 }
 
 }  // namespace exl3

@@ -79,7 +79,8 @@ int hx_workspace_init(void* workspace, size_t bytes, hx_stream_t stream);
 /* Whether a bounded wait inside the few-token MoE layer (hx_moe_layer / hx_moe_grouped with T <= 8:
  * a down-projection workgroup waiting for its activations) gave up since the last check: synchronizes
  * `stream`, clears the flag, returns HX_ERR_TIMEOUT if it was set (the results of those calls are
- * then not to be trusted), else 0.  With HX_MOE_SYNC_CHECK=1 in the environment every few-token
+ * then not to be trusted), HX_ERR_UNSUPPORTED if a per-expert bit table held a width outside 1..8,
+ * else 0.  With HX_MOE_SYNC_CHECK=1 in the environment every few-token
  * hx_moe_layer / hx_moe_grouped call runs this check itself (outside graph capture) and returns its
  * result (debug option).  No counterpart in the reference, whose kernels cannot wait on each other. */
 int hx_moe_check_status(void* workspace, hx_stream_t stream);
@@ -137,10 +138,21 @@ int hx_exl3_reconstruct_had_slice(void* unpacked, const void* packed, const void
 int hx_exl3_pack_trellis(void* packed, const void* unpacked, int rows, int cols, int K, hx_stream_t stream);
 int hx_exl3_unpack_trellis(void* unpacked, const void* packed, int rows, int cols, int K, hx_stream_t stream);
 
-/* Row-wise Hadamard-128 with optional fp16 pre/post scales, fp16 in/out.
- * Replaces helios::exl3::had_r_128 (src/cuda/quant/hadamard.cuh:14-43) for DType::Half. */
+/* Row-wise Hadamard-128: y = H128(x) * scale / sqrt(128) on each consecutive 128-element group of a
+ * rows x cols tensor of `dtype` (HX_DTYPE_HALF fp16, HX_DTYPE_FLOAT fp32; in place when
+ * input == output), with an optional fp16 scale of `cols` entries applied before (pre_scale) or after
+ * (post_scale) the transform, not both.  Replaces helios::exl3::had_r_128 (src/cuda/quant/
+ * hadamard.cuh:14-25, hadamard.cu:86-170); dtype codes are the reference's DType values. */
+#define HX_DTYPE_HALF 0
+#define HX_DTYPE_FLOAT 1
+#define HX_HAD_RSQRT128 0.088388347648f
 int hx_had_r_128(const void* input, void* output, const void* pre_scale, const void* post_scale, int64_t rows,
-                 int cols, float r_scale, hx_stream_t stream);
+                 int cols, int dtype, float scale, hx_stream_t stream);
+/* The same transform on two tensors of one shape in one launch; both use the same scaling mode.
+ * Replaces helios::exl3::had_r_128_dual (src/cuda/quant/hadamard.cuh:27-43, hadamard.cu:173-290). */
+int hx_had_r_128_dual(const void* input1, void* output1, const void* pre_scale1, const void* post_scale1,
+                      const void* input2, void* output2, const void* pre_scale2, const void* post_scale2,
+                      int64_t rows, int cols, int dtype, float scale, hx_stream_t stream);
 
 /* ---- router / permutation / reduction ----------------------------------------------------- */
 

@@ -199,6 +199,55 @@ int main(int argc, char** argv)
         }
     }
 
+    // ---- helios::exl3::had_r_128 in the reference's form: DType, scale multiplied by 1/sqrt(128),
+    //      pre and post scales exclusive
+    {
+        const int rows = 8, cols = 256;
+        const auto x = normal_f16((size_t)rows * cols, r);
+        auto sc = normal_f16(cols, r);
+        uint16_t* dx = upload(x);
+        uint16_t* dsc = upload(sc);
+        uint16_t* dout = nullptr;
+        hip_ok(hipMalloc(&dout, (size_t)rows * cols * 2), "hipMalloc");
+        helios::exl3::had_r_128(dx, dout, nullptr, dsc, rows, cols, helios::exl3::DType::Half, 1.0f, s);
+        hip_ok(hipStreamSynchronize(s), "sync");
+        const auto o = download(dout, (size_t)rows * cols);
+        dump("had_x", x.data(), x.size() * 2);
+        dump("had_post", sc.data(), sc.size() * 2);
+        dump("had_y", o.data(), o.size() * 2);
+        int refused = 0;
+        try {
+            helios::exl3::had_r_128(dx, dout, dsc, dsc, rows, cols, helios::exl3::DType::Half, 1.0f, s);
+        } catch (const helios::exl3::Error&) {
+            refused = 1;
+        }
+        dump("had_refused", &refused, sizeof(refused));
+    }
+
+    // ---- the same linear on two streams at once: each (device, stream) has its own workspace
+    {
+        const int K = 4096, N = 2048, bits = 2;
+        Lin l(K, N, bits, r);
+        Stream s2 = nullptr;
+        hip_ok(hipStreamCreate(&s2), "hipStreamCreate");
+        uint16_t* dx = upload(normal_f16(K, r));
+        float *y1 = nullptr, *y2 = nullptr;
+        hip_ok(hipMalloc(&y1, (size_t)N * 4), "hipMalloc");
+        hip_ok(hipMalloc(&y2, (size_t)N * 4), "hipMalloc");
+        helios::exl3::gemm(y1, dx, l.gw(), 1, N, K, bits, true, s);
+        hip_ok(hipDeviceSynchronize(), "sync");
+        const auto ref = download(y1, N);
+        int same = 1;
+        for (int it = 0; it < 20; ++it) {
+            helios::exl3::gemm(y1, dx, l.gw(), 1, N, K, bits, true, s);
+            helios::exl3::gemm(y2, dx, l.gw(), 1, N, K, bits, true, s2);
+            hip_ok(hipDeviceSynchronize(), "sync");
+            const auto a = download(y1, N), b = download(y2, N);
+            for (int n = 0; n < N; ++n) same &= (a[n] == ref[n]) & (b[n] == ref[n]);
+        }
+        dump("two_streams_same", &same, sizeof(same));
+    }
+
     // ---- the engine's routed-MoE sequence (runner.cpp:759-764, 918-922): router, permutation,
     //      moe_grouped with sorted contributions, ordered reduction; then the dense fallback's row glue
     const int E = 16, hidden = 512, inter = 256, topk = 4, bits = 2;

@@ -70,6 +70,9 @@ def test_cpp_compat_header_compiles_and_links(tmp_path):
                    "    helios::glue::gemm_nt_f16(nullptr, nullptr, nullptr, 1, 288, 4096, false, false);\n"
                    "    helios::exl3::pack_trellis(nullptr, nullptr, 1, 1, 2);\n"
                    "    (void)helios::exl3::moe_max_concurrency(0);\n"
+                   "    helios::exl3::had_r_128(nullptr, nullptr, nullptr, nullptr, 1, 128, helios::exl3::DType::Half, 1.0f);\n"
+                   "    helios::exl3::had_r_128_dual(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1, 128,"
+                   " helios::exl3::DType::Float, 1.0f, nullptr);\n"
                    "    helios::exl3::reconstruct_had_slice(nullptr, nullptr, nullptr, nullptr, 8, 8, 128, 128, 2, false, true, 0);\n"
                    "  }\n  return 0;\n}\n")
     lib = Path(_lib.LIB_PATH)

@@ -282,3 +282,36 @@ def test_native_load_experts_and_layer(tmp_path):
         yb = moe.MoeLayer(py, None, topk=2)(x, s)
         torch.cuda.synchronize()
         assert torch.equal(ya, yb), T
+
+
+def test_native_rejects_shard_outside_directory(tmp_path):
+    """An index whose weight map names '../x' or an absolute path is refused, not followed."""
+    import json
+    from helios_glm53flash_amd import checkpoint as ck
+    from helios_glm53flash_amd._lib import HxError
+    make_checkpoint(tmp_path, shards=1)
+    for bad in ("../outside.safetensors", "/etc/passwd", "sub/inner.safetensors"):
+        (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": {"a": bad}}))
+        with pytest.raises(HxError, match="outside the checkpoint directory"):
+            ck.NativeCheckpoint(tmp_path)
+
+
+@pytest.mark.parametrize("offsets", ["[0, 12-3]", "[+0, 4]", "[0, 4e0]", "[0, 99999999999999999999999]", "[0, 4.]"])
+def test_native_rejects_malformed_offsets(tmp_path, offsets):
+    """data_offsets must be plain JSON integers: '12-3', '+0', '4e0', an overflowing integer or '4.' are
+    header errors, not numbers read up to the first odd character."""
+    import struct
+    from helios_glm53flash_amd import checkpoint as ck
+    from helios_glm53flash_amd._lib import HxError
+    head = ('{"t": {"dtype": "F16", "shape": [2], "data_offsets": %s}}' % offsets).encode()
+    (tmp_path / "model.safetensors").write_bytes(struct.pack("<Q", len(head)) + head + b"\0" * 16)
+    with pytest.raises(HxError):
+        ck.NativeCheckpoint(tmp_path)
+
+
+def test_native_accepts_plain_offsets(tmp_path):
+    import struct
+    from helios_glm53flash_amd import checkpoint as ck
+    head = b'{"__metadata__": {"v": -1.5e+2}, "t": {"dtype": "F16", "shape": [2], "data_offsets": [0, 4]}}'
+    (tmp_path / "model.safetensors").write_bytes(struct.pack("<Q", len(head)) + head + b"\0" * 4)
+    assert ck.NativeCheckpoint(tmp_path).tensor_count() == 1

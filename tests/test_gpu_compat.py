@@ -53,6 +53,27 @@ def test_compat_gemm(run):
         assert_close(y, O.linear(x, tr, suh, svh, K, N, bits, 2), what=f"compat gemm M={M}")
 
 
+def test_compat_had_r_128(run):
+    """helios::exl3::had_r_128(..., DType::Half, 1.0f, s) as the reference's test calls it
+    (test_reconstruct.cpp:330): the transform scaled by 1/sqrt(128), here with a post scale; pre and
+    post together are refused."""
+    from oracle import oracle as O
+    load, _ = run
+    x = load("had_x", np.uint16).reshape(8, 256)
+    post = load("had_post", np.uint16)
+    got = load("had_y", np.uint16).view(np.float16).astype(np.float64)
+    ref = O.had_r_128_f16(x, None, post, 0.088388347648).view(np.float16).astype(np.float64).reshape(-1)
+    assert np.all(np.abs(got - ref) <= np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) * 1.01)
+    assert int(load("had_refused", np.int32)[0]) == 1
+
+
+def test_compat_two_streams(run):
+    """Config-1 linears issued on two streams at once, 20 times: both equal the single-stream result
+    bit for bit (each stream has its own split-K counters)."""
+    load, _ = run
+    assert int(load("two_streams_same", np.int32)[0]) == 1
+
+
 def _experts(load, E, hidden, inter, bits):
     shapes = [(hidden, inter), (hidden, inter), (inter, hidden)]
     out = {"trellis": [[], [], []], "suh": [[], [], []], "svh": [[], [], []],

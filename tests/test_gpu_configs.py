@@ -5,7 +5,7 @@ per-weight rounding that the fused codebook-2 paths skip could accumulate."""
 import numpy as np
 import pytest
 
-from helpers import assert_close, make_linear, make_x, zipf_scores
+from helpers import assert_close, expert_contrib_numpy, make_linear, make_x, zipf_scores
 
 pytestmark = pytest.mark.gpu
 
@@ -52,14 +52,13 @@ def _al(v):
     return (v + 255) & ~255
 
 
-def test_moe_prefill_config4_zipf(hx):
-    """Config 4 at its workload: 4096 tokens, top-8 of 288 with Zipf(1.1) popularity, experts 0-143
-    2-bit and 144-287 3-bit.  The layer's own router indices and chunked permutation (read from its
-    workspace) are bit-exact for all 4096 tokens, its weights within one fp16 ulp; sampled rows (the
-    hottest expert's first and last token, a token routed only to experts with at most 64 rows, a token
-    of an expert with 65-128 rows, and fixed tokens) match the oracle."""
+@pytest.fixture(scope="module")
+def config4(hx):
+    """Config 4 at its workload, run once: 4096 tokens, top-8 of 288 with Zipf(1.1) popularity,
+    experts 0-143 2-bit and 144-287 3-bit.  Returns the layer's inputs, y_routed, its workspace's
+    router outputs and permutation, and the per-route contributions of the same routing through
+    moe_grouped(sorted_contributions) (the same grouped gate/up and down kernels)."""
     import torch
-    from oracle import oracle as O
     exl3, moe = hx
     E, hidden, inter, topk, T = 288, 4096, 2048, 8, 4096
     bits = [2 if e < 144 else 3 for e in range(E)]
@@ -71,12 +70,6 @@ def test_moe_prefill_config4_zipf(hx):
     y_routed = torch.empty((T, hidden), dtype=torch.float32, device="cuda")
     layer(_dev(x), _dev(scores), y_routed=y_routed, ws=ws)
     torch.cuda.synchronize()
-
-    idx, w = O.routing(scores, topk, 2.5)
-    counts = np.bincount(idx.reshape(-1), minlength=E)
-    # the workload has the shapes the prefill tiles are chosen for
-    assert counts.max() > 256 and ((counts > 64) & (counts <= 128)).any()
-
     # router outputs and permutation in the workspace (layout of MoeWs::plan: after the 64 KiB
     # counter area, idx int64[R], w fp16[R], expert_count int64[E+1], token_sorted int64[R],
     # weight_sorted fp16[R], route_to_sorted int64[R], each 256-byte aligned)
@@ -88,15 +81,43 @@ def test_moe_prefill_config4_zipf(hx):
     off_ws = _al(off_ts + 8 * R)
     off_r2s = _al(off_ws + 2 * R)
     raw = ws[:off_r2s + 8 * R].cpu().numpy()
-    assert np.array_equal(raw[off_idx:off_idx + 8 * R].view(np.int64).reshape(T, topk), idx)
+    d = dict(E=E, hidden=hidden, inter=inter, topk=topk, T=T, ex=ex, x=x, scores=scores,
+             y_routed=y_routed.cpu().numpy(),
+             idx=raw[off_idx:off_idx + 8 * R].view(np.int64).reshape(T, topk).copy(),
+             w=raw[off_w:off_w + 2 * R].view(np.uint16).reshape(T, topk).copy(),
+             cnt=raw[off_cnt:off_cnt + 8 * (E + 1)].view(np.int64).copy(),
+             ts=raw[off_ts:off_ts + 8 * R].view(np.int64).copy(),
+             wsr=raw[off_ws:off_ws + 2 * R].view(np.uint16).copy(),
+             r2s=raw[off_r2s:off_r2s + 8 * R].view(np.int64).copy())
+    contrib = torch.empty((R, hidden), dtype=torch.float32, device="cuda")
+    moe.moe_grouped(_dev(x), None, _dev(d["cnt"]), _dev(d["ts"]), _dev(d["wsr"], torch.float16), ex, T, topk,
+                    sorted_contributions=contrib)
+    torch.cuda.synchronize()
+    d["contrib"] = contrib.cpu().numpy()
+    return d
+
+
+def test_moe_prefill_config4_zipf(hx, config4):
+    """Config 4: the layer's own router indices and chunked permutation (read from its workspace)
+    are bit-exact for all 4096 tokens, its weights within one fp16 ulp; sampled rows (the hottest
+    expert's first and last token, a token routed only to experts with at most 64 rows, a token of an
+    expert with 65-128 rows, and fixed tokens) match the oracle."""
+    from oracle import oracle as O
+    c4 = config4
+    E, hidden, inter, topk, T, x = c4["E"], c4["hidden"], c4["inter"], c4["topk"], c4["T"], c4["x"]
+    idx, w = O.routing(c4["scores"], topk, 2.5)
+    counts = np.bincount(idx.reshape(-1), minlength=E)
+    # the workload has the shapes the prefill tiles are chosen for
+    assert counts.max() > 256 and ((counts > 64) & (counts <= 128)).any()
+    assert np.array_equal(c4["idx"], idx)
     # weights: sigmoid through exp, within one fp16 ulp of the oracle's (as the router test)
-    lw = raw[off_w:off_w + 2 * R].view(np.uint16).reshape(T, topk)
+    lw = c4["w"]
     assert np.abs(lw.view(np.float16).astype(np.float64) - w.view(np.float16).astype(np.float64)).max() <= 2 ** -9 * 2.5
     cnt, ts, wsr, r2s = O.permute(idx, lw, E)  # the permutation of the layer's own weights, bit-exact
-    assert np.array_equal(raw[off_cnt:off_cnt + 8 * (E + 1)].view(np.int64), cnt)
-    assert np.array_equal(raw[off_ts:off_ts + 8 * R].view(np.int64), ts)
-    assert np.array_equal(raw[off_ws:off_ws + 2 * R].view(np.uint16), wsr)
-    assert np.array_equal(raw[off_r2s:off_r2s + 8 * R].view(np.int64), r2s)
+    assert np.array_equal(c4["cnt"], cnt)
+    assert np.array_equal(c4["ts"], ts)
+    assert np.array_equal(c4["wsr"], wsr)
+    assert np.array_equal(c4["r2s"], r2s)
 
     hot = int(counts.argmax())
     hot_tokens = np.nonzero((idx == hot).any(axis=1))[0]
@@ -106,8 +127,61 @@ def test_moe_prefill_config4_zipf(hx):
     rows = sorted({int(hot_tokens[0]), int(hot_tokens[-1]), mid_tok, 0, 2047, T - 1}
                   | ({int(cold[0])} if len(cold) else set()))
     used = set(int(e) for e in idx[rows].reshape(-1))
-    ref, _ = O.moe_rows(x, hidden, inter, idx, w, rows, _oracle_experts(ex, used), None, 10.0)
-    assert_close(y_routed.cpu().numpy()[rows], ref, what=f"config 4 rows {rows}")
+    ref, _ = O.moe_rows(x, hidden, inter, idx, w, rows, _oracle_experts(c4["ex"], used), None, 10.0)
+    assert_close(c4["y_routed"][rows], ref, what=f"config 4 rows {rows}")
+
+
+def test_moe_prefill_config4_every_job(hx, config4):
+    """Config 4, every grouped-GEMM job: the prefill cuts each expert's rows into 128-row jobs (the
+    remainder as a 32-, 64- or 128-row tile); the first and last row of every (expert, job) pair are
+    compared against the dense numpy expert (decoded W_hat from the oracle's reconstruct, the fp16
+    rounding points of exl3_moe_kernel.cuh:85-262, pinned by test_moe_rows_matches_dense_numpy) as
+    per-route contributions, and the layer's y_routed equals the rank-order sum of those
+    contributions for all 4096 tokens."""
+    import concurrent.futures as cf
+    import os
+    from oracle import oracle as O
+    c4 = config4
+    E, hidden, inter, topk, T, ex = c4["E"], c4["hidden"], c4["inter"], c4["topk"], c4["T"], c4["ex"]
+    cnt, ts, wsr, r2s, contrib = c4["cnt"], c4["ts"], c4["wsr"], c4["r2s"], c4["contrib"]
+    off = np.concatenate([[0], np.cumsum(cnt[:E])])
+    jobs = []  # (expert, first sorted row, last sorted row)
+    for e in range(E):
+        for j0 in range(0, int(cnt[e]), 128):
+            jobs.append((e, int(off[e]) + j0, int(off[e]) + min(j0 + 128, int(cnt[e])) - 1))
+    # the workload has remainder jobs of every tile height, and 3-bit remainders off the 32-row grid
+    rem = [int(cnt[e]) % 128 for e in range(E)]
+    assert any(0 < r <= 32 for r in rem) and any(32 < r <= 64 for r in rem) and any(r > 64 for r in rem)
+    assert any(e >= 144 and cnt[e] > 128 and cnt[e] % 32 for e in range(E))
+    shapes = [(hidden, inter), (hidden, inter), (inter, hidden)]
+
+    def check_expert(e):
+        pos = sorted({p for (je, a, b) in jobs if je == e for p in (a, b)})
+        if not pos:
+            return e, [], None, None
+        Ws = []
+        for p, (K, N) in enumerate(shapes):
+            tr = _host(ex.trellis[p][e])
+            Ws.append(O.reconstruct(tr, K, N, ex.bits[p][e], 2).view(np.float16).astype(np.float64))
+        su = [_host(ex.suh[p][e]).astype(np.float64) for p in range(3)]
+        sv = [_host(ex.svh[p][e]).astype(np.float64) for p in range(3)]
+        tok = ts[pos] // topk
+        wt = wsr[pos].view(np.float16).astype(np.float64)
+        ref = expert_contrib_numpy(c4["x"][tok], *Ws, su, sv, wt, 10.0)
+        return e, pos, ref, contrib[pos]
+
+    got_all, ref_all, covered = [], [], 0
+    with cf.ThreadPoolExecutor(min(16, os.cpu_count() or 1)) as pool:
+        for e, pos, ref, got in pool.map(check_expert, range(E)):
+            if pos:
+                ref_all.append(ref)
+                got_all.append(got)
+                covered += sum(1 for (je, _, _) in jobs if je == e)
+    assert covered == len(jobs) and len(jobs) > 400, (covered, len(jobs))
+    assert_close(np.concatenate(got_all), np.concatenate(ref_all), what=f"config 4, {len(jobs)} jobs' end rows")
+    # the layer's combine: y_routed[t] = sum over ranks k of contribution row r2s[t * topk + k]
+    y_sum = contrib[r2s.reshape(T, topk)].astype(np.float64).sum(axis=1)
+    assert_close(c4["y_routed"], y_sum, tol=1e-5, what="config 4 y_routed vs contributions")
 
 
 @pytest.mark.parametrize("M", [1, 512])
@@ -153,14 +227,16 @@ def test_config2_every_m(hx):
 
 
 def test_decode_sweep_42_layers(hx):
-    """Config 5b: 42 decode layers of 288 2-bit experts each, all resident, run back to back on one
-    stream with independent seeded routing per layer.  Sampled layers equal the same layer run alone
-    (bit for bit), and two of them match the oracle."""
+    """Config 5b: 42 decode layers of 288 routed 2-bit experts and one 2-bit shared expert each, all
+    resident, run back to back on one stream with independent seeded routing per layer.  Sampled
+    layers equal the same layer run alone (bit for bit), and the full fp16 y (routed + shared) of
+    three layers matches the oracle."""
     import torch
     from oracle import oracle as O
     exl3, moe = hx
     E, hidden, inter, topk, L = 288, 4096, 2048, 8, 42
-    layers = [moe.MoeLayer(moe.ExpertSet.synthetic(E, hidden, inter, 2, seed=7000 + i), None, topk=topk)
+    layers = [moe.MoeLayer(moe.ExpertSet.synthetic(E, hidden, inter, 2, seed=7000 + i),
+                           moe.synthetic_dense_mlp(hidden, inter, 2, seed=8000 + i), topk=topk)
               for i in range(L)]
     r = np.random.default_rng(42)
     xs = [r.standard_normal((1, hidden)).astype(np.float16) for _ in range(L)]
@@ -168,21 +244,22 @@ def test_decode_sweep_42_layers(hx):
     xd = [_dev(v) for v in xs]
     sd = [_dev(v) for v in ss]
     ws = torch.zeros(layers[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
-    outs = [torch.empty((1, hidden), dtype=torch.float32, device="cuda") for _ in range(L)]
+    outs = [torch.empty((1, hidden), dtype=torch.float16, device="cuda") for _ in range(L)]
     for i in range(L):
-        layers[i](xd[i], sd[i], y_routed=outs[i], ws=ws)
+        layers[i](xd[i], sd[i], y=outs[i], ws=ws)
     torch.cuda.synchronize()
     moe.check_status(ws)
     for i in (0, 17, L - 1):
-        alone = torch.empty((1, hidden), dtype=torch.float32, device="cuda")
-        layers[i](xd[i], sd[i], y_routed=alone, ws=ws)
+        alone = torch.empty((1, hidden), dtype=torch.float16, device="cuda")
+        layers[i](xd[i], sd[i], y=alone, ws=ws)
         torch.cuda.synchronize()
         assert torch.equal(alone, outs[i]), f"layer {i} differs from its run in the sweep"
-    for i in (5, L - 2):
+    for i in (5, 30, L - 2):
         idx, w = O.routing(ss[i], topk, 2.5)
         used = set(int(e) for e in idx.reshape(-1))
-        ref, _ = O.moe_rows(xs[i], hidden, inter, idx, w, [0], _oracle_experts(layers[i].experts, used), None, 10.0)
-        assert_close(outs[i].cpu().numpy(), ref, what=f"sweep layer {i}")
+        _, ref = O.moe_rows(xs[i], hidden, inter, idx, w, [0], _oracle_experts(layers[i].experts, used),
+                            _oracle_shared(layers[i].shared), 10.0)
+        assert_close(outs[i].float().cpu().numpy(), ref.view(np.float16).astype(np.float64), what=f"sweep layer {i}")
 
 
 def _structured_inputs(K, suh, seed):

@@ -137,20 +137,71 @@ def test_reduce_sorted_random(hx):
     assert np.array_equal(y.cpu().numpy(), O.reduce_sorted(contrib, r2s, M, topk))
 
 
-def test_had_r_128(hx):
+@pytest.mark.parametrize("mode", ["none", "pre", "post"])
+@pytest.mark.parametrize("scale", [1.0, 2.5])
+def test_had_r_128(hx, mode, scale):
+    """fp16 data: within one fp16 ulp of the exact transform with the reference's rounding points;
+    `scale` is multiplied by 1/sqrt(128) inside (hadamard.cu:104)."""
     import torch
     from oracle import oracle as O
     r = np.random.default_rng(3)
     x = (r.integers(-1000, 1001, (64, 256)) / 250.0).astype(np.float16)
-    pre = r.choice([-1.0, 1.0], 256).astype(np.float16)
-    post = r.uniform(0.5, 1.5, 256).astype(np.float16)
+    sc = (r.choice([-1.0, 1.0], 256) * r.uniform(0.5, 1.5, 256)).astype(np.float16)
+    pre, post = (sc if mode == "pre" else None), (sc if mode == "post" else None)
     out = torch.empty((64, 256), dtype=torch.float16, device="cuda")
-    hx.had_r_128(_dev(x), out, _dev(pre), _dev(post), 64, 256)
+    hx.had_r_128(_dev(x), out, None if pre is None else _dev(pre), None if post is None else _dev(post), 64, 256,
+                 scale)
     torch.cuda.synchronize()
-    ref = O.had_r_128_f16(x, pre, post).view(np.float16).astype(np.float64)
+    ref = O.had_r_128_f16(x, pre, post, scale * 0.088388347648).view(np.float16).astype(np.float64)
     got = out.cpu().float().numpy().astype(np.float64)
     # fp32 butterfly order vs exact: at most one fp16 ulp apart
     assert np.all(np.abs(got - ref) <= np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) * 1.01)
+
+
+def _had_exact(x, pre=None, post=None, scale=1.0):
+    from scipy.linalg import hadamard
+    H = hadamard(128).astype(np.float64)
+    v = x.astype(np.float64).reshape(x.shape[0], -1, 128)
+    if pre is not None:
+        v = v * pre.astype(np.float64).reshape(-1, 128)
+    v = (v @ H) * (scale / np.sqrt(128.0))
+    if post is not None:
+        v = v * post.astype(np.float64).reshape(-1, 128)
+    return v.reshape(x.shape)
+
+
+@pytest.mark.parametrize("mode", ["none", "pre", "post"])
+def test_had_r_128_fp32_and_dual(hx, mode):
+    """DType::Float data (had_ff_r_128, hadamard.cu:140-166) against scipy's Sylvester matrix in fp64,
+    in place, and the dual form on two tensors equal to two single calls."""
+    import torch
+    r = np.random.default_rng(5)
+    x1 = r.standard_normal((33, 384)).astype(np.float32)
+    x2 = r.standard_normal((33, 384)).astype(np.float32)
+    s1 = r.uniform(0.5, 1.5, 384).astype(np.float16)
+    s2 = r.uniform(-1.5, -0.5, 384).astype(np.float16)
+    pick = lambda s: (s if mode == "pre" else None, s if mode == "post" else None)
+    d = lambda a: None if a is None else _dev(a)
+    a = _dev(x1).clone()
+    hx.had_r_128(a, a, d(pick(s1)[0]), d(pick(s1)[1]), 33, 384, 0.75)  # in place
+    torch.cuda.synchronize()
+    ref = _had_exact(x1, *pick(s1), scale=0.75)
+    assert np.abs(a.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
+    o1, o2 = torch.empty_like(a), torch.empty_like(a)
+    hx.had_r_128_dual(_dev(x1), o1, d(pick(s1)[0]), d(pick(s1)[1]), _dev(x2), o2, d(pick(s2)[0]), d(pick(s2)[1]),
+                      33, 384, 0.75)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, a)
+    ref2 = _had_exact(x2, *pick(s2), scale=0.75)
+    assert np.abs(o2.cpu().numpy() - ref2).max() <= 1e-5 * np.abs(ref2).max()
+    # fp16 dual equals two single calls bit for bit
+    h1, h2 = _dev(x1.astype(np.float16)), _dev(x2.astype(np.float16))
+    e1, e2, f1, f2 = (torch.empty_like(h1) for _ in range(4))
+    hx.had_r_128(h1, e1, d(pick(s1)[0]), d(pick(s1)[1]), 33, 384)
+    hx.had_r_128(h2, e2, d(pick(s2)[0]), d(pick(s2)[1]), 33, 384)
+    hx.had_r_128_dual(h1, f1, d(pick(s1)[0]), d(pick(s1)[1]), h2, f2, d(pick(s2)[0]), d(pick(s2)[1]), 33, 384)
+    torch.cuda.synchronize()
+    assert torch.equal(e1, f1) and torch.equal(e2, f2)
 
 
 def test_swiglu_clamp(hx):

@@ -105,6 +105,35 @@ def test_moe_decode_mixed_bits(hx):
     _run_layer(hx, E=12, hidden=256, inter=384, topk=3, T=2, bits=bits, shared_bits=(4, 4, 3), seed=3)
 
 
+def test_moe_decode_bad_bit_table_is_reported(hx):
+    """A per-expert bit table holding a width outside 1..8 (device data the host does not read) is
+    reported by the status check as HX_ERR_UNSUPPORTED; the units of that width still take part in
+    their handoffs, so the next call with a corrected table runs normally and equals the first."""
+    import torch
+    from helios_glm53flash_amd._lib import HxError
+    exl3, moe = hx
+    bits = [(2, 3, 4) if e % 2 else (3, 2, 2) for e in range(12)]
+    ex = moe.ExpertSet.synthetic(12, 256, 384, bits, seed=9)
+    layer = moe.MoeLayer(ex, moe.synthetic_dense_mlp(256, 384, 2, seed=10), topk=3)
+    r = np.random.default_rng(11)
+    x = torch.from_numpy(r.standard_normal((2, 256)).astype(np.float16)).cuda()
+    s = torch.from_numpy(r.standard_normal((2, 12)).astype(np.float16)).cuda()
+    ws = torch.zeros(layer.workspace_bytes(2), dtype=torch.uint8, device="cuda")
+    y0 = layer(x, s, ws=ws).clone()
+    moe.check_status(ws)
+    for which in (9, 11):  # the gate, then the down bit table (tables() keeps 9 pointer arrays first)
+        tab = ex._keep[which]
+        good = tab.clone()
+        tab.fill_(12)
+        with pytest.raises(HxError, match="width outside"):  # raised by the call (HX_MOE_SYNC_CHECK) or the check
+            layer(x, s, ws=ws)
+            moe.check_status(ws)
+        tab.copy_(good)
+        y1 = layer(x, s, ws=ws)
+        moe.check_status(ws)
+        assert torch.equal(y0, y1), which
+
+
 @pytest.mark.parametrize("T", [9, 40])
 def test_moe_prefill_small(hx, T):
     _run_layer(hx, E=16, hidden=512, inter=256, topk=4, T=T, bits=2, shared_bits=3, seed=20 + T)

@@ -13,7 +13,7 @@ import scipy.linalg
 import scipy.special
 
 from oracle import oracle as O
-from helpers import make_linear, make_x
+from helpers import expert_contrib_numpy, make_linear, make_x
 
 GOLD = Path(__file__).resolve().parent / "golden"
 
@@ -412,7 +412,8 @@ def _gelu_erf16(g):
 
 def _moe_layer_numpy(x, hidden, inter, idx, wt, ex, sh, L, act=None):
     """Dense numpy restatement of one MoE layer from decoded W_hat matrices and scipy's Sylvester
-    Hadamard (exl3_moe_kernel.cuh:57-262, hadamard_inner.cuh:284-481, runner.cpp:723-738,918-958).
+    Hadamard (exl3_moe_kernel.cuh:57-262, hadamard_inner.cuh:284-481, runner.cpp:723-738,918-958);
+    the routed expert is helpers.expert_contrib_numpy, which this pins.
     act: None SiLU, "gelu_erf" the exact GELU, "relu2" the non-gated relu2 (no gate GEMM)."""
     H = scipy.linalg.hadamard(128).astype(np.float64) / np.sqrt(128.0)
 
@@ -428,30 +429,15 @@ def _moe_layer_numpy(x, hidden, inter, idx, wt, ex, sh, L, act=None):
     T = x.shape[0]
     xd = x.astype(np.float64)
     y_routed = np.zeros((T, hidden), np.float32)
+    shapes = [(hidden, inter), (hidden, inter), (inter, hidden)]
     for t in range(T):
         for j in range(idx.shape[1]):
             e = int(idx[t, j])
             w_e = float(wt[t, j].view(np.float16))
-            tr = [ex["trellis"][p][e] for p in range(3)]
+            Ws = [W(ex["trellis"][p][e], *shapes[p], int(ex["bits"][p][e])) for p in range(3)]
             su = [ex["suh"][p][e].view(np.float16).astype(np.float64) for p in range(3)]
             sv = [ex["svh"][p][e].view(np.float16).astype(np.float64) for p in range(3)]
-            b = [int(ex["bits"][p][e]) for p in range(3)]
-            U = a_in(xd[t], su[1]) @ W(tr[1], hidden, inter, b[1])
-            u = _h16(_h16(had(_h16(U))) * sv[1])
-            if act == "relu2":
-                g = np.maximum(u, 0.0)
-            else:
-                G = a_in(xd[t], su[0]) @ W(tr[0], hidden, inter, b[0])
-                g = _h16(_h16(had(_h16(G))) * sv[0])
-                g = _gelu_erf16(g) if act == "gelu_erf" else _silu16(g)
-            if L:
-                Lh = float(np.float16(L))
-                u = np.clip(u, -Lh, Lh)
-                g = np.minimum(g, Lh)
-            p = _h16(_h16(g * u) * su[2])
-            ad = _h16(had(p))
-            D = _h16(ad @ W(tr[2], inter, hidden, b[2]))
-            c = had(D) * w_e * sv[2]
+            c = expert_contrib_numpy(xd[t], *Ws, su, sv, [w_e], L, act=act)[0]
             y_routed[t] += c.astype(np.float32)   # fp32 accumulation in rank order
     y16 = None
     if sh is not None:
