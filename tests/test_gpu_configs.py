@@ -165,7 +165,7 @@ def test_moe_prefill_config4_every_job(hx, config4):
             Ws.append(O.reconstruct(tr, K, N, ex.bits[p][e], 2).view(np.float16).astype(np.float64))
         su = [_host(ex.suh[p][e]).astype(np.float64) for p in range(3)]
         sv = [_host(ex.svh[p][e]).astype(np.float64) for p in range(3)]
-        tok = ts[pos] // topk
+        tok = ts[pos]  # token_sorted holds token indices
         wt = wsr[pos].view(np.float16).astype(np.float64)
         ref = expert_contrib_numpy(c4["x"][tok], *Ws, su, sv, wt, 10.0)
         return e, pos, ref, contrib[pos]
