@@ -22,6 +22,7 @@ typedef uint32_t hx_u4 __attribute__((ext_vector_type(4)));
 typedef float hx_f16v __attribute__((ext_vector_type(16)));
 
 #define HX_INLINE __device__ __forceinline__
+#define HX_INLINE_HD __host__ __device__ __forceinline__
 
 #ifdef HX_NO_PRIO
 #define HX_SETPRIO(p) do { } while (0)
@@ -34,6 +35,13 @@ static constexpr float HX_RSQRT128 = 0.088388347648f;
 // Workgroup size in threads / waves (kernels here run 256 or 1024 threads).
 HX_INLINE int hx_nthreads() { return (int)blockDim.x; }
 HX_INLINE int hx_nwaves() { return (int)blockDim.x >> 6; }
+
+// Rotated wave / thread index of a 4-wave (256-thread) workgroup: wave (blockIdx.x & 3) acts as wave
+// 0.  The waves of a workgroup sit on the CU's four SIMDs in order, so serial per-workgroup work
+// (routing, bookkeeping, one-row epilogues) given to wave 0 of every co-resident workgroup would
+// all land on one SIMD and run there one workgroup after the other.
+HX_INLINE int hx_vwave() { return (int)(((threadIdx.x >> 6) - blockIdx.x) & 3u); }
+HX_INLINE int hx_vtid() { return (int)((threadIdx.x + 256u - 64u * (blockIdx.x & 3u)) & 255u); }
 
 HX_INLINE hx_h2 u32_as_h2(uint32_t u) { return __builtin_bit_cast(hx_h2, u); }
 HX_INLINE uint32_t h2_as_u32(hx_h2 h) { return __builtin_bit_cast(uint32_t, h); }

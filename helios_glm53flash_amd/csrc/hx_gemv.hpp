@@ -371,8 +371,9 @@ HX_INLINE uint32_t input_transform(uint32_t xv, uint32_t sv, bool pre_transforme
 // for several rows it replaces a wave-wide butterfly per row and block with 32 MFMAs per block.
 // Lane l: A row l % 16, k = 32 kk + 8 (l / 16) + 0..7; C rows 4 (l / 16) + i, column 16 nb + l % 16.
 HX_INLINE void input_mfma(uint32_t* a_lds, const _Float16* x, const int* rows, const _Float16* suh, int M, int K,
-                          int k0, int kc)
+                          int k0, int kc, int ld = -1)
 {
+    if (ld < 0) ld = kc;  // row stride of the LDS rows (fp16)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = lane & 15, g = lane >> 4;
     const int blocks = kc >> 7;
@@ -415,7 +416,7 @@ HX_INLINE void input_mfma(uint32_t* a_lds, const _Float16* x, const int* rows, c
             const int m = 4 * g + i;
             if (m < M) {
 #pragma unroll
-                for (int nb = 0; nb < 8; ++nb) al[m * kc + b * 128 + 16 * nb + c] = (_Float16)(y[nb][i] * HX_RSQRT128);
+                for (int nb = 0; nb < 8; ++nb) al[m * ld + b * 128 + 16 * nb + c] = (_Float16)(y[nb][i] * HX_RSQRT128);
             }
         }
     }

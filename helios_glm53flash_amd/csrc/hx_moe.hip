@@ -16,9 +16,8 @@
 
 namespace hx {
 
-hipError_t launch_moe_decode_m1(const MoeDecodeArgs& a, int cb, int bits, hipStream_t st);
-hipError_t launch_moe_decode_m4(const MoeDecodeArgs& a, int cb, int bits, hipStream_t st);
-hipError_t launch_moe_decode_m8(const MoeDecodeArgs& a, int cb, int bits, hipStream_t st);
+template <int MT>
+hipError_t launch_moe_decode_mt(const MoeDecodeArgs& a, int cb, int bits, hipStream_t st);  // hx_moe_decode_m*.hip
 
 static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -115,12 +114,6 @@ int resident_blocks(const void* kernel, int threads, size_t lds)
 // enforces it in hardware (the runtime's occupancy query is not relied on for the LDS size per CU).
 constexpr size_t DEC_LDS_PER_CU = 160 * 1024;
 
-static int dec_per_cu(int max_per_cu)
-{
-    if (const char* v = getenv("HX_DEC_PER_CU")) return atoi(v) > 0 ? atoi(v) : max_per_cu;  // sweeps
-    return max_per_cu;
-}
-
 static int device_cus()
 {
     static std::mutex mu;
@@ -140,7 +133,7 @@ int decode_resident(const void* kernel, int threads, size_t lds, int max_per_cu)
     const int res = resident_blocks(kernel, threads, lds);
     const int cus = device_cus();
     if (cus <= 0) return res;
-    const int cap = dec_per_cu(max_per_cu) * cus;
+    const int cap = max_per_cu * cus;
     return res < cap ? res : cap;
 }
 
@@ -164,7 +157,7 @@ size_t decode_lds_pad(const void* kernel, size_t lds, int max_per_cu)
             cache.push_back({kernel, stat});
         }
     }
-    const size_t total = DEC_LDS_PER_CU / (size_t)(dec_per_cu(max_per_cu) + 1) + 1024;
+    const size_t total = DEC_LDS_PER_CU / (size_t)(max_per_cu + 1) + 1024;
     const size_t dyn = total > stat ? total - stat : 0;
     return lds > dyn ? lds : dyn;
 }
@@ -181,8 +174,7 @@ size_t decode_lds_pad(const void* kernel, size_t lds, int max_per_cu)
 // (With the earlier ring, whose waits drained every load in flight once per group, 864 + 864 was
 // the faster one.)
 // A fused variant (workgroup w runs gate/up unit w then down unit w, reusing its plan) took 60 us.
-// HX_MOE_UNITS="g,d" sets the two counts as fractions of the resident count (tuning).  Returns the
-// longest unit's k extent.
+// Returns the longest unit's k extent.
 int decode_units(MoeDecodeArgs& a, int resident)
 {
     const long slots = a.routed_slots + 1;
@@ -190,12 +182,6 @@ int decode_units(MoeDecodeArgs& a, int resident)
     const long cg_d = slots * (a.hidden / 128), kb_d = a.inter / 128;
     auto clampu = [](long u, long c, long kb) { return u < c ? c : (u > c * kb ? c * kb : u); };
     long ug = clampu(resident, cg_gu, kb_gu), ud = clampu(resident - resident / 16, cg_d, kb_d);
-    if (const char* v = getenv("HX_MOE_UNITS")) {  // fractions of the resident count, for sweeps
-        double fg = 1.0, fd = 1.0;
-        sscanf(v, "%lf,%lf", &fg, &fd);
-        ug = clampu((long)(resident * fg), cg_gu, kb_gu);
-        ud = clampu((long)(resident * fd), cg_d, kb_d);
-    }
     a.units_gu = (int)ug;
     a.units_d = (int)ud;
     const long bg = (kb_gu + ug / cg_gu - 1) / (ug / cg_gu), bd = (kb_d + ud / cg_d - 1) / (ud / cg_d);
@@ -215,9 +201,9 @@ hipError_t run_moe_decode(MoeDecodeArgs& a, int cb, uint32_t bits_mask, hipStrea
     // units skip their stream) -> per-unit dispatch
     const bool one = (bits_mask & (bits_mask - 1)) == 0 && a.act_fn != HX_ACT_RELU2_NOGATE;
     const int bits = one ? __builtin_ctz(bits_mask) : 0;
-    if (a.T <= 1) return launch_moe_decode_m1(a, cb, bits, st);
-    if (a.T <= 4) return launch_moe_decode_m4(a, cb, bits, st);
-    return launch_moe_decode_m8(a, cb, bits, st);
+    if (a.T <= 1) return launch_moe_decode_mt<1>(a, cb, bits, st);
+    if (a.T <= 4) return launch_moe_decode_mt<4>(a, cb, bits, st);
+    return launch_moe_decode_mt<8>(a, cb, bits, st);
 }
 
 }  // namespace hx

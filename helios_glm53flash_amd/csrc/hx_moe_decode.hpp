@@ -18,14 +18,6 @@
 #pragma once
 #include "hx_gemv.hpp"
 
-// Table entries of every expert loaded with the scores (1) or the slot's entries after the ranking (0).
-#ifndef HX_DEC_PFTAB
-#define HX_DEC_PFTAB 1
-#endif
-// ... and the epilogue tables of every expert with the scores (1), or the slot's after the plan (0).
-#ifndef HX_DEC_PFEP
-#define HX_DEC_PFEP 1
-#endif
 
 namespace hx {
 
@@ -325,7 +317,7 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
     __shared__ float sel_w[DEC_MAX_R];
     constexpr int TAB_MAX_E = 320, TPL = TAB_MAX_E / 64;
     __shared__ uint64_t tab_lds[DEC_TABS][TAB_MAX_E];  // table entries of every expert
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = hx_vwave(), lane = threadIdx.x & 63;
     const int R = a.T * a.topk;
     if (a.scores) {
         // The slot's table entries would be one more dependent load after the ranking.  Instead
@@ -333,7 +325,7 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
         // loads trellis and suh (parked after its selection, which then waits for the scores only,
         // as loads complete in order), wave 1 the epilogue tables.  The owning lane of the slot's
         // expert takes trellis and suh after the ranking, thread 0 the rest after the plan barrier.
-        const bool pf_tab = my_slot >= 0 && HX_DEC_PFTAB && a.E <= TAB_MAX_E;
+        const bool pf_tab = my_slot >= 0 && a.E <= TAB_MAX_E;
         auto load_tabs = [&](int q0, int q1, uint64_t (*v)[TPL]) {
 #pragma unroll
             for (int q = q0; q < q1; ++q) {
@@ -352,7 +344,7 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
         auto prefetch = [&]() {
             if (pf_tab && wave == 0) load_tabs(0, 2, v_main);
         };
-        if (pf_tab && HX_DEC_PFEP && wave == 1) {
+        if (pf_tab && wave == 1) {
             uint64_t v_ep[DEC_TABS - 2][TPL];
             load_tabs(2, DEC_TABS, v_ep);
             park_tabs(2, DEC_TABS, v_ep);
@@ -473,16 +465,11 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
     }
     __syncthreads();
     // the slot's epilogue tables (the epilogues read them after later barriers)
-    if (a.scores && threadIdx.x == 0 && my_slot >= 0 && my_slot < p.n && HX_DEC_PFTAB && a.E <= TAB_MAX_E) {
+    if (a.scores && hx_vtid() == 0 && my_slot >= 0 && my_slot < p.n && a.E <= TAB_MAX_E) {
         const int e = p.expert[my_slot];
 #pragma unroll
         for (int q = 2; q < DEC_TABS; ++q) {
-            if constexpr (HX_DEC_PFEP) {
-                set_tab(p.tab, q, bits_ptr(tab_lds[q][e]));
-            } else {
-                const void* const* b = tab_base(a, q, proj);
-                set_tab(p.tab, q, b ? b[e] : nullptr);
-            }
+            set_tab(p.tab, q, bits_ptr(tab_lds[q][e]));
         }
     }
 }
@@ -518,7 +505,7 @@ template <int MT>
 __device__ __forceinline__ void guad_epilogue(const MoeDecodeArgs& a, const DecodePlan& p, const SlotInfo& si, int slot,
                                               int cg, const float* cs_g, const float* cs_u)
 {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = hx_vwave(), lane = threadIdx.x & 63;
     const int c = cg * 128 + 2 * lane;
     const bool shared = si.expert < 0;
     // (the gate's svh of a non-gated expert need not exist)
@@ -582,7 +569,7 @@ template <int MT>
 __device__ __forceinline__ void down_epilogue(const MoeDecodeArgs& a, const DecodePlan& p, const SlotInfo& si, int cg,
                               const float* cs)
 {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = hx_vwave(), lane = threadIdx.x & 63;
     const int c = cg * 128 + 2 * lane;
     const bool shared = si.expert < 0;
     const hx_h2 sd = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(p.tab.ep[0]) + c);
@@ -661,25 +648,16 @@ __device__ __forceinline__ void combine_columns(const MoeDecodeArgs& a, const De
 // projection's HBM latency overlaps the end of the gate/up phase.  Units of slots beyond the
 // active ones (fewer distinct experts than routed rows) return at once.
 
-// Workgroup shape: 4 * DEC_KS waves.  With DEC_KS > 1 the DEC_KS wave groups split each
-// segment's 128-k blocks (block j of the segment goes to group j % DEC_KS) and add their sums in
-// group order through LDS.  Measured on MI355X (config-3 layer, 1 token): 4 waves x 4 workgroups
-// per CU 73 us, 8 x 2 76 us, 16 x 1 83 us -- fewer, larger workgroups wait longer at their
-// barriers than they save in segment handoffs.
-#ifndef HX_DEC_KS
-#define HX_DEC_KS 1
-#endif
-constexpr int DEC_KS = HX_DEC_KS;
+// Workgroup shape: 4 waves.  (Measured on MI355X, config-3 layer, 1 token, with an earlier unit
+// scheme: 4 waves x 4 workgroups per CU 73 us, 8 x 2 76 us, 16 x 1 83 us -- fewer, larger workgroups
+// wait longer at their barriers than they save in handoffs.)
 // Tile-word steps in flight per wave in the layer kernel (up to 4 bits).  Every resident unit's ring
 // is in flight at once, and the queue that builds up in the memory system delays each unit's own
 // dependent loads (scores, inputs, flags, partial sums): measured at config 3 (layer time), 8 steps
 // 51.1 us, 6 steps 49.8 us, 5 steps 49.6 us, 4 steps 49.4 us, 3 steps 50.5 us, 2 steps 51.7 us.
 // (The linear GEMV keeps its own ring depth: it streams alone.)
-#ifndef HX_DEC_PF
-#define HX_DEC_PF 4
-#endif
-constexpr int DEC_PF = HX_DEC_PF;
-constexpr int DEC_THREADS = 256 * DEC_KS;
+constexpr int DEC_PF = 4;
+constexpr int DEC_THREADS = 256;
 
 // Bounded wait of thread 0 for *flag >= target (the producers are resident workgroups that do not
 // wait for anything themselves, so the wait ends; the bound only turns a bug into a flagged wrong
@@ -762,7 +740,7 @@ __device__ __forceinline__ void gu_finish(const MoeDecodeArgs& a, const DecodePl
     // the activations of this block are stored (device-coherent): flag them for the down phase
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_store(&a.ready[slot * gg + cg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (hx_vtid() == 0) __hip_atomic_store(&a.ready[slot * gg + cg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Streams gate/up unit (c, j) and publishes its partial sum (gu_finish follows).
@@ -788,7 +766,7 @@ __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodeP
     g.K = a.hidden;
     g.N = a.inter;
     g.pre_transformed = false;
-    gemv_range<BITS, CB, MT, DEC_KS, DEC_PF>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
+    gemv_range<BITS, CB, MT, 1, DEC_PF>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
 
     // partial of segment i of (slot, proj, cg): partial_{g,u}[((slot*gg + cg) * (KB + 1) + i) * 8 + m][128]
     float* pbase = (proj == 0 ? a.partial_g : a.partial_u) + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
@@ -816,11 +794,11 @@ __device__ __forceinline__ void d_segment(const MoeDecodeArgs& a, const DecodePl
     g.pre_transformed = true;
     // the input blocks kb0..kb1-1 of this slot are the guad outputs of gate/up column groups kb0..kb1-1
     auto wait_inputs = [&]() {
-        if (threadIdx.x == 0)
+        if (hx_vtid() == 0)
             for (int kb = kb0; kb < kb1; ++kb) wait_flag(&a.ready[slot * gg + kb], 1, a.status);
         hx_lds_barrier();
     };
-    gemv_range<BITS, CB, MT, DEC_KS, DEC_PF>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs, wait_inputs);
+    gemv_range<BITS, CB, MT, 1, DEC_PF>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs, wait_inputs);
 }
 
 // Split-K handoff of a down unit: publish, arrive; the last unit of the column group runs the down
@@ -915,7 +893,7 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
     const int proj = gu ? (c / gg) & 1 : 2;       // the projection this unit streams
     if (gu && shared_unit && !(w == 0 && a.out_idx)) {
         // the shared expert's gate/up needs no routing: its tables are arguments, its rows every token
-        if (threadIdx.x == 0) {
+        if (hx_vtid() == 0) {
             plan.n = 0;
             load_slot_tables(a, plan.tab, -1, proj);
         }
@@ -941,22 +919,22 @@ __device__ __forceinline__ void moe_decode_body(const MoeDecodeArgs& a)
     run_unit<BITS, CB, MT>(a, plan, sp, gu, c, j, a_lds, cs_g, cs_u, rows);
     // the last workgroup to finish clears the activation flags for the next call
     __shared__ bool last;
-    if (threadIdx.x == 0)
+    if (hx_vtid() == 0)
         last = __hip_atomic_fetch_add(a.exit_count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
     __syncthreads();
     if (last) {
         for (int i = threadIdx.x; i < (a.routed_slots + 1) * gg; i += hx_nthreads())
             __hip_atomic_store(&a.ready[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (threadIdx.x == 0) __hip_atomic_store(a.exit_count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (hx_vtid() == 0) __hip_atomic_store(a.exit_count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-// Fixed bit width: at most 128 VGPRs so that 16 waves (4 / DEC_KS workgroups) share a CU, and
+// Fixed bit width: at most 128 VGPRs so that 16 waves (4 workgroups) share a CU, and
 // exactly that occupancy as the scheduling target (4 waves per SIMD).  Without the upper bound the
 // compiler trades the streaming loop's latency hiding for registers to reach 6 waves per SIMD,
 // which the launch never uses (measured 58 against 51 us at config 3).
 template <int BITS, int CB, int MT>
-__global__ __launch_bounds__(DEC_THREADS, 4 / DEC_KS) __attribute__((amdgpu_waves_per_eu(4, 4)))
+__global__ __launch_bounds__(DEC_THREADS, 4) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void moe_decode_kernel(MoeDecodeArgs a)
 {
     moe_decode_body<BITS, CB, MT>(a);
