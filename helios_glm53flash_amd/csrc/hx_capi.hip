@@ -365,6 +365,29 @@ int hx_routing_ds3_nogroup(const void* scores, const void* bias, int64_t* topk_i
                       "hx_routing_ds3_nogroup");
 }
 
+int hx_routing_gemv(const void* x, const void* gate_t, void* scores, int k, int E, hx_stream_t stream)
+{
+    if (!x || !gate_t || !scores || k <= 0 || E < 1 || (k & 1))
+        return fail(HX_ERR_INVALID, "hx_routing_gemv: bad arguments (k must be even)");
+    if (k % 32) return fail(HX_ERR_UNSUPPORTED, "hx_routing_gemv: k must be a multiple of 32 here");
+    return hip_status(hx::launch_gemm_nt_f16(static_cast<const _Float16*>(x), static_cast<const _Float16*>(gate_t),
+                                             scores, 1, E, k, false, false, (hipStream_t)stream),
+                      "hx_routing_gemv");
+}
+
+int hx_routing_ds3_nogroup_hidden(const void* hidden, const void* gate_t, void* scores, const void* bias,
+                                  int64_t* topk_indices, void* topk_weights, int k, int num_experts, int K,
+                                  float scaling_factor, int act_fn, hx_stream_t stream)
+{
+    if (act_fn != 0 && act_fn != 1)
+        return fail(HX_ERR_UNSUPPORTED, "hx_routing_ds3_nogroup_hidden: act_fn must be 0 (sigmoid) or 1 (sqrt-softplus)");
+    if (!topk_indices || !topk_weights || num_experts > 512 || K < 1 || K > 64 || K > num_experts)
+        return fail(HX_ERR_INVALID, "hx_routing_ds3_nogroup_hidden: bad arguments");
+    if (int r = hx_routing_gemv(hidden, gate_t, scores, k, num_experts, stream)) return r;
+    return hx_routing_ds3_nogroup(scores, bias, topk_indices, topk_weights, 1, num_experts, K, scaling_factor, 1,
+                                  act_fn, stream);
+}
+
 int hx_moe_permute(const int64_t* ids, const void* weights, int M, int topk, int E, int64_t* expert_count,
                    int64_t* token_sorted, void* weight_sorted, int64_t* workspace, hx_stream_t stream,
                    int64_t* route_to_sorted)

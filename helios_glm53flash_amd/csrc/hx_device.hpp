@@ -24,11 +24,7 @@ typedef float hx_f16v __attribute__((ext_vector_type(16)));
 #define HX_INLINE __device__ __forceinline__
 #define HX_INLINE_HD __host__ __device__ __forceinline__
 
-#ifdef HX_NO_PRIO
-#define HX_SETPRIO(p) do { } while (0)
-#else
 #define HX_SETPRIO(p) __builtin_amdgcn_s_setprio(p)
-#endif
 
 static constexpr float HX_RSQRT128 = 0.088388347648f;
 

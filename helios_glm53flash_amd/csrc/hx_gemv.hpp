@@ -27,12 +27,8 @@ namespace hx {
 // flight shorten the memory queue that every workgroup's dependent loads (inputs, partial sums,
 // arrival counters) wait behind: config 2 (4096 -> 12288, 4-bit) at M = 1 measured 15.6 us with
 // 8 steps, 13.9 with 4, 13.4 with 2; the 5-bit lm_head is flat between 2 and 4.
-#ifndef HX_LIN_PF
-#define HX_LIN_PF 2
-#endif
-#ifndef HX_LIN_PFW
-#define HX_LIN_PFW 4
-#endif
+constexpr int LIN_PF = 2;   // up to 4 bits
+constexpr int LIN_PFW = 4;  // wider
 
 constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_WAVES = 4;
@@ -651,7 +647,7 @@ __device__ __forceinline__ void gemv_split_sum(const GemvArgs& g, int cg, int s,
                                                Before before_input = Before(), After after_input = After())
 {
     const int k0 = s * g.kc;
-    gemv_range<BITS, CB, MT, 1, HX_LIN_PF, HX_LIN_PFW>(g, cg, k0, min(g.kc, g.K - k0), a_lds, colsum, before_input,
+    gemv_range<BITS, CB, MT, 1, LIN_PF, LIN_PFW>(g, cg, k0, min(g.kc, g.K - k0), a_lds, colsum, before_input,
                                                    after_input);
 }
 

@@ -22,12 +22,9 @@ void gemv_plan(int M, int K, int N, int bits, int* splits, int* kc)
 {
     (void)bits;
     const int groups = N / 128;
-    int cap = 16384 / (M < 1 ? 1 : M);
-    if (const char* v = getenv("HX_GEMV_KC")) cap = atoi(v) > 0 ? atoi(v) : cap;  // sweeps
+    const int cap = 16384 / (M < 1 ? 1 : M);
     int c = gemv_kc_for(K, cap);
-    int min_wg = 512, floor_kc = GEMV_KC_FLOOR;
-    if (const char* v = getenv("HX_GEMV_MINWG")) min_wg = atoi(v) > 0 ? atoi(v) : min_wg;  // sweeps
-    if (const char* v = getenv("HX_GEMV_KC_FLOOR")) floor_kc = atoi(v) > 0 ? atoi(v) : floor_kc;
+    const int min_wg = 512, floor_kc = GEMV_KC_FLOOR;
     while (c > 128 && c > floor_kc && (long)groups * (K / c) < min_wg) {
         // one shrink step can skip past the floor when K has no multiple-of-128 divisor in
         // [floor_kc, c) (K = 1152: 1152 -> 384): stop at c then

@@ -763,10 +763,7 @@ hipError_t run_moe_prefill(const PrefillArgs& p, float* contrib, const float* sh
     if (!p.r2s) return hipErrorInvalidValue;
     if (p.topk > 64) return hipErrorInvalidValue;
     if (p.T > 0 && (p.topk == 1 || p.topk == 2 || p.topk == 4 || p.topk == 8 || p.topk == 16)) {
-#ifndef HX_CMB_KBC
-#define HX_CMB_KBC 4
-#endif
-        constexpr int KBC = HX_CMB_KBC;  // 128-column blocks per wave (the route lookups are paid once for them)
+        constexpr int KBC = 4;  // 128-column blocks per wave (the route lookups are paid once for them)
         const long units = ((long)p.T * p.topk + 15) / 16 * ((p.hidden / 128 + KBC - 1) / KBC);
         const dim3 grid((unsigned)((units + 3) / 4));
 #define HX_CMB(K)                                                                                             \

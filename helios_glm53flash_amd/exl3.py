@@ -212,6 +212,30 @@ def had_r_128_dual(input1: torch.Tensor, output1: torch.Tensor, pre_scale1, post
                                 cols, dt, scale, _stream(stream)), "hx_had_r_128_dual")
 
 
+def routing_gemv(x: torch.Tensor, gate_t: torch.Tensor, scores: torch.Tensor, k: int, num_experts: int,
+                 stream=None) -> None:
+    """Single-token router GEMV scores = x @ gate_t.T (reference routing.cuh:19-29)."""
+    _need(x, "x", (torch.float16,))
+    _need(gate_t, "gate_t", (torch.float16,))
+    _need(scores, "scores", (torch.float16,))
+    check(lib.hx_routing_gemv(x.data_ptr(), gate_t.data_ptr(), scores.data_ptr(), k, num_experts, _stream(stream)),
+          "hx_routing_gemv")
+
+
+def routing_ds3_nogroup_hidden(hidden: torch.Tensor, gate_t: torch.Tensor, scores: torch.Tensor,
+                               bias: Optional[torch.Tensor], topk_indices: torch.Tensor, topk_weights: torch.Tensor,
+                               k: int, num_experts: int, K: int, scaling_factor: float, act_fn: int = 0,
+                               stream=None) -> None:
+    """Decode fast path: router GEMV into the scratch `scores`, then top-k (reference routing.cuh:51-66)."""
+    _need(hidden, "hidden", (torch.float16,))
+    _need(topk_indices, "topk_indices", (torch.int64,))
+    _need(topk_weights, "topk_weights", (torch.float16,))
+    check(lib.hx_routing_ds3_nogroup_hidden(hidden.data_ptr(), gate_t.data_ptr(), scores.data_ptr(), _ptr(bias),
+                                            topk_indices.data_ptr(), topk_weights.data_ptr(), k, num_experts, K,
+                                            scaling_factor, act_fn, _stream(stream)),
+          "hx_routing_ds3_nogroup_hidden")
+
+
 def routing_ds3_nogroup(scores: torch.Tensor, bias: Optional[torch.Tensor], topk_indices: torch.Tensor,
                         topk_weights: torch.Tensor, bsz: int, num_experts: int, K: int, scaling_factor: float,
                         use_topk: bool = True, act_fn: int = 0, stream=None) -> None:
@@ -289,6 +313,6 @@ def gemm_nt_f16(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor, M: int, N: in
                              _stream(stream)), "hx_gemm_nt_f16")
 
 
-__all__ = ["GroupWords", "gemm", "gemm_nt_f16", "reconstruct_had_slice", "pack_trellis", "unpack_trellis", "gemv", "reconstruct", "reconstruct_slice", "had_r_128", "had_r_128_dual", "routing_ds3_nogroup",
+__all__ = ["GroupWords", "gemm", "gemm_nt_f16", "reconstruct_had_slice", "pack_trellis", "unpack_trellis", "gemv", "reconstruct", "reconstruct_slice", "had_r_128", "had_r_128_dual", "routing_gemv", "routing_ds3_nogroup_hidden", "routing_ds3_nogroup",
            "moe_permute", "moe_reduce_sorted", "swiglu_clamp", "workspace", "MUL1", "HxError",
            "HX_GEMM_PATH_GEMV", "HX_GEMM_PATH_MFMA"]

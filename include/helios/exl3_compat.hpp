@@ -273,6 +273,25 @@ inline void routing_ds3_nogroup(const void* scores, const void* bias, int64_t* t
                                        use_topk, act_fn, (hx_stream_t)s),
                 "helios::aux::routing_ds3_nogroup");
 }
+
+// reference: src/cuda/aux/routing.cuh:9-17
+enum RoutingAct : int { ROUTING_ACT_SIGMOID = 0, ROUTING_ACT_SQRTSP = 1 };
+
+// reference: src/cuda/aux/routing.cuh:19-29
+inline void routing_gemv(const void* x, const void* gate_t, void* scores, int k, int E, Stream s = 0)
+{
+    exl3::check(hx_routing_gemv(x, gate_t, scores, k, E, (hx_stream_t)s), "helios::aux::routing_gemv");
+}
+
+// reference: src/cuda/aux/routing.cuh:51-66
+inline void routing_ds3_nogroup_hidden(const void* hidden, const void* gate_t, void* scores, const void* bias,
+                                       int64_t* topk_indices, void* topk_weights, int k, int num_experts, int K,
+                                       float scaling_factor, int act_fn = ROUTING_ACT_SIGMOID, Stream s = 0)
+{
+    exl3::check(hx_routing_ds3_nogroup_hidden(hidden, gate_t, scores, bias, topk_indices, topk_weights, k, num_experts,
+                                              K, scaling_factor, act_fn, (hx_stream_t)s),
+                "helios::aux::routing_ds3_nogroup_hidden");
+}
 }  // namespace aux
 
 namespace glue {

@@ -165,6 +165,18 @@ int hx_routing_ds3_nogroup(const void* scores, const void* bias, int64_t* topk_i
                            int bsz, int num_experts, int K, float scaling_factor, int use_topk, int act_fn,
                            hx_stream_t stream);
 
+/* Single-token router GEMV: scores[e] = fp16(sum_j x[j] * gate_t[e][j]) (fp32 accumulate), gate_t
+ * (E, k) row-major; k even, and a multiple of 32 here (HX_ERR_UNSUPPORTED otherwise).
+ * Replaces helios::aux::routing_gemv (src/cuda/aux/routing.cuh:19-29, routing.cu:148-204). */
+int hx_routing_gemv(const void* x, const void* gate_t, void* scores, int k, int E, hx_stream_t stream);
+
+/* Decode fast path (one token): scores = hidden . gate_t^T into the scratch `scores`, then the top-k
+ * variant of hx_routing_ds3_nogroup.  Replaces helios::aux::routing_ds3_nogroup_hidden
+ * (src/cuda/aux/routing.cuh:51-66, routing.cu:547-567). */
+int hx_routing_ds3_nogroup_hidden(const void* hidden, const void* gate_t, void* scores, const void* bias,
+                                  int64_t* topk_indices, void* topk_weights, int k, int num_experts, int K,
+                                  float scaling_factor, int act_fn, hx_stream_t stream);
+
 /* Token-by-expert permutation: expert_count int64 [E+1], token_sorted int64 [M*topk],
  * weight_sorted fp16 [M*topk], route_to_sorted int64 [M*topk] (optional).  Within an expert the
  * order is ascending flat routing index (deterministic; the reference uses an atomic cursor).

@@ -70,6 +70,8 @@ def test_cpp_compat_header_compiles_and_links(tmp_path):
                    "    helios::glue::gemm_nt_f16(nullptr, nullptr, nullptr, 1, 288, 4096, false, false);\n"
                    "    helios::exl3::pack_trellis(nullptr, nullptr, 1, 1, 2);\n"
                    "    (void)helios::exl3::moe_max_concurrency(0);\n"
+                   "    helios::aux::routing_ds3_nogroup_hidden(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 4096, 288, 8, 2.5f,"
+                   " helios::aux::ROUTING_ACT_SIGMOID);\n"
                    "    helios::exl3::had_r_128(nullptr, nullptr, nullptr, nullptr, 1, 128, helios::exl3::DType::Half, 1.0f);\n"
                    "    helios::exl3::had_r_128_dual(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1, 128,"
                    " helios::exl3::DType::Float, 1.0f, nullptr);\n"

@@ -80,3 +80,38 @@ def test_layer_with_router_weight(torch_mod, T):
     y2 = layer(x, scores)
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
+
+
+@pytest.mark.parametrize("bias,act", [(False, 0), (True, 0), (False, 1)])
+def test_routing_ds3_nogroup_hidden(torch_mod, bias, act):
+    """Decode fast path (routing.cuh:51-66): the router GEMV (routing_gemv) within one fp16 spacing of
+    the fp64 dot products plus fp32 noise, and the top-k indices bit-exact against the oracle's
+    routing of the GEMV's own scores (weights within one fp16 ulp), at E = 288, K = 8, k = 4096."""
+    torch = torch_mod
+    from helios_glm53flash_amd import exl3
+    from oracle import oracle as O
+    E, k, K = 288, 4096, 8
+    r = np.random.default_rng(91 + 7 * act + bias)
+    x = r.standard_normal(k).astype(np.float16)
+    gate = (r.standard_normal((E, k)) * 0.02).astype(np.float16)
+    b = (r.standard_normal(E) * 0.05).astype(np.float16) if bias else None
+    scores = torch.empty(E, dtype=torch.float16, device="cuda")
+    idx = torch.empty(K, dtype=torch.int64, device="cuda")
+    w = torch.empty(K, dtype=torch.float16, device="cuda")
+    exl3.routing_ds3_nogroup_hidden(torch.from_numpy(x).cuda(), torch.from_numpy(gate).cuda(), scores,
+                                    torch.from_numpy(b).cuda() if bias else None, idx, w, k, E, K, 2.5, act)
+    torch.cuda.synchronize()
+    ref64 = gate.astype(np.float64) @ x.astype(np.float64)
+    got = scores.cpu().numpy()
+    mag = np.abs(gate.astype(np.float64)) @ np.abs(x.astype(np.float64))
+    spacing = np.spacing(np.abs(ref64).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(got.astype(np.float64) - ref64) <= spacing + 2.0 ** -20 * mag)
+    ridx, rw = O.routing(got[None, :], K, 2.5, b, True, act)
+    assert np.array_equal(idx.cpu().numpy(), ridx[0])
+    dw = np.abs(w.cpu().numpy().astype(np.float64) - rw[0].view(np.float16).astype(np.float64))
+    assert dw.max() <= 2.0 ** -9 * 2.5
+    # routing_gemv alone writes the same scores
+    s2 = torch.empty(E, dtype=torch.float16, device="cuda")
+    exl3.routing_gemv(torch.from_numpy(x).cuda(), torch.from_numpy(gate).cuda(), s2, k, E)
+    torch.cuda.synchronize()
+    assert torch.equal(s2, scores)

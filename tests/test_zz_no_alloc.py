@@ -56,3 +56,51 @@ def test_noalloc_rejects_oversize(hx):
     y = torch.empty((M, N), dtype=torch.float32, device="cuda")
     with pytest.raises(HxError, match="scratch"):
         hx.gemm_noalloc(y, x, w, M, N, K, 2, True)
+
+
+_CAPTURE_SCRIPT = r"""
+import sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + "/tests")
+from helios_glm53flash_amd import exl3
+from helpers import make_linear, make_x
+M, K, N, bits = 1, 4096, 2048, 2
+tr, suh, svh = make_linear(90, K, N, bits)
+dev = lambda a, dt=None: (torch.from_numpy(np.ascontiguousarray(a)).view(dt) if dt else torch.from_numpy(np.ascontiguousarray(a))).cuda()
+w = exl3.GroupWords(dev(tr, torch.int16), dev(suh), dev(svh), exl3.MUL1)
+x = dev(make_x(91, M, K))
+y_g = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+s = torch.cuda.Stream()
+with torch.cuda.graph(g, stream=s):
+    # the process's first no-alloc call: the per-device scratch lookup happens inside the capture
+    exl3.gemm_noalloc(y_g, x, w, M, N, K, bits, True, stream=s)
+y_ws = torch.empty((M, N), dtype=torch.float32, device="cuda")
+exl3.gemm(y_ws, x, w, M, N, K, bits, True)
+torch.cuda.synchronize()
+for rep in range(3):
+    y_g.fill_(float("nan"))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y_g, y_ws), rep
+    exl3.gemm(y_ws, x, w, M, N, K, bits, True)  # eager work between replays
+    torch.cuda.synchronize()
+print("ok")
+"""
+
+
+def test_noalloc_first_call_under_graph_capture(hx, tmp_path):
+    """The first no-alloc call of a fresh process made inside a HIP graph capture (the per-device
+    scratch lookup then runs while the stream captures); three replays, with eager calls between
+    them, equal the workspace path bit for bit."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parent.parent
+    script = tmp_path / "capture.py"
+    script.write_text(_CAPTURE_SCRIPT)
+    r = subprocess.run([sys.executable, str(script), str(root)], capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0 and "ok" in r.stdout, (r.stdout[-1500:], r.stderr[-3000:])
