@@ -23,9 +23,7 @@ constexpr int MF_THREADS = 256;
 constexpr int MF_BM = 128;  // largest row tile
 constexpr int MF_BN = 128;
 constexpr int MF_BK = 64;
-#ifndef HX_MF_SWZ
-#define HX_MF_SWZ 2
-#endif
+constexpr int MF_SWZ = 2;  // LDS swizzle of the A operand rows (below)
 // Operand rows of a chunk in LDS (64 halves of k each, 128-byte rows).  Swizzled layout: 16-byte chunk
 // c of row r is stored at chunk c ^ f(r), f(r) = (r & 7) ^ ((r >> 3) & 1).  The fragment reads (16
 // consecutive rows, one chunk) then touch 8 different 16-byte bank groups in every aligned group of
@@ -33,15 +31,15 @@ constexpr int MF_BK = 64;
 // whether the LDS serves 8 or 16 lanes of a 16-byte access per cycle; a row's 8 chunk stores are
 // conflict-free in any case.  (SWZ 1, f(r) = ((r >> 1) & 7) ^ (((r >> 4) & 1) << 2), suits only the
 // 16-lane case and measured 1.3 % slower in the config-4 prefill; SWZ 0 pads rows to 72 halves.)
-constexpr int MF_LDA = HX_MF_SWZ ? MF_BK : MF_BK + 8;  // halves per LDS row
+constexpr int MF_LDA = MF_SWZ ? MF_BK : MF_BK + 8;  // halves per LDS row
 constexpr int MF_LDC = MF_BN + 4;  // floats per LDS row in the epilogue
 
 // Chunk permutation of LDS row r (an XOR, so it is its own inverse: slot c of row r holds chunk
 // c ^ mf_swz(r)).
 HX_INLINE int mf_swz(int r)
 {
-    if constexpr (HX_MF_SWZ == 2) return (r & 7) ^ ((r >> 3) & 1);
-    else if constexpr (HX_MF_SWZ) return ((r >> 1) & 7) ^ (((r >> 4) & 1) << 2);
+    if constexpr (MF_SWZ == 2) return (r & 7) ^ ((r >> 3) & 1);
+    else if constexpr (MF_SWZ) return ((r >> 1) & 7) ^ (((r >> 4) & 1) << 2);
     else return 0;
 }
 
@@ -77,24 +75,13 @@ HX_INLINE void qt_rowcol(int rb, int nh, int i, int& row, int& col)
 
 // Chunks of global loads in flight for the quarter-operand tile (2 keeps it at 3 workgroups per CU):
 // A chunks (QT_PF) and trellis-word chunks (QT_PT).
-#ifndef HX_QT_PF
-#define HX_QT_PF 2
-#endif
-#ifndef HX_QT_PT
-#define HX_QT_PT 2
-#endif
-// 1: the next chunk's decode sliced between the row blocks' MFMAs (one wave overlaps its own VALU and
-// matrix work); 0: decode after the chunk's MFMAs.  Measured equal on the config-4 prefill (3.14 ms
-// either way; the co-resident waves of a SIMD already overlap the two), so the simpler schedule.
-#ifndef HX_QT_IL
-#define HX_QT_IL 0
-#endif
+constexpr int QT_PF = 2;
+constexpr int QT_PT = 2;
+// The next chunk's decode runs after the chunk's MFMAs.  (Slicing it between the row blocks' MFMAs,
+// so that one wave overlaps its own VALU and matrix work, measured equal on the config-4 prefill:
+// 3.14 ms either way; the co-resident waves of a SIMD already overlap the two.)
 // workgroups per CU the MFMA-tile kernels are compiled for (their register budget)
-#ifndef HX_QT_OCC
-#define HX_QT_OCC 3
-#endif
-constexpr int QT_PF = HX_QT_PF;
-constexpr int QT_PT = HX_QT_PT;
+constexpr int QT_OCC = 3;
 // LDS A buffers: with A loaded straight into LDS, the chunks in flight and the one being read
 constexpr int QT_NB = QT_PF + 1;
 // s_waitcnt immediate that waits until at most n vector-memory instructions are outstanding
@@ -102,9 +89,6 @@ constexpr int QT_NB = QT_PF + 1;
 constexpr int qt_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 // 1: A by buffer loads that write LDS directly wherever the tile does not sum A's rows itself (those
 // read A in registers); 0: always through registers and ds_write (measured 2 % slower, 32 more VGPRs)
-#ifndef HX_QT_DMA
-#define HX_QT_DMA 1
-#endif
 constexpr int qt_lcm(int a, int b)
 {
     int x = a, y = b;
@@ -127,16 +111,13 @@ struct MfmaSmemQ {
 // that XCD's L2 for what they all read, while the groups still go round the XCDs in order (whole
 // rounds of 8 groups; the rest as issued), so every XCD gets the same mix of groups.  Returns false
 // for ids past the ngroups * nx real workgroups.
-#ifndef HX_XCD_REMAP
-#define HX_XCD_REMAP 1
-#endif
 HX_INLINE bool xcd_group_index(int i, int nx, int ngroups, int& member, int& group)
 {
     const int total = ngroups * nx;
     if (i >= total) return false;
     int l = i;
     constexpr int NXCD = 8;
-    if (HX_XCD_REMAP && i < ngroups / NXCD * NXCD * nx) {
+    if (i < ngroups / NXCD * NXCD * nx) {
         const int x = i % NXCD, k = i / NXCD;  // k-th workgroup on XCD x: group x + 8 (k / nx)
         l = ((k / nx) * NXCD + x) * nx + k % nx;
     }
@@ -178,7 +159,7 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
     // PT chunks of trellis words (BITS + 1 VGPRs per chunk)
     constexpr int PT = QT_PT;
     // A through LDS by DMA, unless the tile sums A's rows itself (that reads A in registers)
-    constexpr bool DMA = HX_QT_DMA && (EXT_RS || CB != 2);
+    constexpr bool DMA = EXT_RS || CB != 2;
     static_assert(!DMA || (MF_LDA == MF_BK && PF + 1 <= QT_NB), "A ring in LDS");
     hx_u4v av[DMA ? 1 : PF][NA];
     uint32_t wv[PT][BITS + 1];
@@ -264,10 +245,9 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
     // chunk 0: the prologue issued at most the other chunks' loads after it
     if constexpr (DMA) __builtin_amdgcn_s_waitcnt(qt_vmcnt((PF - 1) * NA + (PT - 1) * NT));
     else store_a(0, 0, true);
-    // d[c & 1] holds the decoded quarter of chunk c; the next chunk's quarter is decoded into the
-    // other half while the matrix cores work on this one, interleaved with the MFMAs in one block
-    // (with the decode after the chunk's MFMAs one buffer serves: the B operands are read first)
-    constexpr int ND = HX_QT_IL ? 2 : 1;
+    // d holds the decoded quarter of the current chunk; the next chunk's quarter is decoded into it
+    // after the chunk's MFMAs (their B operands are read before the decode overwrites it)
+    constexpr int ND = 1;
     uint32_t d[ND][16];
     decode(0, d[0]);
     hx_lds_barrier();
@@ -298,30 +278,9 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
             read_a(rb, a0, a1);
             mfma_ab(rb, a0, a1);
         };
-        if constexpr (CB == 2 && HX_QT_IL) {
-            // the next chunk's decode is cut into RB slices, one per row block: piece R reads the A
-            // fragments of row block R + 1, decodes slice R and issues row block R's MFMAs, so the
-            // slice's VALU work runs while the previous MFMAs execute and the LDS reads have a
-            // whole piece to land.  The fences keep that order (left alone, the scheduler gathers
-            // all MFMAs in one run and the decode in another).
-            const uint32_t* wn = wv[(ut + 1) % PT];
-            uint32_t M[BITS + 1];
 #pragma unroll
-            for (int j = 1; j <= BITS; ++j) M[j] = __builtin_amdgcn_alignbit(wn[j - 1], wn[j], 16);
-            constexpr int PS = 32 / RB;
-            hx_h8 fa[2][2];
-            read_a(0, fa[0][0], fa[0][1]);
-            [&]<int... R>(std::integer_sequence<int, R...>) {
-                (((R + 1 < RB ? read_a(R + 1, fa[(R + 1) & 1][0], fa[(R + 1) & 1][1]) : void()),
-                  quarter_affine_range<BITS, R * PS, (R + 1) * PS>(wn, M, dn), mfma_ab(R, fa[R & 1][0], fa[R & 1][1]),
-                  __builtin_amdgcn_sched_barrier(0)),
-                 ...);
-            }(std::make_integer_sequence<int, RB>{});
-        } else {
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) mfma_rb(rb);
-            decode((ut + 1) % PT, dn);
-        }
+        for (int rb = 0; rb < RB; ++rb) mfma_rb(rb);
+        decode((ut + 1) % PT, dn);
         if constexpr (DMA) __builtin_amdgcn_s_waitcnt(qt_vmcnt(A_WAIT));
         else store_a((ua + 1) % PF, (c + 1) & 1, c + 1 < nk);
         hx_lds_barrier();
