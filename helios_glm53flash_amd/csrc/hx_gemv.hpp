@@ -45,21 +45,12 @@ inline int gemv_kc_for(int K, int cap)
 
 typedef const __attribute__((address_space(1))) uint32_t hx_gu32;
 
-// Words q*BITS-1 .. q*BITS+BITS-1 (cyclic) of the tile at `tile`.
-template <int BITS>
-HX_INLINE void load_quarter(uint32_t* r, const uint32_t* tile, int q)
-{
-    constexpr int NW = 8 * BITS;
-    hx_gu32* t = (hx_gu32*)tile;
-    r[0] = __builtin_nontemporal_load(t + (q * BITS + NW - 1) % NW);
-#pragma unroll
-    for (int i = 0; i < BITS; ++i) r[i + 1] = __builtin_nontemporal_load(t + q * BITS + i);
-}
-
-// The same words through a buffer resource: the per-lane byte offsets are fixed for a whole
-// range (voff0 of the wrapped first word, voff1 of the rest) and the step moves only the scalar
-// offset, so a step's loads cost no vector ALU address arithmetic; a read past the tensor's end
-// (num_records) returns zeros instead of faulting.
+// A lane decodes quarter q of a 16x16 tile from the tile's words q*BITS-1 .. q*BITS+BITS-1 (cyclic;
+// NW = 8*BITS words per tile), held in r[0..BITS].  Only words q*BITS .. q*BITS+BITS-1 are loaded,
+// through a buffer resource: the per-lane byte offset is fixed for a whole range and the step moves
+// only the scalar offset, so a step's loads cost no vector ALU address arithmetic, and a read past
+// the tensor's end (num_records) returns zeros instead of faulting.  The first word is the last
+// word of quarter q-1, which the neighbouring lane loaded (quarter_wrap).
 typedef unsigned int hx_u2 __attribute__((ext_vector_type(2)));
 typedef unsigned int hx_u3 __attribute__((ext_vector_type(3)));
 typedef unsigned int hx_u4v __attribute__((ext_vector_type(4)));
@@ -83,18 +74,32 @@ HX_INLINE void buf_words(uint32_t* r, __amdgpu_buffer_rsrc_t rs, int voff, int s
     }
 }
 
-// VMEM instructions that load_quarter_buf issues: one dword for the wrapped first word, then the
-// BITS words in 16-byte pieces (buf_words).  Waits that count loads in flight (the MFMA tile's
+// VMEM instructions that load_quarter_buf issues: the BITS words in 16-byte pieces (buf_words).  Waits that count loads in flight (the MFMA tile's
 // s_waitcnt on its LDS-DMA ring) take their per-chunk count from here.  Each piece is its own
 // buffer-load builtin with its own offset register, so the compiler cannot merge pieces into fewer
 // instructions (which would make a counted wait too short).
-constexpr int quarter_buf_vmem(int bits) { return 1 + (bits + 3) / 4; }
+constexpr int quarter_buf_vmem(int bits) { return (bits + 3) / 4; }
 
+// r[1..BITS] = words q*BITS .. q*BITS+BITS-1 of the lane's tile (voff: their byte offset).
 template <int BITS>
-HX_INLINE void load_quarter_buf(uint32_t* r, __amdgpu_buffer_rsrc_t rs, int voff0, int voff1, int soff)
+HX_INLINE void load_quarter_buf(uint32_t* r, __amdgpu_buffer_rsrc_t rs, int voff, int soff)
 {
-    r[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff0, soff, HX_BUF_NT);
-    buf_words<BITS>(r + 1, rs, voff1, soff);
+    buf_words<BITS>(r + 1, rs, voff, soff);
+}
+
+// r[0] = word q*BITS-1 (cyclic) of the tile, once r[1..BITS] have arrived in every lane of the wave.
+// The 8 quarters of a tile are decoded by 8 consecutive lanes (q = lane & 7), so the word is r[BITS]
+// of lane q-1, or of lane q+7 for q = 0: a rotation of each 16-lane row by 1 or by 9 (DPP
+// row_ror, lane i reads lane (i - n) mod 16 of its row).  A separate load of that word cost as much
+// memory throughput as the quarter's own words (a loads-only stream of the lm_head: 115 us with it,
+// 83 us without).  Every lane of the wave must be active.
+template <int BITS>
+HX_INLINE void quarter_wrap(uint32_t* r)
+{
+    const int w = (int)r[BITS];
+    const uint32_t prev = (uint32_t)__builtin_amdgcn_mov_dpp(w, 0x121, 0xf, 0xf, false);  // row_ror:1
+    const uint32_t last = (uint32_t)__builtin_amdgcn_mov_dpp(w, 0x129, 0xf, 0xf, false);  // row_ror:9
+    r[0] = (threadIdx.x & 7) ? prev : last;
 }
 
 // The 32 bits ending at local bit E of the quarter registers (bit 0 = local bit E-1).
@@ -263,18 +268,6 @@ HX_INLINE void quarter_affine_pairs(const uint32_t* r, const uint32_t* M, uint32
         const uint32_t x1 = quarter_window<BITS, P + 1>(r, M) * 0x83DCD12Du;
         out[qpos(P / 2)] = __builtin_amdgcn_sad_hi_u8(x1, 0u, __builtin_amdgcn_sad_u8(x0, 0u, 0x64006400u));
         quarter_affine_pairs<BITS, P + 2>(r, M, out);
-    }
-}
-
-// Positions [P0, P1) of quarter_affine_pairs (for spreading a quarter's decode over a loop).
-template <int BITS, int P0, int P1>
-HX_INLINE void quarter_affine_range(const uint32_t* r, const uint32_t* M, uint32_t* out)
-{
-    if constexpr (P0 < P1) {
-        const uint32_t x0 = quarter_window<BITS, P0>(r, M) * 0x83DCD12Du;
-        const uint32_t x1 = quarter_window<BITS, P0 + 1>(r, M) * 0x83DCD12Du;
-        out[qpos(P0 / 2)] = __builtin_amdgcn_sad_hi_u8(x1, 0u, __builtin_amdgcn_sad_u8(x0, 0u, 0x64006400u));
-        quarter_affine_range<BITS, P0 + 2, P1>(r, M, out);
     }
 }
 
@@ -521,7 +514,7 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
         reinterpret_cast<void*>(twb), 0, (int)min((size_t)0x7fffffff, (size_t)(g.K >> 4) * tiles_n * NW * 4),
         0x00020000);
     const int lane_off = ((gq * tiles_n + tn) * NW) * 4;
-    const int voff0 = lane_off + ((q * BITS + NW - 1) % NW) * 4, voff1 = lane_off + q * BITS * 4;
+    const int voff = lane_off + q * BITS * 4;
     const int row_bytes = tiles_n * NW * 4;
     auto soff = [&](int st) { return ((k0 + step_k(min(st, steps - 1))) >> 4) * row_bytes; };
     InputRegs in;
@@ -530,7 +523,7 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     if (!g.pre_transformed && !MF_IN) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, false);
     if (steps > 0) {
 #pragma unroll
-        for (int j = 0; j < PF; ++j) load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff(j));
+        for (int j = 0; j < PF; ++j) load_quarter_buf<BITS>(buf[j], rs, voff, soff(j));
     }
 
     before_input();
@@ -574,10 +567,11 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
             const bool live = !GUARD || st < steps;
             uint32_t d[16];
             if (live) {
+                quarter_wrap<BITS>(buf[j]);
                 if constexpr (AFFINE) quarter_affine<BITS>(buf[j], d);
                 else quarter_decode<BITS, CB>(buf[j], d);
             }
-            load_quarter_buf<BITS>(buf[j], rs, voff0, voff1, soff(st + PF));
+            load_quarter_buf<BITS>(buf[j], rs, voff, soff(st + PF));
             if (live) {
                 const int kl = step_k(st) + 16 * gq;
                 const hx_h8 a0 = *reinterpret_cast<const hx_h8*>(arow + kl);

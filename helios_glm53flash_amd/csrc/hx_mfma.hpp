@@ -152,7 +152,7 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
     }
     const int g = lane >> 4, tq = (lane >> 3) & 1, q = lane & 7;
     const int t_off = ((g * tiles_n + tn0 + 2 * wave + tq) * NW) * 4;
-    const int voff0 = t_off + ((q * BITS + NW - 1) % NW) * 4, voff1 = t_off + q * BITS * 4;
+    const int voff = t_off + q * BITS * 4;
     const int row_bytes = tiles_n * NW * 4;
 
     // A and the trellis words have rings of their own: PF chunks of A (16 VGPRs per chunk at BM 128),
@@ -170,7 +170,7 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
 #pragma unroll
         for (int i = 0; i < NA; ++i) av[slot][i] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[i], k0 * 2, 0);
     };
-    auto load_t = [&](int slot, int k0) { load_quarter_buf<BITS>(wv[slot], rt, voff0, voff1, (k0 >> 4) * row_bytes); };
+    auto load_t = [&](int slot, int k0) { load_quarter_buf<BITS>(wv[slot], rt, voff, (k0 >> 4) * row_bytes); };
     // A straight into LDS (buffer loads with an LDS destination): instruction i of wave w fills rows
     // 32i + 8w .. +7 of the buffer, lane l 16 bytes at slot l % 8 of row 32i + 8w + l / 8, so the lane
     // fetches the chunk that the swizzle puts in that slot.  Rows past the tile's end read zeros (the
@@ -210,6 +210,7 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
         }
     };
     auto decode = [&](int slot, uint32_t* d) {
+        quarter_wrap<BITS>(wv[slot]);
         if constexpr (CB == 2) quarter_affine<BITS>(wv[slot], d);
         else quarter_decode<BITS, CB>(wv[slot], d);
     };
