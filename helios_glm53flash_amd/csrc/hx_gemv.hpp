@@ -30,6 +30,15 @@ namespace hx {
 constexpr int LIN_PF = 2;   // up to 4 bits
 constexpr int LIN_PFW = 4;  // wider
 
+// Stream-K for one row when the split-K grid is one workgroup per column group and does not spread
+// evenly over the 256 CUs (the lm_head, 4096 -> 151552: 1184 groups, 4 or 5 workgroups per CU, and
+// the CUs with 4 go idle while those with 5 finish): 1024 workgroups (4 on every CU) take equal runs
+// of the (column group, 128-k block) units.  lm_head in a graph of 20 calls on one box: 101-104 ->
+// 96 us; 2048 workgroups: no gain.  A grid already even over the CUs (K = 16384 -> 32768, 2-bit:
+// 4 splits, 1024 workgroups) measured 2 us slower as stream-K, and small linears are bound by their
+// chain of dependent steps, not by the work.
+constexpr int GEMV_SK_WGS = 1024;
+constexpr int GEMV_CUS = 256;
 constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_WAVES = 4;
 
@@ -449,6 +458,7 @@ struct GemvArgs {
     float* partial;          // [splits][M][N] fp32 (unused when splits == 1)
     int* counter;            // [N/128] (unused when splits == 1)
     bool pre_transformed;
+    int sk_blocks;           // stream-K: (column group, 128-k block) units in all (0: split-K grid)
 };
 
 // LDS scratch of gemv_range: one array per (N, KS), shared by every instantiation of a kernel (a
@@ -460,6 +470,13 @@ __device__ __forceinline__ float* gemv_lds()
     return buf;
 }
 
+// 16 zero halves in LDS (the row-step A operand outside the diagonal).
+__device__ __forceinline__ uint32_t* gemv_zero_lds()
+{
+    __shared__ __align__(16) uint32_t z[8];
+    return z;
+}
+
 // This workgroup's partial sum of the GEMV over k in [k0, k0 + kc) (kc a multiple of 128): on
 // return colsum[m][c] (LDS fp32, MT x 128) holds sum over that range of a[m][k] * W[k][cg*128 + c].
 // a_lds must hold MT * kc fp16.  MT <= 16.
@@ -468,33 +485,48 @@ __device__ __forceinline__ float* gemv_lds()
 // owns tile columns 2(w%4), 2(w%4)+1 over the 128-k blocks j = w/4, w/4 + 4, ... of the range, and
 // the four partial sums of a column pair are added in block-subset order through LDS.
 //
+// ROW (one row, KS = 1): a step of a wave covers ONE tile row of all 8 tiles of the group instead of
+// 4 tile rows of 2 tiles, and wave w takes tile rows w, w+4, w+8, ... of the range.  Lane 16p + 8t + q
+// then decodes quarter q of tile 2p + t, so a step's loads cover the group's whole tile row
+// contiguously (a loads-only stream of the lm_head, 5-bit: 73 us against 83 us for the 4-row step).
+// The matrix cores still sum over the four 8-k groups of an MFMA; with one row the groups are kept
+// apart through A: row i of A holds the input only in k group i (lanes with lane % 16 == lane / 16),
+// zeros elsewhere, so output row p of the MFMA is tile pair p's sum.  The four waves' sums are added
+// in wave order through LDS.
+//
 // before_input() runs after the tile prefetch is issued and before a pre-transformed input is read
 // (a consumer waits there for its producer); after_input() runs once the input is in LDS.
 // PF4 / PFW: steps of tile words in flight per wave for bit widths up to 4 / wider.
-template <int BITS, int CB, int MT, int KS = 1, int PF4 = 8, int PFW = 4, class Before = NoHook, class After = NoHook>
+template <int BITS, int CB, int MT, int KS = 1, int PF4 = 8, int PFW = 4, bool ROW = false, class Before = NoHook,
+          class After = NoHook>
 __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, int kc, uint32_t* a_lds, float* colsum,
                                            Before before_input = Before(), After after_input = After())
 {
     static_assert(MT <= 16, "one MFMA holds 16 rows");
     static_assert(KS == 1 || KS == 2 || KS == 4, "k subsets");
+    static_assert(!ROW || (MT == 1 && KS == 1), "row steps: one row, no k subsets");
     constexpr bool AFFINE = CB == 2;
     float* asum = gemv_lds<MT, 1>();  // sum of the transformed input over the range, per row (cb2)
-    float* kpart = gemv_lds<MT * 128, KS>();
+    float* kpart = gemv_lds<MT * 128, ROW ? 4 : KS>();
     // wave index as a uniform (scalar) value: the step offsets below stay in SGPRs
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int pair = KS == 1 ? wave : (wave & 3);  // tile-column pair of this wave
-    const int ks = KS == 1 ? 0 : (wave >> 2);      // block subset of this wave
-    const int gq = lane >> 4;             // tile row within the 4-row step (MFMA k-group)
-    const int t = (lane >> 3) & 1;        // tile column of the wave's pair
-    const int q = lane & 7;               // quarter
+    // tile-column pair of this lane: the wave's (row steps: the lane group's)
+    const int pair = ROW ? (lane >> 4) : KS == 1 ? wave : (wave & 3);
+    const int ks = KS == 1 ? 0 : (wave >> 2);  // block subset of this wave
+    const int gq = ROW ? 0 : (lane >> 4);      // tile row within the 4-row step (MFMA k-group)
+    const int t = (lane >> 3) & 1;             // tile column of the pair
+    const int q = lane & 7;                    // quarter
     const int tiles_n = g.N >> 4;
     constexpr int NW = 8 * BITS;
     const uint32_t* tw = reinterpret_cast<const uint32_t*>(g.trellis);
     const int tn = cg * 8 + 2 * pair + t;
     const int nblk = kc >> 7;
-    // this wave's steps: step s covers k = k0 + 128 * (ks + KS * (s / 2)) + 64 * (s % 2)
+    // this wave's steps: step s covers k = k0 + 128 * (ks + KS * (s / 2)) + 64 * (s % 2) (row steps:
+    // the 16 k of tile row wave + 4s); kc is a multiple of 128, so every wave has kc / 64 row steps
     const int steps = KS == 1 ? (kc >> 6) : 2 * max(0, (nblk - ks + KS - 1) / KS);
-    auto step_k = [&](int st) { return 128 * (ks + KS * (st >> 1)) + 64 * (st & 1); };  // relative to k0
+    auto step_k = [&](int st) {  // relative to k0
+        return ROW ? 16 * (wave + 4 * st) : 128 * (ks + KS * (st >> 1)) + 64 * (st & 1);
+    };
 
     // software pipeline: PF steps of tile words in flight.  The first PF are issued before the input
     // transform (after the input loads themselves) so their HBM latency overlaps it; every step then
@@ -530,6 +562,12 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     if (g.pre_transformed) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, true);
     if (MF_IN && !g.pre_transformed) input_mfma(a_lds, g.x, g.rows, g.suh, g.M, g.K, k0, kc);
     else input_finish(a_lds, in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, g.pre_transformed);
+    // row steps: the A rows of the lanes outside the diagonal read zeros (16 halves)
+    uint32_t* zrow = nullptr;
+    if constexpr (ROW) {
+        zrow = gemv_zero_lds();
+        if (threadIdx.x < 8) zrow[threadIdx.x] = 0u;
+    }
     hx_lds_barrier();
     after_input();
     if constexpr (AFFINE) {
@@ -545,7 +583,10 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
 
     hx_f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
     const int am = min(lane & 15, g.M - 1);  // A row of this lane (rows >= M repeat the last row)
-    const _Float16* arow = reinterpret_cast<const _Float16*>(a_lds) + (size_t)am * kc;
+    const bool diag = (lane & 15) == (lane >> 4);
+    const _Float16* arow = ROW && !diag ? reinterpret_cast<const _Float16*>(zrow)
+                                        : reinterpret_cast<const _Float16*>(a_lds) + (size_t)am * kc;
+    const int kmask = ROW && !diag ? 0 : -1;
     // one group of PF steps; GUARD: the group runs past the range (only the last group can)
     auto group = [&](int st0, auto guard) {
         constexpr bool GUARD = decltype(guard)::value;
@@ -573,7 +614,7 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
             }
             load_quarter_buf<BITS>(buf[j], rs, voff, soff(st + PF));
             if (live) {
-                const int kl = step_k(st) + 16 * gq;
+                const int kl = (step_k(st) + 16 * gq) & kmask;
                 const hx_h8 a0 = *reinterpret_cast<const hx_h8*>(arow + kl);
                 const hx_h8 a1 = *reinterpret_cast<const hx_h8*>(arow + kl + 8);
                 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, quarter_operand<0, 0>(d), acc0, 0, 0, 0);
@@ -595,7 +636,22 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     HX_SETPRIO(3);  // the split-K handoff and epilogues are on the critical path
     // C: lane holds rows 4*(lane/16) + i of column label lane%16 = 8t + q; label -> column
     // 16*(2*pair + t) + 8*nh + q of the group
-    if constexpr (KS > 1) {
+    if constexpr (ROW) {
+        // lanes 0..15 hold output rows 0..3 = the sums of tile pairs 0..3 (column label 8t + q)
+        if (lane < 16) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                kpart[wave * 128 + 16 * (2 * i + t) + q] = acc0[i];
+                kpart[wave * 128 + 16 * (2 * i + t) + 8 + q] = acc1[i];
+            }
+        }
+        hx_lds_barrier();
+        for (int i = threadIdx.x; i < 128; i += hx_nthreads()) {
+            float v = ((kpart[i] + kpart[128 + i]) + kpart[256 + i]) + kpart[384 + i];
+            if constexpr (AFFINE) v = fmaf(v, CB2_SCALE, CB2_BIAS * asum[0]);
+            colsum[i] = v;
+        }
+    } else if constexpr (KS > 1) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int m = 4 * gq + i;
@@ -641,7 +697,7 @@ __device__ __forceinline__ void gemv_split_sum(const GemvArgs& g, int cg, int s,
                                                Before before_input = Before(), After after_input = After())
 {
     const int k0 = s * g.kc;
-    gemv_range<BITS, CB, MT, 1, LIN_PF, LIN_PFW>(g, cg, k0, min(g.kc, g.K - k0), a_lds, colsum, before_input,
+    gemv_range<BITS, CB, MT, 1, LIN_PF, LIN_PFW, MT == 1>(g, cg, k0, min(g.kc, g.K - k0), a_lds, colsum, before_input,
                                                    after_input);
 }
 

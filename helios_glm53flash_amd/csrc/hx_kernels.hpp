@@ -15,7 +15,14 @@ constexpr size_t HX_COUNTER_BYTES = 64 * 1024;
 constexpr int GEMV_MAX_M = 16;
 
 // small-M linear (hx_linear.hip)
-void gemv_plan(int M, int K, int N, int bits, int* splits, int* kc);
+// Grid of the small-M linear: either column groups x `splits` k chunks of `kc`, or (one row, many
+// 128-k blocks) `sk_wgs` workgroups over equal runs of (column group, block) units, whose column
+// groups are shared by at most `slots` workgroups (stream-K).
+struct GemvPlan {
+    int splits, kc;
+    int sk_wgs, sk_blocks, slots;
+};
+GemvPlan gemv_plan(int M, int K, int N);
 size_t gemv_workspace_bytes(int M, int K, int N);
 hipError_t launch_linear_gemv(const _Float16* x, const uint16_t* trellis, const _Float16* suh, const _Float16* svh,
                               void* y, int M, int K, int N, int bits, int cb, bool y_fp32, void* ws, hipStream_t st);

@@ -3,7 +3,7 @@
 #include "hx_gemv.hpp"
 #include "hx_kernels.hpp"
 
-#include <stdlib.h>
+#include <algorithm>
 
 namespace hx {
 
@@ -18,9 +18,8 @@ hipError_t launch_gemv_cb(int cb, const GemvArgs& g, const _Float16* svh, void* 
 // config 2 (N = 12288) best at 8 splits too (15.0 us; 20.6 us with 16 splits).
 constexpr int GEMV_KC_FLOOR = 512;
 
-void gemv_plan(int M, int K, int N, int bits, int* splits, int* kc)
+static void split_plan(int M, int K, int N, int* splits, int* kc)
 {
-    (void)bits;
     const int groups = N / 128;
     const int cap = 16384 / (M < 1 ? 1 : M);
     int c = gemv_kc_for(K, cap);
@@ -36,11 +35,31 @@ void gemv_plan(int M, int K, int N, int bits, int* splits, int* kc)
     *splits = K / c;
 }
 
+GemvPlan gemv_plan(int M, int K, int N)
+{
+    GemvPlan p{};
+    split_plan(M, K, N, &p.splits, &p.kc);
+    const int groups = N / 128;
+    const long long nb = K / 128, blocks = (long long)groups * nb;
+    // unit and workgroup indices are multiplied in 32 bits in the kernel: blocks * wgs < 2^31
+    if (M == 1 && p.splits == 1 && groups > GEMV_SK_WGS && groups % GEMV_CUS != 0 &&
+        blocks * GEMV_SK_WGS < (1LL << 31) &&
+        (blocks + GEMV_SK_WGS - 1) / GEMV_SK_WGS <= 16384 / 128) {
+        p.sk_wgs = GEMV_SK_WGS;
+        p.sk_blocks = (int)blocks;
+        // a workgroup covers at least blocks / wgs blocks, so a column group's nb blocks meet at most
+        // nb / (blocks / wgs) + 2 workgroups
+        p.slots = (int)(nb / (blocks / GEMV_SK_WGS) + 2);
+        p.kc = (int)std::min<long long>(nb, (blocks + GEMV_SK_WGS - 1) / GEMV_SK_WGS) * 128;  // LDS per workgroup
+    }
+    return p;
+}
+
 size_t gemv_workspace_bytes(int M, int K, int N)
 {
-    int s, kc;
-    gemv_plan(M, K, N, 8, &s, &kc);
-    return HX_COUNTER_BYTES + (size_t)s * M * N * sizeof(float);
+    const GemvPlan p = gemv_plan(M, K, N);
+    const int parts = p.sk_wgs ? p.slots : p.splits;
+    return HX_COUNTER_BYTES + (size_t)parts * M * N * sizeof(float);
 }
 
 hipError_t launch_linear_gemv(const _Float16* x, const uint16_t* trellis, const _Float16* suh, const _Float16* svh,
@@ -54,7 +73,10 @@ hipError_t launch_linear_gemv(const _Float16* x, const uint16_t* trellis, const 
     g.M = M;
     g.K = K;
     g.N = N;
-    gemv_plan(M, K, N, bits, &g.splits, &g.kc);
+    const GemvPlan p = gemv_plan(M, K, N);
+    g.splits = p.splits;
+    g.kc = p.kc;
+    g.sk_blocks = p.sk_wgs ? p.sk_blocks : 0;
     if ((size_t)(N / 128) * sizeof(int) > HX_COUNTER_BYTES) return hipErrorInvalidValue;
     g.counter = static_cast<int*>(ws);
     g.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + HX_COUNTER_BYTES);

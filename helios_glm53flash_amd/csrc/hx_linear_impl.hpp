@@ -50,6 +50,37 @@ __global__ __launch_bounds__(GEMV_THREADS) void linear_gemv_kernel(GemvArgs g, c
     linear_epilogue<MT>(colsum, svh, y, g.M, g.N, cg, y_fp32);
 }
 
+// Workgroup owning unit b of `units` split evenly over `wgs` workgroups (workgroup i takes units
+// [i*units/wgs, (i+1)*units/wgs)): the largest i whose first unit is <= b.  units * wgs < 2^31.
+HX_INLINE unsigned stream_owner(unsigned b, unsigned units, unsigned wgs) { return ((b + 1) * wgs - 1) / units; }
+
+// One row, stream-K: workgroup i runs the (column group, 128-k block) units [i*T/G, (i+1)*T/G) of
+// T = (N/128) * (K/128), group by group.  A group met by several workgroups is finished by the last
+// to arrive, which adds the partials in workgroup order (deterministic); the others publish theirs.
+template <int BITS, int CB>
+__global__ __launch_bounds__(GEMV_THREADS) void linear_gemv_stream_kernel(GemvArgs g, const _Float16* svh, void* y,
+                                                                         bool y_fp32)
+{
+    extern __shared__ uint32_t a_lds[];
+    __shared__ float colsum[128];
+    const unsigned T = g.sk_blocks, G = gridDim.x, nb = g.K >> 7, i = blockIdx.x;
+    const unsigned b1 = (i + 1) * T / G;
+    for (unsigned b = i * T / G; b < b1;) {
+        const unsigned cg = b / nb, e = min(b1, (cg + 1) * nb);
+        gemv_range<BITS, CB, 1, 1, LIN_PF, LIN_PFW, true>(g, cg, (b - cg * nb) * 128, (e - b) * 128, a_lds, colsum);
+        const unsigned first = stream_owner(cg * nb, T, G), last = stream_owner(cg * nb + nb - 1, T, G);
+        bool finish = true;
+        if (last > first) {
+            publish_partial<1>(g.partial, 1, g.N, cg, i - first, colsum);
+            finish = arrive_last(&g.counter[cg], last - first + 1);
+            if (finish) gather_partials<1>(g.partial, 1, g.N, last - first + 1, cg, colsum);
+        }
+        if (finish) linear_epilogue<1>(colsum, svh, y, 1, g.N, cg, y_fp32);
+        __syncthreads();  // colsum is read before the next group overwrites it
+        b = e;
+    }
+}
+
 template <int BITS, int CB, int MT>
 hipError_t launch_gemv_t(const GemvArgs& g, const _Float16* svh, void* y, bool y_fp32, hipStream_t st)
 {
@@ -63,6 +94,11 @@ hipError_t launch_gemv_t(const GemvArgs& g, const _Float16* svh, void* y, bool y
 template <int BITS, int CB>
 hipError_t launch_gemv_b(const GemvArgs& g, const _Float16* svh, void* y, bool y_fp32, hipStream_t st)
 {
+    if (g.sk_blocks) {  // one row (gemv_plan): the grid is the plan's workgroup count
+        hipLaunchKernelGGL((linear_gemv_stream_kernel<BITS, CB>), dim3(GEMV_SK_WGS), dim3(GEMV_THREADS),
+                           (size_t)g.kc * sizeof(_Float16), st, g, svh, y, y_fp32);
+        return hipGetLastError();
+    }
     if (g.M <= 1) return launch_gemv_t<BITS, CB, 1>(g, svh, y, y_fp32, st);
     if (g.M <= 4) return launch_gemv_t<BITS, CB, 4>(g, svh, y, y_fp32, st);
     if (g.M <= 8) return launch_gemv_t<BITS, CB, 8>(g, svh, y, y_fp32, st);
