@@ -237,3 +237,45 @@ def test_moe_prefill_topk_variants(hx, topk):
     """The matrix-core combine serves topk dividing 16 (1, 2, 16 here, besides 4 and 8 above), the
     per-token combine any other topk (6)."""
     _run_layer(hx, E=32, hidden=256, inter=256, topk=topk, T=20, bits=2, shared_bits=2, seed=950 + topk)
+
+
+@pytest.mark.parametrize("cb", [2, 1])
+@pytest.mark.parametrize("T", [5, 160])
+def test_moe_grouped_every_bit_width(hx, cb, T):
+    """hx_moe_grouped with per-expert bit widths that cover 1..8 in every projection (expert e:
+    gate 1 + e % 8, up 1 + (e + 3) % 8, down 1 + (e + 5) % 8), codebook mul1 (cb 2) and MCG (cb 1),
+    on the few-token decode kernel (T = 5) and the grouped MFMA path (T = 160).  Tokens 0..3 route
+    to every expert; in the longer batch the other tokens favour experts 0..3, which then take
+    128-row tiles besides the 32-row ones of the others."""
+    import torch
+    from oracle import oracle as O
+    exl3, moe = hx
+    E, hidden, inter, topk = 16, 512, 256, 4
+    bits = [(1 + e % 8, 1 + (e + 3) % 8, 1 + (e + 5) % 8) for e in range(E)]
+    ex = moe.ExpertSet.synthetic(E, hidden, inter, bits, seed=1000 + T + cb, mul1=(cb == 2))
+    r = np.random.default_rng(1000 + T)
+    xh = (r.standard_normal((T, hidden)) * 0.5).astype(np.float16)
+    s = r.standard_normal((T, E))
+    for t in range(4):  # tokens 0..3 route to experts 4t..4t+3: every expert, so every width, is used
+        s[t, 4 * t:4 * t + 4] += 6.0
+    s[4:, :4] += 3.0  # the hot experts of the longer batch
+    sh = s.astype(np.float16)
+    idx, w = O.routing(sh, topk, 2.5)
+    used = set(int(e) for e in idx.reshape(-1))
+    assert len(used) == E, "every expert (so every width) is routed"
+    x = torch.from_numpy(xh).cuda()
+    idx_d = torch.from_numpy(idx).cuda()
+    w_d = torch.from_numpy(w.view(np.float16)).cuda()
+    cnt = torch.empty(E + 1, dtype=torch.int64, device="cuda")
+    ts = torch.empty(T * topk, dtype=torch.int64, device="cuda")
+    wsr = torch.empty(T * topk, dtype=torch.float16, device="cuda")
+    r2s = torch.empty(T * topk, dtype=torch.int64, device="cuda")
+    exl3.moe_permute(idx_d, w_d, T, topk, E, cnt, ts, wsr, None, route_to_sorted=r2s)
+    y = torch.zeros((T, hidden), dtype=torch.float32, device="cuda")
+    moe.moe_grouped(x, y, cnt, ts, wsr, ex, T, topk, act_limit=10.0, route_to_sorted=r2s, mcg=(cb == 1))
+    torch.cuda.synchronize()
+    ref, _ = O.moe_rows(xh.view(np.uint16), hidden, inter, idx, w, np.arange(T), _oracle_experts(ex, used), None,
+                        10.0, cb=cb)
+    got = y.cpu().numpy()
+    assert np.isfinite(got).all()
+    assert_close(got, ref, what=f"every width, cb={cb}, T={T}")
