@@ -114,18 +114,20 @@ def test_dense_3bit_real_shape(hx, M):
     assert_close(got, ref, what=f"3-bit 4096x12288 M={M}")
 
 
-def test_gemv_stream_k_sampled_columns(hx):
+@pytest.mark.parametrize("cb", [2, 1, 0])
+def test_gemv_stream_k_sampled_columns(hx, cb):
     """One row whose split-K grid would be one workgroup per column group, unevenly spread over the
     256 CUs (1100 groups), takes the stream-K grid: 1024 workgroups over equal runs of (column group,
     128-k block) units, so most column groups are shared by two workgroups whose partials the last
     arriver adds.  Sampled column groups against the oracle, fp16 output, three calls in a row (the
-    arrival counters are reset by each call, and the result is the same every time)."""
+    arrival counters are reset by each call, and the result is the same every time); codebooks mul1
+    (2), MCG (1) and the 3INST table (0)."""
     import torch
     from oracle import oracle as O
     K, N, bits = 4096, 1100 * 128, 2
-    tr, suh, svh = make_linear(702, K, N, bits)
+    tr, suh, svh = make_linear(702 + cb, K, N, bits)
     x = make_x(703, 1, K)
-    w = hx.GroupWords(_dev(tr, torch.int16), _dev(suh), _dev(svh), hx.MUL1)
+    w = hx.GroupWords(_dev(tr, torch.int16), _dev(suh), _dev(svh), hx.MUL1 if cb == 2 else 0)
     # workgroup i takes units [i*T/1024, (i+1)*T/1024) of T = 1100 * 32 (34.4 blocks each): groups 1,
     # 30, 31 and 32 are split over two workgroups, 0, 549, 550 and the last lie in one
     groups = (0, 1, 30, 31, 32, 549, 550, N // 128 - 1)
@@ -133,16 +135,16 @@ def test_gemv_stream_k_sampled_columns(hx):
     for g in groups:
         sl = slice(128 * g, 128 * g + 128)
         sub = np.ascontiguousarray(tr[:, 8 * g:8 * g + 8, :])
-        refs[g] = O.linear(x, sub, suh, np.ascontiguousarray(svh[sl]), K, 128, bits, 2, out_f16=True)
+        refs[g] = O.linear(x, sub, suh, np.ascontiguousarray(svh[sl]), K, 128, bits, cb, out_f16=True)
     first = None
     for call in range(3):
         y = torch.empty((1, N), dtype=torch.float16, device="cuda")
-        assert hx.gemm(y, _dev(x), w, 1, N, K, bits, False) == hx.HX_GEMM_PATH_GEMV
+        assert hx.gemm(y, _dev(x), w, 1, N, K, bits, False, mcg=(cb == 1)) == hx.HX_GEMM_PATH_GEMV
         torch.cuda.synchronize()
         got = y.float().cpu().numpy()
         for g in groups:
             sl = slice(128 * g, 128 * g + 128)
-            assert_close(got[:, sl], refs[g], what=f"stream-K {bits}-bit group {g} call {call}")
+            assert_close(got[:, sl], refs[g], what=f"stream-K {bits}-bit cb {cb} group {g} call {call}")
         if first is None:
             first = got
         else:
