@@ -655,8 +655,11 @@ __device__ __forceinline__ void combine_columns(const MoeDecodeArgs& a, const De
 // is in flight at once, and the queue that builds up in the memory system delays each unit's own
 // dependent loads (scores, inputs, flags, partial sums): measured at config 3 (layer time), 8 steps
 // 51.1 us, 6 steps 49.8 us, 5 steps 49.6 us, 4 steps 49.4 us, 3 steps 50.5 us, 2 steps 51.7 us.
+// Since a step loads only the quarter's own words (one load per lane at 2 bits, the wrapped word
+// comes from the neighbouring lane), 5 steps are best: 45.9-46.0 us against 46.4-46.5 us with 4 and
+// 3, 46.3-46.5 us with 6 (one box, two runs each).
 // (The linear GEMV keeps its own ring depth: it streams alone.)
-constexpr int DEC_PF = 4;
+constexpr int DEC_PF = 5;
 constexpr int DEC_THREADS = 256;
 
 // Bounded wait of thread 0 for *flag >= target (the producers are resident workgroups that do not
