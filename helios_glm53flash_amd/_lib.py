@@ -68,6 +68,8 @@ SIGNATURES: dict[str, tuple] = {
                                                 C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int64, C.c_void_p]),
     "hx_exl3_pack_trellis": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "hx_exl3_unpack_trellis": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "hx_pack_signs": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]),
+    "hx_count_inf_nan": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_int, C.c_void_p]),
     "hx_moe_check_status": (C.c_int, [C.c_void_p, C.c_void_p]),
     "hx_moe_max_concurrency": (C.c_int, [C.c_int]),
     "hx_gemm_nt_f16": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,

@@ -323,6 +323,25 @@ int hx_exl3_unpack_trellis(void* unpacked, const void* packed, int rows, int col
                       "hx_exl3_unpack_trellis");
 }
 
+int hx_pack_signs(void* packed, const void* unpacked, int cols, hx_stream_t stream)
+{
+    if (cols < 0 || (cols > 0 && (!packed || !unpacked))) return fail(HX_ERR_INVALID, "hx_pack_signs: bad arguments");
+    if (cols == 0) return 0;
+    return hip_status(hx::launch_pack_signs(static_cast<uint16_t*>(packed), static_cast<const uint16_t*>(unpacked), cols,
+                                            (hipStream_t)stream),
+                      "hx_pack_signs");
+}
+
+int hx_count_inf_nan(const void* x, unsigned long long* counts, uint64_t numel, int dtype, hx_stream_t stream)
+{
+    if (!counts || (numel > 0 && !x)) return fail(HX_ERR_INVALID, "hx_count_inf_nan: null pointer");
+    if (dtype != HX_DTYPE_HALF && dtype != HX_DTYPE_FLOAT)
+        return fail(HX_ERR_INVALID, "hx_count_inf_nan: dtype must be HX_DTYPE_HALF or HX_DTYPE_FLOAT");
+    if (numel == 0) return 0;
+    return hip_status(hx::launch_count_inf_nan(x, counts, numel, dtype == HX_DTYPE_FLOAT, (hipStream_t)stream),
+                      "hx_count_inf_nan");
+}
+
 int hx_had_r_128(const void* input, void* output, const void* pre_scale, const void* post_scale, int64_t rows,
                  int cols, int dtype, float scale, hx_stream_t stream)
 {

@@ -35,6 +35,8 @@ hipError_t launch_linear_mfma(const _Float16* a_had, const uint16_t* trellis, co
 // utilities (hx_misc.hip)
 hipError_t launch_reconstruct(_Float16* out, const uint16_t* packed, int packed_rows, int packed_cols,
                               int unpacked_cols, int bits, int cb, long n_offset, hipStream_t st);
+hipError_t launch_pack_signs(uint16_t* packed, const uint16_t* unpacked, int cols, hipStream_t st);
+hipError_t launch_count_inf_nan(const void* x, unsigned long long* counts, uint64_t numel, bool fp32, hipStream_t st);
 hipError_t launch_had_r_128(const void* in1, void* out1, const void* scale1, const void* in2, void* out2,
                             const void* scale2, int scale_mode, long rows, int cols, bool fp32, float r_scale,
                             hipStream_t st);

@@ -503,4 +503,115 @@ hipError_t launch_scatter_add_rows(float* y, const float* src, const int64_t* id
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------------ sign packing, inf / NaN count
+
+// packed[c] bit i = sign bit of fp16 unpacked[16 c + i] (reference pack_signs_kernel,
+// src/cuda/quant/pack.cu:180-204: each value is shifted in at bit 15, then right, so value i ends in
+// bit i).  One lane per column: its 16 values are 32 contiguous bytes, two 16-byte loads when the
+// buffer is 16-byte aligned.
+template <bool VEC>
+__global__ __launch_bounds__(256) void pack_signs_kernel(uint16_t* packed, const uint16_t* unpacked, int cols)
+{
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= cols) return;
+    uint32_t w[8];
+    if constexpr (VEC) {
+        const uint4* src = reinterpret_cast<const uint4*>(unpacked + (size_t)16 * c);
+        const uint4 a = src[0], b = src[1];
+        w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w, w[4] = b.x, w[5] = b.y, w[6] = b.z, w[7] = b.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            w[j] = (uint32_t)unpacked[(size_t)16 * c + 2 * j] | ((uint32_t)unpacked[(size_t)16 * c + 2 * j + 1] << 16);
+    }
+    uint32_t out = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out |= ((w[j] >> 15) & 1u) << (2 * j) | (w[j] >> 31) << (2 * j + 1);
+    packed[c] = (uint16_t)out;
+}
+
+hipError_t launch_pack_signs(uint16_t* packed, const uint16_t* unpacked, int cols, hipStream_t st)
+{
+    const dim3 grid((unsigned)((cols + 255) / 256));
+    if (reinterpret_cast<uintptr_t>(unpacked) % 16 == 0)
+        hipLaunchKernelGGL(pack_signs_kernel<true>, grid, dim3(256), 0, st, packed, unpacked, cols);
+    else
+        hipLaunchKernelGGL(pack_signs_kernel<false>, grid, dim3(256), 0, st, packed, unpacked, cols);
+    return hipGetLastError();
+}
+
+// counts[0] += infinities, counts[1] += NaNs among numel fp16 (T = uint16_t) or fp32 (uint32_t) values
+// (reference count_inf_nan_kernel, src/cuda/quant/util.cu:54-80).  An infinity has every exponent
+// bit and no mantissa bit, a NaN every exponent bit and some mantissa bit.  Grid-stride over 16-byte
+// chunks (element by element when the buffer is not 16-byte aligned), a wave then workgroup sum, one
+// atomic add per counter per workgroup.
+template <class T, bool VEC>
+__global__ __launch_bounds__(256) void count_inf_nan_kernel(const T* x, unsigned long long* counts, uint64_t numel)
+{
+    constexpr uint32_t EXP = sizeof(T) == 2 ? 0x7c00u : 0x7f800000u, ABS = sizeof(T) == 2 ? 0x7fffu : 0x7fffffffu;
+    uint32_t n_inf = 0, n_nan = 0;
+    auto classify = [&](uint32_t v) {
+        v &= ABS;
+        n_inf += v == EXP;
+        n_nan += v > EXP;
+    };
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    uint64_t done = 0;
+    if constexpr (VEC) {
+        constexpr int PER = 16 / sizeof(T);  // values per 16-byte chunk
+        const uint64_t chunks = numel / PER;
+        const uint4* src = reinterpret_cast<const uint4*>(x);
+        for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < chunks; i += stride) {
+            const uint4 v = src[i];
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (sizeof(T) == 2) {
+                    classify(w[j] & 0xffffu);
+                    classify(w[j] >> 16);
+                } else {
+                    classify(w[j]);
+                }
+            }
+        }
+        done = chunks * PER;
+    }
+    for (uint64_t i = done + (uint64_t)blockIdx.x * 256 + threadIdx.x; i < numel; i += stride) classify(x[i]);
+    // per-thread counts stay below 2^32: numel / stride < 2^32 for every launch (grid below)
+    unsigned long long a = n_inf, b = n_nan;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        a += __shfl_xor(a, o, 64);
+        b += __shfl_xor(b, o, 64);
+    }
+    __shared__ unsigned long long part[2][4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        part[0][wave] = a;
+        part[1][wave] = b;
+    }
+    __syncthreads();
+    if (threadIdx.x < 2) {
+        const unsigned long long t = part[threadIdx.x][0] + part[threadIdx.x][1] + part[threadIdx.x][2] + part[threadIdx.x][3];
+        if (t) __hip_atomic_fetch_add(&counts[threadIdx.x], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+hipError_t launch_count_inf_nan(const void* x, unsigned long long* counts, uint64_t numel, bool fp32, hipStream_t st)
+{
+    // enough workgroups to fill the GPU a few times over, each thread covering numel / (grid * 256)
+    // values (below 2^32 for any numel below 2^51)
+    const uint64_t per = 16 / (fp32 ? 4 : 2), want = (numel / per + 255) / 256;
+    const unsigned grid = (unsigned)(want < 1 ? 1 : want > 4096 ? 4096 : want);
+    const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    if (fp32) {
+        if (vec) hipLaunchKernelGGL((count_inf_nan_kernel<uint32_t, true>), dim3(grid), dim3(256), 0, st, (const uint32_t*)x, counts, numel);
+        else hipLaunchKernelGGL((count_inf_nan_kernel<uint32_t, false>), dim3(grid), dim3(256), 0, st, (const uint32_t*)x, counts, numel);
+    } else {
+        if (vec) hipLaunchKernelGGL((count_inf_nan_kernel<uint16_t, true>), dim3(grid), dim3(256), 0, st, (const uint16_t*)x, counts, numel);
+        else hipLaunchKernelGGL((count_inf_nan_kernel<uint16_t, false>), dim3(grid), dim3(256), 0, st, (const uint16_t*)x, counts, numel);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace hx

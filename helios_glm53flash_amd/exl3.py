@@ -184,6 +184,29 @@ def unpack_trellis(unpacked: torch.Tensor, packed: torch.Tensor, rows: int, cols
           "hx_exl3_unpack_trellis")
 
 
+def pack_signs(packed: torch.Tensor, unpacked: torch.Tensor, cols: int, stream=None) -> None:
+    """packed[c] bit i = sign bit of unpacked[16 c + i]: uint16 [cols] from fp16 [cols * 16]
+    (reference pack.cuh:36-44)."""
+    _need(unpacked, "unpacked", (torch.float16,))
+    _need(packed, "packed", (torch.int16, torch.uint16))
+    if unpacked.numel() < 16 * cols or packed.numel() < cols:
+        raise ValueError("pack_signs: unpacked needs 16 * cols values and packed cols")
+    check(lib.hx_pack_signs(packed.data_ptr(), unpacked.data_ptr(), cols, _stream(stream)), "hx_pack_signs")
+
+
+def count_inf_nan(x: torch.Tensor, counts: torch.Tensor, stream=None) -> None:
+    """counts[0] += infinities, counts[1] += NaNs in x (fp16 or fp32); counts is an int64 [2] tensor
+    that the caller zeroes first (reference util.cuh:9-19)."""
+    if x.dtype not in (torch.float16, torch.float32):
+        raise TypeError("count_inf_nan: x must be float16 or float32")
+    _need(x, "x", (x.dtype,))
+    _need(counts, "counts", (torch.int64,))
+    if counts.numel() < 2:
+        raise ValueError("count_inf_nan: counts needs 2 elements")
+    check(lib.hx_count_inf_nan(x.data_ptr(), counts.data_ptr(), x.numel(), 0 if x.dtype == torch.float16 else 1,
+                               _stream(stream)), "hx_count_inf_nan")
+
+
 _HAD_DTYPES = {torch.float16: 0, torch.float32: 1}
 
 

@@ -165,6 +165,18 @@ inline void unpack_trellis(void* unpacked, const void* packed, int rows, int col
     check(hx_exl3_unpack_trellis(unpacked, packed, rows, cols, K, (hx_stream_t)s), "helios::exl3::unpack_trellis");
 }
 
+// reference: src/cuda/quant/pack.cuh:36-44 (packed[c] bit i = sign of unpacked[16 c + i])
+inline void pack_signs(void* packed, const void* unpacked, int cols, Stream s = 0)
+{
+    check(hx_pack_signs(packed, unpacked, cols, (hx_stream_t)s), "helios::exl3::pack_signs");
+}
+
+// reference: src/cuda/quant/util.cuh:9-19 (y[0] += infinities, y[1] += NaNs; the caller zeroes y)
+inline void count_inf_nan(const void* x, unsigned long long* y, uint64_t numel, DType dt, Stream s = 0)
+{
+    check(hx_count_inf_nan(x, y, numel, (int)dt, (hx_stream_t)s), "helios::exl3::count_inf_nan");
+}
+
 // reference: src/cuda/quant/exl3_moe.cuh:35
 inline int moe_max_concurrency(int device) { return check(hx_moe_max_concurrency(device), "helios::exl3::moe_max_concurrency"); }
 

@@ -137,6 +137,15 @@ int hx_exl3_reconstruct_had_slice(void* unpacked, const void* packed, const void
  * pack.cu:7-176); unpack writes symbols with the bits above K zero. */
 int hx_exl3_pack_trellis(void* packed, const void* unpacked, int rows, int cols, int K, hx_stream_t stream);
 int hx_exl3_unpack_trellis(void* unpacked, const void* packed, int rows, int cols, int K, hx_stream_t stream);
+/* Sign bits of fp16 values, 16 per column: packed[c] (uint16) bit i = sign bit of unpacked[16 c + i]
+ * (fp16), c < cols.  Replaces helios::exl3::pack_signs (src/cuda/quant/pack.cuh:36-44, pack.cu:180-233;
+ * the bit order is that of the reference kernel, which puts value i in bit i, whatever the comment in
+ * pack.cuh:36 says about bit 15). */
+int hx_pack_signs(void* packed, const void* unpacked, int cols, hx_stream_t stream);
+/* counts[0] += the number of infinities, counts[1] += the number of NaNs among numel values of x
+ * (dtype HX_DTYPE_HALF or HX_DTYPE_FLOAT); the caller zeroes counts first.  Replaces
+ * helios::exl3::count_inf_nan (src/cuda/quant/util.cuh:9-19, util.cu:54-116). */
+int hx_count_inf_nan(const void* x, unsigned long long* counts, uint64_t numel, int dtype, hx_stream_t stream);
 
 /* Row-wise Hadamard-128: y = H128(x) * scale / sqrt(128) on each consecutive 128-element group of a
  * rows x cols tensor of `dtype` (HX_DTYPE_HALF fp16, HX_DTYPE_FLOAT fp32; in place when

@@ -230,6 +230,30 @@ def moe_rows(x: np.ndarray, hidden: int, inter: int, topk_idx: np.ndarray, topk_
     return yr, yo
 
 
+def pack_signs(unpacked: np.ndarray, cols: int) -> np.ndarray:
+    """uint16 [cols] from fp16 bit patterns [cols * 16]: the reference kernel's loop
+    (src/cuda/quant/pack.cu:180-204): for each of the column's 16 values in order, shift the word
+    right by one and put the value's sign bit in bit 15, so value i ends in bit i."""
+    u = _u16(np.asarray(unpacked).reshape(-1))[:16 * cols].reshape(cols, 16)
+    out = np.zeros(cols, np.uint16)
+    for i in range(16):
+        out = (out >> np.uint16(1)) | (u[:, i] & np.uint16(0x8000))
+    return out
+
+
+def count_inf_nan(x: np.ndarray) -> tuple[int, int]:
+    """(infinities, NaNs) of an fp16 (uint16 bit patterns / float16) or fp32 array, by bit pattern: all
+    exponent bits set and a zero (inf) or non-zero (NaN) mantissa (src/cuda/quant/util.cu:54-80)."""
+    x = np.asarray(x)
+    if x.dtype in (np.float32, np.uint32):
+        v = x.view(np.uint32).reshape(-1) & np.uint32(0x7fffffff)
+        e = np.uint32(0x7f800000)
+    else:
+        v = _u16(x.reshape(-1)) & np.uint16(0x7fff)
+        e = np.uint16(0x7c00)
+    return int(np.count_nonzero(v == e)), int(np.count_nonzero(v > e))
+
+
 def cpu_linear_f32(x: np.ndarray, trellis, suh, svh, K: int, N: int, bits: int, cb: int, threads: int = 0):
     """CPU baseline: returns (y fp32 [M][N], seconds)."""
     x = _u16(x)

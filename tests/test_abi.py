@@ -76,6 +76,9 @@ def test_cpp_compat_header_compiles_and_links(tmp_path):
                    "    helios::exl3::had_r_128_dual(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1, 128,"
                    " helios::exl3::DType::Float, 1.0f, nullptr);\n"
                    "    helios::exl3::reconstruct_had_slice(nullptr, nullptr, nullptr, nullptr, 8, 8, 128, 128, 2, false, true, 0);\n"
+                   "    helios::exl3::pack_signs(nullptr, nullptr, 0);\n"
+                   "    unsigned long long* cnt = nullptr;\n"
+                   "    helios::exl3::count_inf_nan(nullptr, cnt, 0, helios::exl3::DType::Half);\n"
                    "  }\n  return 0;\n}\n")
     lib = Path(_lib.LIB_PATH)
     r = subprocess.run([hipcc, "-std=c++17", "-Werror", "-I", str(ROOT / "include"), str(src), "-o",

@@ -248,3 +248,52 @@ def test_gather_and_scatter_add_rows(hx, h):
     want = y0.copy()
     want[idx] = want[idx] + (w.astype(np.float32)[:, None] * add)
     assert np.array_equal(y.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("cols,offset", [(0, 0), (1, 0), (37, 0), (5000, 0), (999, 3)])
+def test_pack_signs(hx, cols, offset):
+    """hx_pack_signs bit-exact against the oracle; offset > 0 starts the fp16 buffer 2*offset bytes
+    into an allocation (not 16-byte aligned: the element-wise load path)."""
+    import torch
+    from oracle import oracle as O
+    r = np.random.default_rng(cols + offset)
+    u = r.integers(0, 65536, size=16 * cols + offset, dtype=np.uint16)
+    dev = _dev(u.view(np.float16))
+    src = dev[offset:]
+    packed = torch.full((max(cols, 1),), 0x1234, dtype=torch.int16, device="cuda")
+    hx.pack_signs(packed, src, cols)
+    torch.cuda.synchronize()
+    got = packed.cpu().numpy().view(np.uint16)[:cols]
+    assert np.array_equal(got, O.pack_signs(u[offset:], cols))
+    if cols == 0:
+        assert packed.cpu().numpy().view(np.uint16)[0] == 0x1234  # nothing written
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("n,offset", [(4096, 0), (1, 0), (3_000_001, 0), (100_003, 1)])
+def test_count_inf_nan(hx, dtype, n, offset):
+    """hx_count_inf_nan against the oracle on values with sprinkled infinities and NaNs (including
+    the reference test's +inf / -inf / NaN pattern), aligned and unaligned buffers, and the
+    accumulate-into-counts contract (a second call adds the same counts again)."""
+    import torch
+    from oracle import oracle as O
+    r = np.random.default_rng(n + offset)
+    if dtype == "f16":
+        x = r.standard_normal(n + offset).astype(np.float16)
+        specials = np.array([np.inf, -np.inf, np.nan], np.float16)
+    else:
+        x = r.standard_normal(n + offset).astype(np.float32)
+        specials = np.array([np.inf, -np.inf, np.nan], np.float32)
+    pos = r.integers(offset, n + offset, size=min(n, 97))
+    x[pos] = specials[r.integers(0, 3, size=pos.size)]
+    if n >= 4096:
+        x[offset + 17], x[offset + 900], x[offset + 2000] = specials[0], specials[1], specials[2]
+    want = O.count_inf_nan(x[offset:])
+    src = _dev(x)[offset:]
+    counts = torch.zeros(2, dtype=torch.int64, device="cuda")
+    hx.count_inf_nan(src, counts)
+    torch.cuda.synchronize()
+    assert tuple(int(v) for v in counts.cpu()) == want
+    hx.count_inf_nan(src, counts)
+    torch.cuda.synchronize()
+    assert tuple(int(v) for v in counts.cpu()) == (2 * want[0], 2 * want[1])

@@ -575,3 +575,33 @@ def test_h128_register_sign_pattern():
             par = (bin(c & j & 7).count("1") + ((c >> 3) & g & 1) + ((nb & 1) & (g >> 1)) + ((nb >> 1) & kk & 1)
                    + ((nb >> 2) & (kk >> 1) & 1)) & 1
             assert H[k, n] == (-1 if par else 1)
+
+
+def test_pack_signs_oracle():
+    """pack_signs: the reference kernel's shift-in loop puts value i's sign in bit i.  Pinned by a
+    worked example of that loop (only the first value negative -> 0x0001, only the last -> 0x8000,
+    alternating signs starting negative -> 0x5555) and, for random columns, by the bit-position formula
+    sum_i sign_i << i computed independently with numpy."""
+    def col(signs):
+        return np.array([0xbc00 if s else 0x3c00 for s in signs], np.uint16)  # -1.0 / +1.0
+    assert O.pack_signs(col([1] + [0] * 15), 1)[0] == 0x0001
+    assert O.pack_signs(col([0] * 15 + [1]), 1)[0] == 0x8000
+    assert O.pack_signs(col([1, 0] * 8), 1)[0] == 0x5555
+    r = np.random.default_rng(5)
+    u = r.integers(0, 65536, size=(300, 16), dtype=np.uint16)
+    want = ((u >> 15).astype(np.uint32) << np.arange(16, dtype=np.uint32)).sum(axis=1).astype(np.uint16)
+    assert np.array_equal(O.pack_signs(u.reshape(-1), 300), want)
+
+
+def test_count_inf_nan_oracle():
+    """count_inf_nan: every fp16 bit pattern against numpy's isinf/isnan, fp32 specials, and the
+    reference test's known answer (test_reconstruct.cpp:468-493: 4096 values of 0.5 with +inf at 17,
+    -inf at 900 and a NaN at 2000 give inf = 2, nan = 1)."""
+    allh = np.arange(65536, dtype=np.uint16)
+    f = allh.view(np.float16)
+    assert O.count_inf_nan(allh) == (int(np.isinf(f).sum()), int(np.isnan(f).sum())) == (2, 2046)
+    kat = np.full(4096, 0x3800, np.uint16)
+    kat[17], kat[900], kat[2000] = 0x7c00, 0xfc00, 0x7e00
+    assert O.count_inf_nan(kat) == (2, 1)
+    f32 = np.array([1.0, np.inf, -np.inf, np.nan, -np.nan, 3.4e38, 0.0], np.float32)
+    assert O.count_inf_nan(f32) == (2, 2)
