@@ -30,9 +30,9 @@ namespace hx {
 constexpr int LIN_PF = 2;   // up to 4 bits
 constexpr int LIN_PFW = 4;  // wider
 
-// Stream-K for one row when the split-K grid is one workgroup per column group and does not spread
-// evenly over the 256 CUs (the lm_head, 4096 -> 151552: 1184 groups, 4 or 5 workgroups per CU, and
-// the CUs with 4 go idle while those with 5 finish): 1024 workgroups (4 on every CU) take equal runs
+// Stream-K for one row over more than 1024 column groups that do not spread evenly over the 256 CUs
+// (the lm_head, 4096 -> 151552: 1184 groups; one workgroup per group put 4 or 5 on a CU, and the CUs
+// with 4 went idle while those with 5 finished): 1024 workgroups (4 on every CU) take equal runs
 // of the (column group, 128-k block) units.  lm_head in a graph of 20 calls on one box: 101-104 ->
 // 96 us; 2048 workgroups: no gain.  A grid already even over the CUs (K = 16384 -> 32768, 2-bit:
 // 4 splits, 1024 workgroups) measured 2 us slower as stream-K, and small linears are bound by their

@@ -11,19 +11,28 @@ template <int BITS>
 hipError_t launch_gemv_cb(int cb, const GemvArgs& g, const _Float16* svh, void* y, bool y_fp32, hipStream_t st);
 
 // Split-K plan: grid = (N / 128) column groups x (K / kc) splits.  kc shrinks from the largest
-// chunk whose activation block (M x kc fp16) fits 32 KiB of LDS until the grid holds ~2 workgroups
-// per CU, but not below 512: each split adds a partial sum that the last arriver gathers, on the
-// critical path of a small linear.  Measured at K = 4096, M = 1: config 1 (N = 2048, 16 column
-// groups) 13.2 us with 32 splits of 128, 9.0 us with 8 splits of 512, 11.5 us with 4 of 1024;
-// config 2 (N = 12288) best at 8 splits too (15.0 us; 20.6 us with 16 splits).
+// chunk whose activation block (M x kc fp16) fits 32 KiB of LDS, in two stages:
+//  1. toward 2048 workgroups (8 per CU) while the chunks stay at least 2048 long: a long stream
+//     wants the occupancy (2-bit K = 16384 -> N = 32768: 2 splits 81.3-82.3 us, 4 splits 77.1-77.4,
+//     8 splits 73.2, graphs of 20 calls on one box);
+//  2. toward 512 workgroups (2 per CU), not below 512: each split adds a partial sum that the last
+//     arriver gathers, on the critical path of a small linear.  Measured at K = 4096, M = 1:
+//     config 1 (N = 2048, 16 column groups) 13.2 us with 32 splits of 128, 9.0 us with 8 splits of
+//     512, 11.5 us with 4 of 1024; config 2 (N = 12288) best at 8 splits too (13.4 us; 13.8 us with 16).
 constexpr int GEMV_KC_FLOOR = 512;
+constexpr int GEMV_LONG_KC = 2048;
 
 static void split_plan(int M, int K, int N, int* splits, int* kc)
 {
     const int groups = N / 128;
     const int cap = 16384 / (M < 1 ? 1 : M);
     int c = gemv_kc_for(K, cap);
-    const int min_wg = 512, floor_kc = GEMV_KC_FLOOR;
+    while (c > GEMV_LONG_KC && (long)groups * (K / c) < 8 * GEMV_CUS) {
+        const int smaller = gemv_kc_for(K, c - 128);
+        if (smaller == c || smaller < GEMV_LONG_KC) break;
+        c = smaller;
+    }
+    const int min_wg = 2 * GEMV_CUS, floor_kc = GEMV_KC_FLOOR;
     while (c > 128 && c > floor_kc && (long)groups * (K / c) < min_wg) {
         // one shrink step can skip past the floor when K has no multiple-of-128 divisor in
         // [floor_kc, c) (K = 1152: 1152 -> 384): stop at c then
@@ -42,7 +51,7 @@ GemvPlan gemv_plan(int M, int K, int N)
     const int groups = N / 128;
     const long long nb = K / 128, blocks = (long long)groups * nb;
     // unit and workgroup indices are multiplied in 32 bits in the kernel: blocks * wgs < 2^31
-    if (M == 1 && p.splits == 1 && groups > GEMV_SK_WGS && groups % GEMV_CUS != 0 &&
+    if (M == 1 && groups > GEMV_SK_WGS && groups % GEMV_CUS != 0 &&
         blocks * GEMV_SK_WGS < (1LL << 31) &&
         (blocks + GEMV_SK_WGS - 1) / GEMV_SK_WGS <= 16384 / 128) {
         p.sk_wgs = GEMV_SK_WGS;
