@@ -8,16 +8,22 @@
 
 namespace hx {
 
-// Output epilogue for one 128-column group: y[m][cg*128 + c] = svh . H128(colsum[m][:])
+// This lane's two svh entries of column group cg (columns cg*128 + 2*lane, +1).  Requested when the
+// group's work starts: read in the epilogue, the load would be one more dependent round trip after
+// the split-K arrival and gather.
+HX_INLINE hx_h2 svh_pair(const _Float16* svh, int cg)
+{
+    return *reinterpret_cast<const hx_h2*>(svh + cg * 128 + 2 * (threadIdx.x & 63));
+}
+
+// Output epilogue for one 128-column group: y[m][cg*128 + c] = svh . H128(colsum[m][:]), sv = svh_pair
 //   fp32 out: had_ff_r_128_inner<false,true> (transform in fp32, times float(svh))
 //   fp16 out: had_fh_r_128_inner<false,true> (transform, round to fp16, fp16 multiply by svh)
 template <int MT>
-__device__ void linear_epilogue(const float* colsum, const _Float16* svh, void* y, int M, int N,
-                                int cg, bool y_fp32)
+__device__ void linear_epilogue(const float* colsum, hx_h2 sv, void* y, int M, int N, int cg, bool y_fp32)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = cg * 128 + 2 * lane;
-    hx_h2 sv = *reinterpret_cast<const hx_h2*>(svh + c);
     for (int m = wave; m < M && m < MT; m += hx_nwaves()) {
         float v0 = colsum[m * 128 + 2 * lane], v1 = colsum[m * 128 + 2 * lane + 1];
         hx_had128_wave(v0, v1);
@@ -41,13 +47,14 @@ __global__ __launch_bounds__(GEMV_THREADS) void linear_gemv_kernel(GemvArgs g, c
     const int groups = g.N >> 7;
     const int cg = blockIdx.x % groups;
     const int s = blockIdx.x / groups;
+    const hx_h2 sv = svh_pair(svh, cg);
     gemv_split_sum<BITS, CB, MT>(g, cg, s, a_lds, colsum);
     if (g.splits > 1) {
         publish_partial<MT>(g.partial, g.M, g.N, cg, s, colsum);
         if (!arrive_last(&g.counter[cg], g.splits)) return;
         gather_partials<MT>(g.partial, g.M, g.N, g.splits, cg, colsum);
     }
-    linear_epilogue<MT>(colsum, svh, y, g.M, g.N, cg, y_fp32);
+    linear_epilogue<MT>(colsum, sv, y, g.M, g.N, cg, y_fp32);
 }
 
 // Workgroup owning unit b of `units` split evenly over `wgs` workgroups (workgroup i takes units
@@ -67,6 +74,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void linear_gemv_stream_kernel(GemvAr
     const unsigned b1 = (i + 1) * T / G;
     for (unsigned b = i * T / G; b < b1;) {
         const unsigned cg = b / nb, e = min(b1, (cg + 1) * nb);
+        const hx_h2 sv = svh_pair(svh, cg);
         gemv_range<BITS, CB, 1, 1, LIN_PF, LIN_PFW, true>(g, cg, (b - cg * nb) * 128, (e - b) * 128, a_lds, colsum);
         const unsigned first = stream_owner(cg * nb, T, G), last = stream_owner(cg * nb + nb - 1, T, G);
         bool finish = true;
@@ -75,7 +83,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void linear_gemv_stream_kernel(GemvAr
             finish = arrive_last(&g.counter[cg], last - first + 1);
             if (finish) gather_partials<1>(g.partial, 1, g.N, last - first + 1, cg, colsum);
         }
-        if (finish) linear_epilogue<1>(colsum, svh, y, 1, g.N, cg, y_fp32);
+        if (finish) linear_epilogue<1>(colsum, sv, y, 1, g.N, cg, y_fp32);
         __syncthreads();  // colsum is read before the next group overwrites it
         b = e;
     }
