@@ -292,7 +292,6 @@ __global__ __launch_bounds__(PERM_THREADS) void permute_count_kernel(const int64
                                                                      int64_t* expert_count)
 {
     __shared__ int hist[PERM_EMAX];
-    __shared__ int tot[PERM_EMAX];
     __shared__ bool last;
     const int t = threadIdx.x, chunks = gridDim.x;
     for (int e = t; e < PERM_EMAX; e += PERM_THREADS) hist[e] = 0;
@@ -313,29 +312,51 @@ __global__ __launch_bounds__(PERM_THREADS) void permute_count_kernel(const int64
     }
     __syncthreads();
     if (!last) return;
-    for (int e = t; e < E; e += PERM_THREADS) {
-        int run = 0;
-        for (int c = 0; c < chunks; ++c) {
-            const int v = __hip_atomic_load(&counts[c * E + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            offs[c * E + e] = run;
-            run += v;
+    // one expert per thread (E <= PERM_EMAX <= PERM_THREADS); the chunk counts are read PB at a time,
+    // all PB loads in flight together (one round trip per PB chunks instead of one per chunk)
+    constexpr int PB = 16;
+    static_assert(PERM_EMAX <= PERM_THREADS, "one expert per thread");
+    auto load_counts = [&](int c0, int (&v)[PB]) {
+#pragma unroll
+        for (int j = 0; j < PB; ++j)
+            v[j] = c0 + j < chunks ? __hip_atomic_load(&counts[(c0 + j) * E + t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                   : 0;
+    };
+    int n_e = 0;  // routes of expert t over all chunks
+    if (t < E)
+        for (int c0 = 0; c0 < chunks; c0 += PB) {
+            int v[PB];
+            load_counts(c0, v);
+#pragma unroll
+            for (int j = 0; j < PB; ++j) n_e += v[j];
         }
-        tot[e] = run;
+    // exclusive scan over the experts: inclusive scan per wave, then the totals of the waves below
+    __shared__ int wave_sum[PERM_THREADS / 64];
+    const int lane = t & 63, wave = t >> 6;
+    int inc = n_e;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += u;
     }
+    if (lane == 63) wave_sum[wave] = inc;
     __syncthreads();
-    if (t == 0) {
-        int acc = 0;
-        for (int e = 0; e < E; ++e) {
-            const int v = tot[e];
-            tot[e] = acc;
-            acc += v;
-            expert_count[e] = v;
+    int first = inc - n_e;
+    for (int k = 0; k < wave; ++k) first += wave_sum[k];
+    if (t <= E) expert_count[t] = t < E ? n_e : 0;
+    // each chunk's first position per expert: the expert's first position plus the routes of the
+    // chunks before (the counts again, now cached)
+    if (t < E)
+        for (int c0 = 0; c0 < chunks; c0 += PB) {
+            int v[PB];
+            load_counts(c0, v);
+#pragma unroll
+            for (int j = 0; j < PB; ++j)
+                if (c0 + j < chunks) {
+                    offs[(c0 + j) * E + t] = first;
+                    first += v[j];
+                }
         }
-        expert_count[E] = 0;
-    }
-    __syncthreads();
-    for (int e = t; e < E; e += PERM_THREADS)
-        for (int c = 0; c < chunks; ++c) offs[c * E + e] += tot[e];
 }
 
 __global__ __launch_bounds__(PERM_THREADS) void permute_scatter_kernel(const int64_t* ids, const _Float16* w, int total,
