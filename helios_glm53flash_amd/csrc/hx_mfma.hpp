@@ -133,7 +133,7 @@ __device__ __forceinline__ void mfma_tile_q(const _Float16* A, long lda, int row
                                             int N, int tn0, Smem& sm, hx_f4 (&acc)[BM / 16][2],
                                             const float* rs_src = nullptr, int rs_n = 0)
 {
-    static_assert(BM == 32 || BM == 64 || BM == 128, "row tile");
+    static_assert(BM == 32 || BM == 64 || BM == 96 || BM == 128, "row tile");
     constexpr int RB = BM / 16;
     constexpr int NA = BM / 32;   // 16-byte A loads per thread per chunk
     constexpr int NW = 8 * BITS;

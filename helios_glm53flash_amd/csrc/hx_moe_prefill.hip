@@ -2,7 +2,7 @@
 // token-by-expert permutation).
 //
 // Flow (all stream-ordered, no host synchronisation):
-//   plan       expert_count -> per-row expert id and 128/64/32-row tile jobs per expert
+//   plan       expert_count -> per-row expert id and 128/96/64/32-row tile jobs per expert
 //   gather     xg[r] = fp16(H(x[token_sorted[r]] . suh_g[e])), xu[r] likewise (H on the matrix
 //              cores), and their row sums per 128-column block
 //   gate/up    G = xg . W_g[e], U = xu . W_u[e] (quarter-operand MFMA tiles), then in the same
@@ -21,7 +21,7 @@ namespace hx {
 static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Job {
-    int expert, row0, rows, bm;  // bm: row tile (128, or 64 / 32 for a remainder of at most 64 / 32 rows)
+    int expert, row0, rows, bm;  // bm: row tile (128, or 96 / 64 / 32 for a remainder of at most that many rows)
 };
 
 void MoeWs::prefill_layout(size_t o)
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(512) void prefill_plan_kernel(const int64_t* expert
     if (blockIdx.x == 0) {
         for (int k = 0; k < nj; ++k) {
             const int rows = min(MF_BM, c - k * MF_BM);
-            jobs[j0 + k] = Job{t, r0 + k * MF_BM, rows, rows <= 32 ? 32 : rows <= 64 ? 64 : MF_BM};
+            jobs[j0 + k] = Job{t, r0 + k * MF_BM, rows, rows <= 32 ? 32 : rows <= 64 ? 64 : rows <= 96 ? 96 : MF_BM};
         }
         if (t == 511) *njobs = joff[511];
     }
@@ -261,6 +261,7 @@ __global__ __launch_bounds__(MF_THREADS, QT_OCC) void grouped_gemm_kernel(Groupe
     case B:                                                                                \
         if (job.bm == 32) grouped_tile<B, CB, 32>(g, job, proj, cg, sm);                    \
         else if (job.bm == 64) grouped_tile<B, CB, 64>(g, job, proj, cg, sm);               \
+        else if (job.bm == 96) grouped_tile<B, CB, 96>(g, job, proj, cg, sm);               \
         else grouped_tile<B, CB, MF_BM>(g, job, proj, cg, sm);                              \
         break;
     switch (bits) {
@@ -451,6 +452,7 @@ __global__ __launch_bounds__(MF_THREADS, QT_OCC) void grouped_gu_kernel(GuArgs a
     const Job job = a.jobs[job_i];
     if (job.bm == 32) gu_fused<CB, 32>(a, job, cg, sm);
     else if (job.bm == 64) gu_fused<CB, 64>(a, job, cg, sm);
+    else if (job.bm == 96) gu_fused<CB, 96>(a, job, cg, sm);
     else gu_fused<CB, MF_BM>(a, job, cg, sm);
 }
 

@@ -133,7 +133,7 @@ def test_moe_prefill_config4_zipf(hx, config4):
 
 def test_moe_prefill_config4_every_job(hx, config4):
     """Config 4, every grouped-GEMM job: the prefill cuts each expert's rows into 128-row jobs (the
-    remainder as a 32-, 64- or 128-row tile); the first and last row of every (expert, job) pair are
+    remainder as a 32-, 64-, 96- or 128-row tile); the first and last row of every (expert, job) pair are
     compared against the dense numpy expert (decoded W_hat from the oracle's reconstruct, the fp16
     rounding points of exl3_moe_kernel.cuh:85-262, pinned by test_moe_rows_matches_dense_numpy) as
     per-route contributions, and the layer's y_routed equals the rank-order sum of those
@@ -151,7 +151,8 @@ def test_moe_prefill_config4_every_job(hx, config4):
             jobs.append((e, int(off[e]) + j0, int(off[e]) + min(j0 + 128, int(cnt[e])) - 1))
     # the workload has remainder jobs of every tile height, and 3-bit remainders off the 32-row grid
     rem = [int(cnt[e]) % 128 for e in range(E)]
-    assert any(0 < r <= 32 for r in rem) and any(32 < r <= 64 for r in rem) and any(r > 64 for r in rem)
+    assert any(0 < r <= 32 for r in rem) and any(32 < r <= 64 for r in rem)
+    assert any(64 < r <= 96 for r in rem) and any(r > 96 for r in rem)
     assert any(e >= 144 and cnt[e] > 128 and cnt[e] % 32 for e in range(E))
     shapes = [(hidden, inter), (hidden, inter), (inter, hidden)]
 
