@@ -212,24 +212,28 @@ hipError_t launch_routing(const _Float16* scores, const _Float16* bias, int64_t*
 // Deterministic counting sort of routing slots by expert (reference glue2.cu:244-293 computes the
 // same expert_count / token_sorted / weight_sorted / route_to_sorted, but places slots within an
 // expert with an atomic cursor).  Here slot i of expert e lands at offset[e] + (number of slots
-// i' < i with ids[i'] == e): ascending flat index within each expert.  One 1024-lane workgroup;
-// chunks of 1024 slots are ranked wave by wave in order.
+// i' < i with ids[i'] == e): ascending flat index within each expert.  One 1024-lane workgroup per
+// chunk of 1024 slots (permute_kernel: one workgroup for all chunks, in order).
 constexpr int PERM_THREADS = 1024;
 constexpr int PERM_EMAX = 512;
 
 // Scatter of the routes [base, base + PERM_THREADS) given each expert's next free position in
-// cursor[] (LDS): the waves rank their lanes by ballot and run in wave order, so positions ascend
-// with the flat index within each expert.
+// cursor[] (LDS, advanced past the chunk on return): each wave ranks its lanes by ballot and counts
+// its routes per expert; a wave's group of an expert starts after the groups of the waves before it,
+// so positions ascend with the flat index within each expert.
 __device__ __forceinline__ void permute_scatter_chunk(const int64_t* ids, const _Float16* w, int total, int topk, int E,
                                                       int base, int* cursor, int64_t* token_sorted,
                                                       _Float16* weight_sorted, int64_t* route_to_sorted)
 {
+    constexpr int NW = PERM_THREADS / 64;
+    __shared__ int wfirst[NW * PERM_EMAX];  // [wave][expert]: the wave's group size, then its first position
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     const int i = base + t;
     const int64_t e64 = i < total ? ids[i] : -1;
     const bool valid = e64 >= 0 && e64 < E;
     const int e = valid ? (int)e64 : -1;
+    for (int k = t; k < NW * E; k += PERM_THREADS) wfirst[(k / E) * PERM_EMAX + k % E] = 0;
     int rank = 0, group = 0;
     bool leader = false;
     uint64_t remaining = __ballot(valid);
@@ -244,17 +248,27 @@ __device__ __forceinline__ void permute_scatter_chunk(const int64_t* ids, const 
         }
         remaining &= ~m;
     }
-    for (int wv = 0; wv < PERM_THREADS / 64; ++wv) {
-        if (wave == wv && valid) {
-            const int pos = cursor[e] + rank;
-            __builtin_amdgcn_wave_barrier();
-            if (leader) cursor[e] += group;
-            token_sorted[pos] = i / topk;
-            weight_sorted[pos] = w[i];
-            if (route_to_sorted) route_to_sorted[i] = pos;
+    __syncthreads();
+    if (leader) wfirst[wave * PERM_EMAX + e] = group;
+    __syncthreads();
+    for (int x = t; x < E; x += PERM_THREADS) {
+        int run = cursor[x];
+#pragma unroll
+        for (int wv = 0; wv < NW; ++wv) {
+            const int g = wfirst[wv * PERM_EMAX + x];
+            wfirst[wv * PERM_EMAX + x] = run;
+            run += g;
         }
-        __syncthreads();
+        cursor[x] = run;
     }
+    __syncthreads();
+    if (valid) {
+        const int pos = wfirst[wave * PERM_EMAX + e] + rank;
+        token_sorted[pos] = i / topk;
+        weight_sorted[pos] = w[i];
+        if (route_to_sorted) route_to_sorted[i] = pos;
+    }
+    __syncthreads();  // wfirst and cursor are read before a next chunk rewrites them
 }
 
 __global__ __launch_bounds__(PERM_THREADS) void permute_kernel(const int64_t* ids, const _Float16* w, int total,
