@@ -240,13 +240,15 @@ def test_moe_prefill_topk_variants(hx, topk):
 
 
 @pytest.mark.parametrize("cb", [2, 1])
-@pytest.mark.parametrize("T", [5, 160])
+@pytest.mark.parametrize("T", [5, 160, 404])
 def test_moe_grouped_every_bit_width(hx, cb, T):
     """hx_moe_grouped with per-expert bit widths that cover 1..8 in every projection (expert e:
     gate 1 + e % 8, up 1 + (e + 3) % 8, down 1 + (e + 5) % 8), codebook mul1 (cb 2) and MCG (cb 1),
-    on the few-token decode kernel (T = 5) and the grouped MFMA path (T = 160).  Tokens 0..3 route
-    to every expert; in the longer batch the other tokens favour experts 0..3, which then take
-    128-row tiles besides the 32-row ones of the others."""
+    on the few-token decode kernel (T = 5) and the grouped MFMA path (T = 160, 404).  Tokens 0..3
+    route to every expert.  At T = 160 the other tokens favour experts 0..3, which then take 128-row
+    tiles besides the 32-row ones of the others; at T = 404 token t >= 4 routes to experts
+    (t + k) % 8, k < 4, so experts 0..7 (every width in every projection) get 201 or 200 rows: a
+    128-row tile and a 96-row tile each."""
     import torch
     from oracle import oracle as O
     exl3, moe = hx
@@ -258,11 +260,19 @@ def test_moe_grouped_every_bit_width(hx, cb, T):
     s = r.standard_normal((T, E))
     for t in range(4):  # tokens 0..3 route to experts 4t..4t+3: every expert, so every width, is used
         s[t, 4 * t:4 * t + 4] += 6.0
-    s[4:, :4] += 3.0  # the hot experts of the longer batch
+    if T == 404:
+        for t in range(4, T):
+            s[t, [(t + k) % 8 for k in range(4)]] += 6.0
+    else:
+        s[4:, :4] += 3.0  # the hot experts of the longer batch
     sh = s.astype(np.float16)
     idx, w = O.routing(sh, topk, 2.5)
     used = set(int(e) for e in idx.reshape(-1))
     assert len(used) == E, "every expert (so every width) is routed"
+    if T == 404:
+        c = np.bincount(idx.reshape(-1), minlength=E)
+        for p in range(3):
+            assert {bits[e][p] for e in range(E) if 64 < c[e] % 128 <= 96} == set(range(1, 9)), c
     x = torch.from_numpy(xh).cuda()
     idx_d = torch.from_numpy(idx).cuda()
     w_d = torch.from_numpy(w.view(np.float16)).cuda()
