@@ -127,11 +127,11 @@ HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, in
                          float& w_out, Hook after_loads = Hook())
 {
     const int lane = threadIdx.x & 63;
+    constexpr int PER = 8;  // candidates per lane: E <= 512
     if (!bias) {
         // key = the fp16 logit itself: its monotone 16-bit encoding and the complemented index fit
         // one u32 (larger = higher logit, then lower index; +0 above -0 as in the fp32 encoding)
-        constexpr int PER = 8;  // E <= 512
-        uint32_t cand[PER];
+        uint32_t c[PER];
         uint16_t raw[PER];
         // all loads first (clamped addresses, no branches) so their latencies overlap
 #pragma unroll
@@ -142,33 +142,42 @@ HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, in
             const int e = lane + 64 * i;
             uint32_t h = raw[i];
             h = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
-            cand[i] = e < E ? (h << 16) | (0xffffu - (uint32_t)e) : 0u;
+            c[i] = e < E ? (h << 16) | (0xffffu - (uint32_t)e) : 0u;
         }
-        float sum = 0.0f;
-        e_out = 0;
-        w_out = 0.0f;
+        // each lane's candidates in descending order (Batcher's 19-comparator network for 8), so a
+        // round only compares the lanes' heads: the wave's largest head is selection k, and its lane
+        // (keys are unique) drops its head
+        auto cas = [&](int i, int j) {
+            const uint32_t hi = max(c[i], c[j]), lo = min(c[i], c[j]);
+            c[i] = hi;
+            c[j] = lo;
+        };
+        cas(0, 1); cas(2, 3); cas(4, 5); cas(6, 7);
+        cas(0, 2); cas(1, 3); cas(4, 6); cas(5, 7);
+        cas(1, 2); cas(5, 6);
+        cas(0, 4); cas(1, 5); cas(2, 6); cas(3, 7);
+        cas(2, 4); cas(3, 5);
+        cas(1, 2); cas(3, 4); cas(5, 6);
+        uint32_t sel = 0;
         for (int k = 0; k < topk; ++k) {
-            uint32_t best = cand[0];
+            const uint32_t best = hx_wave_max_u32(c[0]);
+            const bool own = c[0] == best;
 #pragma unroll
-            for (int i = 1; i < PER; ++i) best = max(best, cand[i]);
-            best = hx_wave_max_u32(best);
-#pragma unroll
-            for (int i = 0; i < PER; ++i)
-                if (cand[i] == best) cand[i] = 0;
-            uint32_t h = best >> 16;
-            h = (h & 0x8000u) ? (h & 0x7fffu) : (~h & 0xffffu);
-            const float o = sigmoid_stable((float)u16_as_h((uint16_t)h));
-            sum += o;
-            if (lane == k) {
-                e_out = (int)(0xffffu - (best & 0xffffu));
-                w_out = o;
-            }
+            for (int i = 0; i + 1 < PER; ++i) c[i] = own ? c[i + 1] : c[i];
+            c[PER - 1] = own ? 0u : c[PER - 1];
+            sel = lane == k ? best : sel;
         }
+        // the sigmoid of selection k on lane k; their sum in selection order
+        uint32_t h = sel >> 16;
+        h = (h & 0x8000u) ? (h & 0x7fffu) : (~h & 0xffffu);
+        const float o = sigmoid_stable((float)u16_as_h((uint16_t)h));
+        float sum = 0.0f;
+        for (int k = 0; k < topk; ++k) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, o), k));
         sum += 1e-20f;
-        w_out = (float)(_Float16)(w_out * scale / sum);
+        e_out = lane < topk ? (int)(0xffffu - (sel & 0xffffu)) : 0;
+        w_out = lane < topk ? (float)(_Float16)(o * scale / sum) : 0.0f;
         return;
     }
-    constexpr int PER = 8;  // E <= 512
     uint64_t cand[PER];
     float payload[PER];
     _Float16 sv[PER], bv[PER];
@@ -185,13 +194,8 @@ HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, in
         cand[i] = 0;
         payload[i] = 0.0f;
         if (e < E) {
-            const float logit = (float)sv[i];
-            float key = logit;
-            payload[i] = logit;
-            if (bias) {
-                payload[i] = sigmoid_stable(logit);
-                key = payload[i] + (float)bv[i];
-            }
+            payload[i] = sigmoid_stable((float)sv[i]);
+            const float key = payload[i] + (float)bv[i];
             uint32_t u = __float_as_uint(key);
             u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
             cand[i] = ((uint64_t)u << 32) | (uint64_t)(0xfffffu - (uint32_t)e + 1u);
@@ -201,31 +205,28 @@ HX_INLINE void wave_topk(const _Float16* scores, const _Float16* bias, int E, in
     e_out = 0;
     w_out = 0.0f;
     for (int k = 0; k < topk; ++k) {
-        uint64_t best = 0;
-        float best_p = 0.0f;
+        uint64_t b = 0;
+        float bp = 0.0f;
 #pragma unroll
         for (int i = 0; i < PER; ++i)
-            if (cand[i] > best) {
-                best = cand[i];
-                best_p = payload[i];
+            if (cand[i] > b) {
+                b = cand[i];
+                bp = payload[i];
             }
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const uint64_t ob = __shfl_xor(best, m, 64);
-            const float op = __shfl_xor(best_p, m, 64);
-            if (ob > best) {
-                best = ob;
-                best_p = op;
-            }
-        }
-        const int e = (int)(0xfffffu + 1u - (uint32_t)(best & 0xffffffffu));
+        // the wave's largest 64-bit key in two 32-bit DPP reductions: the largest key word, then
+        // the largest index word (lowest expert) among the lanes holding that key word
+        const uint32_t hi = hx_wave_max_u32((uint32_t)(b >> 32));
+        const uint32_t lo = hx_wave_max_u32((uint32_t)(b >> 32) == hi ? (uint32_t)b : 0u);
+        const uint64_t best = ((uint64_t)hi << 32) | lo;
+        const uint64_t owner = __ballot(b == best);
+        const float o = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bp),
+                                                                            (int)__ffsll((unsigned long long)owner) - 1));
 #pragma unroll
         for (int i = 0; i < PER; ++i)
             if (cand[i] == best) cand[i] = 0;
-        const float o = bias ? best_p : sigmoid_stable(best_p);
         sum += o;
         if (lane == k) {
-            e_out = e;
+            e_out = (int)(0xfffffu + 1u - lo);
             w_out = o;
         }
     }

@@ -84,6 +84,52 @@ def test_moe_layer_router_bias(hx, E, T):
     _run_layer(hx, E=E, hidden=256, inter=256, topk=8, T=T, bits=2, shared_bits=2, seed=700 + E + T, bias=True)
 
 
+@pytest.mark.parametrize("E,T", [(288, 1), (288, 4), (288, 8), (64, 2)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_decode_router_outputs_bit_exact(hx, E, T, bias):
+    """The few-token layer kernel's own top-k: its router outputs (kept in the workspace after the
+    64 KiB counter area: indices [T*topk] int64, then the fp16 weights at the next 256-byte
+    boundary) equal the stand-alone routing kernel's bit for bit and the oracle's indices
+    (routing.cu:211-329), with ties at the top (equal logits: the lower expert first) and, for
+    T > 1, a token whose logits are all equal."""
+    import torch
+    from oracle import oracle as O
+    exl3, moe = hx
+    topk, hidden = 8, 256
+    ex = moe.ExpertSet.synthetic(E, hidden, 256, 2, seed=900 + E)
+    sh = moe.synthetic_dense_mlp(hidden, 256, 2, seed=901)
+    layer = moe.MoeLayer(ex, sh, topk=topk)
+    r = np.random.default_rng(902 + E + T + int(bias))
+    s = r.standard_normal((T, E)).astype(np.float16)
+    s[0, 10] = s[0, 3] = np.float16(3.0)
+    if T > 1:
+        s[1, :] = np.float16(0.25)
+    b = (r.standard_normal(E) * 0.05).astype(np.float16) if bias else None
+    s_d = torch.from_numpy(s).cuda()
+    b_d = torch.from_numpy(b).cuda() if bias else None
+    x = torch.from_numpy((r.standard_normal((T, hidden)) * 0.5).astype(np.float16)).cuda()
+    ws = torch.zeros(layer.workspace_bytes(T), dtype=torch.uint8, device="cuda")
+    layer(x, s_d, bias=b_d, ws=ws)
+    idx = torch.empty((T, topk), dtype=torch.int64, device="cuda")
+    w = torch.empty((T, topk), dtype=torch.float16, device="cuda")
+    exl3.routing_ds3_nogroup(s_d, b_d, idx, w, T, E, topk, 2.5)
+    torch.cuda.synchronize()
+    R = T * topk
+    o_idx = 64 * 1024
+    o_w = (o_idx + 8 * R + 255) // 256 * 256
+    wsh = ws.cpu().numpy()
+    got_i = wsh[o_idx:o_idx + 8 * R].view(np.int64).reshape(T, topk)
+    got_w = wsh[o_w:o_w + 2 * R].view(np.uint16).reshape(T, topk)
+    assert np.array_equal(got_i, idx.cpu().numpy())
+    assert np.array_equal(got_w, w.cpu().numpy().view(np.uint16))
+    ri, _ = O.routing(s, topk, 2.5, b)
+    assert np.array_equal(got_i, ri)
+    if not bias:
+        assert got_i[0, 0] == 3 and got_i[0, 1] == 10
+        if T > 1:
+            assert list(got_i[1]) == list(range(topk))
+
+
 def test_empty_batches_are_noops(hx):
     """tokens == 0 / M == 0 through the layer, the grouped call's Python mirror and the linear: no
     launch, no error, even with the null data pointers of empty tensors."""
