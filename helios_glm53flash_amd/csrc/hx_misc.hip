@@ -171,18 +171,21 @@ __global__ __launch_bounds__(64) void routing_topk_kernel(const _Float16* scores
     int e_sel = 0;
     float sum = 0.0f;
     for (int k = 0; k < K; ++k) {
-        uint64_t best = 0;
-        float best_a = 0.0f;
+        uint64_t b = 0;
+        float ba = 0.0f;
 #pragma unroll
         for (int i = 0; i < PER; ++i)
-            if (cand[i] > best) { best = cand[i]; best_a = act[i]; }
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            uint64_t ob = __shfl_xor(best, m, 64);
-            float oa = __shfl_xor(best_a, m, 64);
-            if (ob > best) { best = ob; best_a = oa; }
-        }
-        const int e = (int)(0xfffffu + 1u - (uint32_t)(best & 0xffffffffu));
+            if (cand[i] > b) { b = cand[i]; ba = act[i]; }
+        // the wave's largest 64-bit key in two 32-bit DPP reductions (the key word, then the index
+        // word among the lanes holding that key word); its activation from the owning lane (K <= E
+        // valid candidates, so the key is nonzero and has one owner)
+        const uint32_t hi = hx_wave_max_u32((uint32_t)(b >> 32));
+        const uint32_t lo = hx_wave_max_u32((uint32_t)(b >> 32) == hi ? (uint32_t)b : 0u);
+        const uint64_t best = ((uint64_t)hi << 32) | lo;
+        const uint64_t owner = __ballot(b == best);
+        const float best_a = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ba), (int)__ffsll((unsigned long long)owner) - 1));
+        const int e = (int)(0xfffffu + 1u - lo);
 #pragma unroll
         for (int i = 0; i < PER; ++i)
             if (cand[i] == best) cand[i] = 0;
