@@ -384,18 +384,43 @@ __device__ __forceinline__ void build_plan(const MoeDecodeArgs& a, DecodePlan& p
             const int i = lane;
             const int ei = i < R ? (a.T == 1 ? e1 : sel_e[i]) : 0x7fffffff;
             const float wi = a.T == 1 ? w1 : (i < R ? sel_w[i] : 0.0f);
-            int less = 0, eqb = 0, cnt = 0;
-            for (int j = 0; j < R; ++j) {
-                const int ej = __builtin_amdgcn_readlane(ei, j);
-                less += ej < ei;
-                eqb += (ej == ei) && (j < i);
-                cnt += ej == ei;
+            int less = 0, eqb = 0, cnt = 0, dless = 0, n = 0;
+            if (a.T == 1) {
+                // one token: its selections are distinct experts, so a selection's rank is the
+                // number of selected experts below it, read from a bitmap of the selection in LDS
+                // (a few independent instructions instead of two loops of R dependent readlanes)
+                __shared__ __align__(16) uint32_t sel_bits[16];  // E <= 512
+                if (lane < 16) sel_bits[lane] = 0u;
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                if (i < R) __hip_atomic_fetch_or(&sel_bits[ei >> 5], 1u << (ei & 31), __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_WAVEFRONT);
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                if (i < R) {
+                    const int wd = ei >> 5;
+                    const uint32_t below = (1u << (ei & 31)) - 1u;
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) {
+                        const uint32_t m = sel_bits[q];
+                        less += __builtin_popcount(q < wd ? m : (q == wd ? (m & below) : 0u));
+                    }
+                }
+                dless = less;
+                cnt = 1;
+                n = R;
+            } else {
+                for (int j = 0; j < R; ++j) {
+                    const int ej = __builtin_amdgcn_readlane(ei, j);
+                    less += ej < ei;
+                    eqb += (ej == ei) && (j < i);
+                    cnt += ej == ei;
+                }
+                const uint64_t fm = __ballot(i < R && eqb == 0);  // first selection of each expert
+                for (int j = 0; j < R; ++j)                        // distinct experts below ei
+                    if ((fm >> j) & 1) dless += __builtin_amdgcn_readlane(ei, j) < ei;
+                n = __popcll(fm);
             }
-            const uint64_t fm = __ballot(i < R && eqb == 0);  // first selection of each expert
-            int dless = 0;                                     // distinct experts below ei
-            for (int j = 0; j < R; ++j)
-                if ((fm >> j) & 1) dless += __builtin_amdgcn_readlane(ei, j) < ei;
-            const int n = __popcll(fm);
             if (i < R) {
                 const int pos = less + eqb;
                 p.token[pos] = i / a.topk;
