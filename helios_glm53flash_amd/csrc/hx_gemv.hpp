@@ -26,9 +26,10 @@ namespace hx {
 // Tile-word steps in flight per wave in the dense linear, up to 4 bits / wider.  Fewer steps in
 // flight shorten the memory queue that every workgroup's dependent loads (inputs, partial sums,
 // arrival counters) wait behind: config 2 (4096 -> 12288, 4-bit) at M = 1 measured 15.6 us with
-// 8 steps, 13.9 with 4, 13.4 with 2; the 5-bit lm_head is flat between 2 and 4.
+// 8 steps, 13.9 with 4, 13.4 with 2; the 5-bit lm_head (stream-K, row steps) 96.7-98.3 us with 2,
+// 98.0-98.7 with 3, 99.1-99.5 with 4, 122 with 6 (one box, three runs each).
 constexpr int LIN_PF = 2;   // up to 4 bits
-constexpr int LIN_PFW = 4;  // wider
+constexpr int LIN_PFW = 2;  // wider
 
 // Stream-K for one row over more than 1024 column groups that do not spread evenly over the 256 CUs
 // (the lm_head, 4096 -> 151552: 1184 groups; one workgroup per group put 4 or 5 on a CU, and the CUs
