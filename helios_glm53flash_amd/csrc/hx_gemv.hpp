@@ -471,13 +471,6 @@ __device__ __forceinline__ float* gemv_lds()
     return buf;
 }
 
-// 16 zero halves in LDS (the row-step A operand outside the diagonal).
-__device__ __forceinline__ uint32_t* gemv_zero_lds()
-{
-    __shared__ __align__(16) uint32_t z[8];
-    return z;
-}
-
 // This workgroup's partial sum of the GEMV over k in [k0, k0 + kc) (kc a multiple of 128): on
 // return colsum[m][c] (LDS fp32, MT x 128) holds sum over that range of a[m][k] * W[k][cg*128 + c].
 // a_lds must hold MT * kc fp16.  MT <= 16.
@@ -563,12 +556,6 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     if (g.pre_transformed) input_issue(in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, true);
     if (MF_IN && !g.pre_transformed) input_mfma(a_lds, g.x, g.rows, g.suh, g.M, g.K, k0, kc);
     else input_finish(a_lds, in, g.x, g.rows, g.suh, g.M, g.K, k0, kc, g.pre_transformed);
-    // row steps: the A rows of the lanes outside the diagonal read zeros (16 halves)
-    uint32_t* zrow = nullptr;
-    if constexpr (ROW) {
-        zrow = gemv_zero_lds();
-        if (threadIdx.x < 8) zrow[threadIdx.x] = 0u;
-    }
     hx_lds_barrier();
     after_input();
     if constexpr (AFFINE) {
@@ -584,10 +571,11 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
 
     hx_f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
     const int am = min(lane & 15, g.M - 1);  // A row of this lane (rows >= M repeat the last row)
+    // row steps: only the lanes on the A diagonal read the input; the others keep zero operands
+    // (their reads of a zero block moved 1 KB through LDS per instruction for 64 bytes of input)
     const bool diag = (lane & 15) == (lane >> 4);
-    const _Float16* arow = ROW && !diag ? reinterpret_cast<const _Float16*>(zrow)
-                                        : reinterpret_cast<const _Float16*>(a_lds) + (size_t)am * kc;
-    const int kmask = ROW && !diag ? 0 : -1;
+    const _Float16* arow = reinterpret_cast<const _Float16*>(a_lds) + (size_t)am * kc;
+    hx_h8 a0 = {}, a1 = {};
     // one group of PF steps; GUARD: the group runs past the range (only the last group can)
     auto group = [&](int st0, auto guard) {
         constexpr bool GUARD = decltype(guard)::value;
@@ -615,9 +603,11 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
             }
             load_quarter_buf<BITS>(buf[j], rs, voff, soff(st + PF));
             if (live) {
-                const int kl = (step_k(st) + 16 * gq) & kmask;
-                const hx_h8 a0 = *reinterpret_cast<const hx_h8*>(arow + kl);
-                const hx_h8 a1 = *reinterpret_cast<const hx_h8*>(arow + kl + 8);
+                const int kl = step_k(st) + 16 * gq;
+                if (!ROW || diag) {
+                    a0 = *reinterpret_cast<const hx_h8*>(arow + kl);
+                    a1 = *reinterpret_cast<const hx_h8*>(arow + kl + 8);
+                }
                 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, quarter_operand<0, 0>(d), acc0, 0, 0, 0);
                 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, quarter_operand<0, 1>(d), acc0, 0, 0, 0);
                 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, quarter_operand<1, 0>(d), acc1, 0, 0, 0);
