@@ -570,10 +570,14 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
     }
 
     hx_f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    const int am = min(lane & 15, g.M - 1);  // A row of this lane (rows >= M repeat the last row)
-    // row steps: only the lanes on the A diagonal read the input; the others keep zero operands
-    // (their reads of a zero block moved 1 KB through LDS per instruction for 64 bytes of input)
+    const int am = min(lane & 15, g.M - 1);  // A row of this lane
+    // Only the lanes whose A row carries input read it from LDS; the others keep zero operands, so
+    // a read moves 16 bytes per input row and k group instead of 1 KB per wave: with row steps the
+    // lanes on the A diagonal, else (MT > 1) the lanes of rows < M (rows >= M of the product are not
+    // used).  With MT = 1 and 4-row steps (the MoE decode layer's one-token units) every lane reads:
+    // the read's exec-mask branch in each step made that layer slower (47.0 against 46.0-46.5 us).
     const bool diag = (lane & 15) == (lane >> 4);
+    const bool a_reads = ROW ? diag : (MT == 1 || (lane & 15) < g.M);
     const _Float16* arow = reinterpret_cast<const _Float16*>(a_lds) + (size_t)am * kc;
     hx_h8 a0 = {}, a1 = {};
     // one group of PF steps; GUARD: the group runs past the range (only the last group can)
@@ -604,7 +608,7 @@ __device__ __forceinline__ void gemv_range(const GemvArgs& g, int cg, int k0, in
             load_quarter_buf<BITS>(buf[j], rs, voff, soff(st + PF));
             if (live) {
                 const int kl = step_k(st) + 16 * gq;
-                if (!ROW || diag) {
+                if (a_reads) {
                     a0 = *reinterpret_cast<const hx_h8*>(arow + kl);
                     a1 = *reinterpret_cast<const hx_h8*>(arow + kl + 8);
                 }
