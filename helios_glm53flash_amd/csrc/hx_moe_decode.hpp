@@ -528,18 +528,14 @@ HX_INLINE int proj_bits(const MoeDecodeArgs& a, int proj, int expert)
 // guad epilogue for rows m < count of one 128-column group (hadamard_inner.cuh:284-413 for routed
 // experts; swiglu_clamp + down-input transform for the shared expert, runner.cpp:723-738).
 template <int MT>
+// sg, su, sd: this lane's pairs (columns cg*128 + 2*lane, +1) of svh_gate, svh_up and suh_down.
 __device__ __forceinline__ void guad_epilogue(const MoeDecodeArgs& a, const DecodePlan& p, const SlotInfo& si, int slot,
-                                              int cg, const float* cs_g, const float* cs_u)
+                                              int cg, const float* cs_g, const float* cs_u, hx_h2 sg, hx_h2 su,
+                                              hx_h2 sd)
 {
     const int wave = hx_vwave(), lane = threadIdx.x & 63;
     const int c = cg * 128 + 2 * lane;
     const bool shared = si.expert < 0;
-    // (the gate's svh of a non-gated expert need not exist)
-    const hx_h2 sg = shared || a.act_fn != HX_ACT_RELU2_NOGATE
-                         ? *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(p.tab.ep[0]) + c)
-                         : hx_h2{(_Float16)0.0f, (_Float16)0.0f};
-    const hx_h2 su = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(p.tab.ep[1]) + c);
-    const hx_h2 sd = *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(p.tab.ep[2]) + c);
     const float L = a.act_limit;
     for (int m = wave; m < si.count && m < MT; m += hx_nwaves()) {
         hx_h2 p;
@@ -761,11 +757,43 @@ __device__ __forceinline__ void gu_finish(const MoeDecodeArgs& a, const DecodePl
     const long cgate = c - proj * gg, cup = cgate + gg;
     const int ng = sp.count(cgate), nu = sp.count(cup);
     if (!arrive_last(&a.counter_gu[slot * gg + cg], ng + nu)) return;
-    float* pg = a.partial_g + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
-    float* pu = a.partial_u + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
-    if (gated) gather_partials<MT>(pg, si.count, 128, ng, 0, cs_g);
-    gather_partials<MT>(pu, si.count, 128, nu, 0, cs_u);
-    guad_epilogue<MT>(a, plan, si, slot, cg, cs_g, cs_u);
+    // the epilogue's scale pairs and both projections' partial sums in one round trip: the scale
+    // loads go first, the gate and up sums are gathered side by side (with one row, threads 0-127
+    // take the gate's columns and 128-255 the up's); the gate's svh of a non-gated expert need not
+    // exist
+    const int lane = threadIdx.x & 63;
+    const int col = cg * 128 + 2 * lane;
+    auto ep = [&](int q) { return *reinterpret_cast<const hx_h2*>(static_cast<const _Float16*>(plan.tab.ep[q]) + col); };
+    const hx_h2 sg = si.expert < 0 || a.act_fn != HX_ACT_RELU2_NOGATE ? ep(0) : hx_h2{(_Float16)0.0f, (_Float16)0.0f};
+    const hx_h2 su = ep(1), sd = ep(2);
+    const float* pg = a.partial_g + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
+    const float* pu = a.partial_u + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
+    for (int i = threadIdx.x; i < 2 * MT * 128; i += hx_nthreads()) {
+        const bool up = i >= MT * 128;
+        const int k = up ? i - MT * 128 : i, m = k >> 7;
+        const int n = up ? nu : ng;
+        float v = 0.0f;
+        if (m < si.count && (up || gated)) {
+            // segment s, row m of the partial sums: (s * rows + m) * 128 + column; 8 segments' loads
+            // together, added in segment order
+            const float* p = (up ? pu : pg) + (size_t)m * 128 + (k & 127);
+            const size_t stride = (size_t)si.count * 128;
+            constexpr int B = 8;
+            for (int s0 = 0; s0 < n; s0 += B) {
+                float t[B];
+#pragma unroll
+                for (int j = 0; j < B; ++j)
+                    t[j] = __hip_atomic_load(p + (size_t)min(s0 + j, n - 1) * stride, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int j = 0; j < B; ++j)
+                    if (s0 + j < n) v += t[j];
+            }
+        }
+        (up ? cs_u : cs_g)[k] = v;
+    }
+    __syncthreads();
+    guad_epilogue<MT>(a, plan, si, slot, cg, cs_g, cs_u, sg, su, sd);
     // the activations of this block are stored (device-coherent): flag them for the down phase
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
