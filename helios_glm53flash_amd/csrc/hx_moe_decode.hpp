@@ -684,13 +684,17 @@ __device__ __forceinline__ void combine_columns(const MoeDecodeArgs& a, const De
 constexpr int DEC_PF = 5;
 constexpr int DEC_THREADS = 256;
 
-// Bounded wait of thread 0 for *flag >= target (the producers are resident workgroups that do not
-// wait for anything themselves, so the wait ends; the bound only turns a bug into a flagged wrong
-// result instead of a hung device).
-HX_INLINE void wait_flag(const int* flag, int target, int* status)
+// Bounded wait of one wave for flags[i] >= target, i < n <= 64: lane i polls flag i and the wave
+// goes on once all are set (polled one after another, the flags cost one dependent round trip each
+// even when all were already set, as they are for the down units that start late).  The producers
+// are resident workgroups that do not wait for anything themselves, so the wait ends; the bound
+// only turns a bug into a flagged wrong result instead of a hung device.
+HX_INLINE void wait_flags(const int* flags, int n, int target, int* status)
 {
+    const int lane = threadIdx.x & 63;
     int spins = 0;
-    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+    while (__ballot(lane < n && __hip_atomic_load(&flags[min(lane, n - 1)], __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT) < target) != 0) {
         // back off: device-coherent loads of a few flags from a thousand workgroups all go to the
         // memory channels of those flags, which the weight streams go through too
         if (spins < 4) __builtin_amdgcn_s_sleep(4);
@@ -700,7 +704,7 @@ HX_INLINE void wait_flag(const int* flag, int target, int* status)
             (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & DEC_STATUS_TIMEOUT))
             break;  // another wait already gave up: do not add its bound to every later wait
         if (spins > (1 << 22)) {
-            __hip_atomic_fetch_or(status, DEC_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0) __hip_atomic_fetch_or(status, DEC_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
     }
@@ -851,8 +855,7 @@ __device__ __forceinline__ void d_segment(const MoeDecodeArgs& a, const DecodePl
     g.pre_transformed = true;
     // the input blocks kb0..kb1-1 of this slot are the guad outputs of gate/up column groups kb0..kb1-1
     auto wait_inputs = [&]() {
-        if (hx_vtid() == 0)
-            for (int kb = kb0; kb < kb1; ++kb) wait_flag(&a.ready[slot * gg + kb], 1, a.status);
+        if (hx_vwave() == 0) wait_flags(&a.ready[slot * gg + kb0], kb1 - kb0, 1, a.status);
         hx_lds_barrier();
     };
     gemv_range<BITS, CB, MT, 1, DEC_PF>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs, wait_inputs);
