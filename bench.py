@@ -50,7 +50,9 @@ def bench_decode(args, torch, moe, lib):
     nsteps = args.warmup + args.steps
     g = torch.Generator(device="cuda")
     g.manual_seed(7)
-    scores = torch.randn((nsteps, 1, E), generator=g, device="cuda").to(torch.float16)
+    # one score row per step, and at least one per rotating layer (the graph below holds one step of each)
+    nrows = max(nsteps, L)
+    scores = torch.randn((nrows, 1, E), generator=g, device="cuda").to(torch.float16)
     x = torch.randn((1, hidden), generator=g, device="cuda").to(torch.float16)
     y = torch.empty((1, hidden), dtype=torch.float16, device="cuda")
     ws = torch.zeros(layers[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
@@ -60,7 +62,7 @@ def bench_decode(args, torch, moe, lib):
     # every rotating layer runs at least once before the timed loop (its first call builds its
     # expert pointer tables on the device)
     for i in range(max(args.warmup, L)):
-        layers[i % L](x, scores[i % nsteps], y=y, ws=ws)
+        layers[i % L](x, scores[i % nrows], y=y, ws=ws)
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
