@@ -680,8 +680,12 @@ __device__ __forceinline__ void combine_columns(const MoeDecodeArgs& a, const De
 // Since a step loads only the quarter's own words (one load per lane at 2 bits, the wrapped word
 // comes from the neighbouring lane), 5 steps are best: 45.9-46.0 us against 46.4-46.5 us with 4 and
 // 3, 46.3-46.5 us with 6 (one box, two runs each).
+// Since the down units poll their flags at once and the gate/up finisher gathers in one round trip,
+// the gate/up units gain from one step more: 6 steps 43.86-43.95 us, 7 steps 43.82-44.08 us, 5 steps
+// 44.13-44.33 us (one box, four runs each); the down units keep 5 (8: slower, 3: no change).
 // (The linear GEMV keeps its own ring depth: it streams alone.)
 constexpr int DEC_PF = 5;
+constexpr int DEC_PF_GU = 6;
 constexpr int DEC_THREADS = 256;
 
 // Bounded wait of one wave for flags[i] >= target, i < n <= 64: lane i polls flag i and the wave
@@ -827,7 +831,7 @@ __device__ __forceinline__ void gu_segment(const MoeDecodeArgs& a, const DecodeP
     g.K = a.hidden;
     g.N = a.inter;
     g.pre_transformed = false;
-    gemv_range<BITS, CB, MT, 1, DEC_PF>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
+    gemv_range<BITS, CB, MT, 1, DEC_PF_GU>(g, cg, kb0 * 128, (kb1 - kb0) * 128, a_lds, cs_g);
 
     // partial of segment i of (slot, proj, cg): partial_{g,u}[((slot*gg + cg) * (KB + 1) + i) * 8 + m][128]
     float* pbase = (proj == 0 ? a.partial_g : a.partial_u) + (size_t)(slot * gg + cg) * (KB + 1) * 8 * 128;
