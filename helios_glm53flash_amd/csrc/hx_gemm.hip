@@ -56,7 +56,7 @@ __device__ void linear_tile_epilogue(const Smem& sm, int half, int rows, const _
 // Quarter-operand tile (each wave decodes its own 32 columns into MFMA B operands; only A is staged
 // in LDS), three workgroups per CU.
 template <int BITS, int CB>
-__global__ __launch_bounds__(MF_THREADS, QT_OCC) void linear_mfma_kernel(const _Float16* a, const uint32_t* trellis,
+__global__ __launch_bounds__(MF_THREADS, qt_occ<CB>()) void linear_mfma_kernel(const _Float16* a, const uint32_t* trellis,
                                                                 const _Float16* svh, void* y, int M, int K, int N,
                                                                 bool y_fp32)
 {

@@ -80,8 +80,14 @@ constexpr int QT_PT = 2;
 // The next chunk's decode runs after the chunk's MFMAs.  (Slicing it between the row blocks' MFMAs,
 // so that one wave overlaps its own VALU and matrix work, measured equal on the config-4 prefill:
 // 3.14 ms either way; the co-resident waves of a SIMD already overlap the two.)
-// workgroups per CU the MFMA-tile kernels are compiled for (their register budget)
+// workgroups per CU the MFMA-tile kernels are compiled for (their register budget, 512 / QT_OCC
+// VGPRs): codebook 2 (the affine decode) fits 168 at 3.  The generic decode of codebooks 0 and 1
+// needs a few more registers, and at 3 the allocator spilled the accumulators themselves to scratch
+// inside the chunk loop (dense linear 31-53 VGPRs, grouped gate/up 1573): the config-4 prefill with
+// MCG experts ran 6.45 ms against 2.91 ms with mul1.  Those codebooks are compiled for 2.
 constexpr int QT_OCC = 3;
+template <int CB>
+constexpr int qt_occ() { return CB == 2 ? QT_OCC : 2; }
 // LDS A buffers: with A loaded straight into LDS, the chunks in flight and the one being read
 constexpr int QT_NB = QT_PF + 1;
 // s_waitcnt immediate that waits until at most n vector-memory instructions are outstanding

@@ -247,7 +247,7 @@ HX_INLINE bool grouped_tile_index(int njobs, int& bx, int& job)
 }
 
 template <int CB>
-__global__ __launch_bounds__(MF_THREADS, QT_OCC) void grouped_gemm_kernel(GroupedGemmArgs g)
+__global__ __launch_bounds__(MF_THREADS, qt_occ<CB>()) void grouped_gemm_kernel(GroupedGemmArgs g)
 {
     __shared__ MfmaSmemQ sm;
     int bx, job_i;
@@ -444,7 +444,7 @@ __device__ __forceinline__ void gu_fused(const GuArgs& a, const Job& job, int cg
 }
 
 template <int CB>
-__global__ __launch_bounds__(MF_THREADS, QT_OCC) void grouped_gu_kernel(GuArgs a)
+__global__ __launch_bounds__(MF_THREADS, qt_occ<CB>()) void grouped_gu_kernel(GuArgs a)
 {
     __shared__ GuSmem sm;
     int cg, job_i;
