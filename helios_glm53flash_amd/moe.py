@@ -143,9 +143,15 @@ class MoeLayer:
     """One MoE FFN layer (routed experts + optional shared expert), resident in HBM."""
 
     def __init__(self, experts: ExpertSet, shared: Optional[list] = None, topk: int = 8,
-                 routed_scale: float = 2.5, act_limit: float = 10.0, router_weight: Optional[torch.Tensor] = None):
+                 routed_scale: float = 2.5, act_limit: float = 10.0, router_weight: Optional[torch.Tensor] = None,
+                 mcg: bool = False):
         """router_weight: optional router gate fp16 [E][hidden]; with it the layer may be called with
-        scores=None and computes the logits itself (gemm_nt_f16, stream-ordered, no host sync)."""
+        scores=None and computes the logits itself (gemm_nt_f16, stream-ordered, no host sync).
+        mcg: the experts (routed and shared) use the MCG codebook (the reference layer's mcg flag;
+        experts.mul1 must then be False).  A layer is MCG or mul1, never the 3INST codebook."""
+        if mcg and experts.mul1:
+            raise ValueError("MoeLayer: mcg=True needs experts built with mul1=False")
+        self.mcg = mcg
         self.router_weight = router_weight
         self.experts = experts
         self.shared = shared
@@ -183,7 +189,8 @@ class MoeLayer:
                                self._shared_c if self._shared_c is not None else None,
                                self._shared_bits if self._shared_bits is not None else None,
                                T, ex.hidden, ex.inter, ex.num_experts, self.topk, ub[0], ub[1], ub[2],
-                               self.routed_scale, self.act_limit, 0, int(ex.mul1), ws.data_ptr(), ws.numel(),
+                               self.routed_scale, self.act_limit, int(self.mcg), int(ex.mul1 and not self.mcg),
+                               ws.data_ptr(), ws.numel(),
                                _stream(stream)), "hx_moe_layer")
         return y
 

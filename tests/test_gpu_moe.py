@@ -70,6 +70,31 @@ def test_moe_decode_small(hx, T):
     _run_layer(hx, E=16, hidden=512, inter=256, topk=4, T=T, bits=2, shared_bits=2, seed=10 + T)
 
 
+@pytest.mark.parametrize("T", [1, 24])
+def test_moe_layer_mcg(hx, T):
+    """MCG-codebook experts through MoeLayer(mcg=True), gate/up/down at 2/3/4 bits: the one-token
+    decode kernel (T = 1) and the grouped prefill path (T = 24, 96 routed rows), against the oracle's
+    layer with codebook 1."""
+    import torch
+    from oracle import oracle as O
+    exl3, moe = hx
+    E, hidden, inter, topk = 16, 512, 256, 4
+    ex = moe.ExpertSet.synthetic(E, hidden, inter, (2, 3, 4), seed=900 + T, mul1=False)
+    with pytest.raises(ValueError):
+        moe.MoeLayer(moe.ExpertSet.synthetic(E, hidden, inter, 2, seed=1), None, topk=topk, mcg=True)
+    layer = moe.MoeLayer(ex, None, topk=topk, mcg=True)
+    r = np.random.default_rng(901 + T)
+    x = r.standard_normal((T, hidden)).astype(np.float16)
+    scores = r.standard_normal((T, E)).astype(np.float16)
+    y_routed = torch.empty((T, hidden), dtype=torch.float32, device="cuda")
+    layer(torch.from_numpy(x).cuda(), torch.from_numpy(scores).cuda(), y_routed=y_routed)
+    torch.cuda.synchronize()
+    idx, w = O.routing(scores, topk, 2.5)
+    used = set(int(e) for e in idx.reshape(-1))
+    yr_ref, _ = O.moe_rows(x, hidden, inter, idx, w, np.arange(T), _oracle_experts(ex, used), None, 10.0, cb=1)
+    assert_close(y_routed.cpu().numpy(), yr_ref, what=f"mcg layer T={T}")
+
+
 @pytest.mark.parametrize("E,T", [(320, 1), (384, 1), (384, 4), (512, 2)])
 def test_moe_decode_many_experts(hx, E, T):
     """Expert counts at and above 320: up to 320 the decode kernel takes every expert's table
