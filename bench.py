@@ -146,8 +146,22 @@ def bench_prefill(args, torch, moe):
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / reps
     flops = 2.0 * T * topk * 3 * hidden * inter
-    del ws
-    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops}
+    del ws, layer, ex
+    # the same workload with MCG-codebook experts (the reference's other MoE codebook)
+    ex = moe.ExpertSet.synthetic(E, hidden, inter, bits, seed=78, mul1=False)
+    layer = moe.MoeLayer(ex, None, topk=topk, mcg=True)
+    ws = torch.zeros(layer.workspace_bytes(T), dtype=torch.uint8, device="cuda")
+    for _ in range(2):
+        layer(x, scores, y=y, ws=ws)
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(reps):
+        layer(x, scores, y=y, ws=ws)
+    t1.record()
+    torch.cuda.synchronize()
+    ms_mcg = t0.elapsed_time(t1) / reps
+    del ws, layer, ex
+    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops, "mcg_ms": ms_mcg}
 
 
 def graph_time_us(torch, fn, reps: int = 20, inner: int = 20) -> float:
@@ -493,6 +507,8 @@ def main():
                              "note": "algorithmic 2*rows*K*N over the routed rows' gate, up and down GEMMs, "
                                      "per layer call (router, permutation, gather and combine included in "
                                      "the time)"},
+                "mcg_ms": round(pre["mcg_ms"], 4),
+                "mcg_note": "the same workload with MCG-codebook experts (mul1 is the headline codebook)",
             },
         },
     }
