@@ -151,6 +151,11 @@ class MoeLayer:
         experts.mul1 must then be False).  A layer is MCG or mul1, never the 3INST codebook."""
         if mcg and experts.mul1:
             raise ValueError("MoeLayer: mcg=True needs experts built with mul1=False")
+        # the layer decodes the shared expert with the routed experts' codebook
+        layer_mul1 = bool(experts.mul1) and not mcg
+        if shared is not None and any(bool(w.mul1) != layer_mul1 for w in shared):
+            raise ValueError("MoeLayer: the shared expert's codebook (GroupWords.mul1) must match the routed "
+                             "experts'")
         self.mcg = mcg
         self.router_weight = router_weight
         self.experts = experts

@@ -85,3 +85,33 @@ def test_cpp_compat_header_compiles_and_links(tmp_path):
                         str(tmp_path / "t"), "-L", str(lib.parent), "-lhx_exl3", f"-Wl,-rpath,{lib.parent}"],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr[-2000:]
+
+
+def test_moe_layer_codebook_checks_without_gpu():
+    """MoeLayer refuses mcg=True over mul1 experts, and a shared expert whose codebook differs from
+    the routed experts' (the layer decodes both with one codebook); host checks only."""
+    import pytest
+    import torch
+    from helios_glm53flash_amd import exl3, moe
+    E, hidden, inter = 2, 128, 128
+
+    def group(K, N, mul1):
+        return exl3.GroupWords(torch.zeros((K // 16, N // 16, 32), dtype=torch.int16),
+                               torch.ones(K, dtype=torch.float16), torch.ones(N, dtype=torch.float16), mul1)
+
+    def experts(mul1):
+        shapes = [(hidden, inter), (hidden, inter), (inter, hidden)]
+        gw = [[group(K, N, 0) for _ in range(E)] for K, N in shapes]
+        return moe.ExpertSet(hidden, inter, [[w.trellis for w in p] for p in gw], [[w.suh for w in p] for p in gw],
+                             [[w.svh for w in p] for p in gw], [[2] * E for _ in range(3)], mul1)
+
+    sh_mul1 = [group(hidden, inter, exl3.MUL1), group(hidden, inter, exl3.MUL1), group(inter, hidden, exl3.MUL1)]
+    sh_mcg = [group(hidden, inter, 0), group(hidden, inter, 0), group(inter, hidden, 0)]
+    moe.MoeLayer(experts(True), sh_mul1, topk=2)
+    moe.MoeLayer(experts(False), sh_mcg, topk=2, mcg=True)
+    with pytest.raises(ValueError):
+        moe.MoeLayer(experts(True), None, topk=2, mcg=True)
+    with pytest.raises(ValueError):
+        moe.MoeLayer(experts(True), sh_mcg, topk=2)
+    with pytest.raises(ValueError):
+        moe.MoeLayer(experts(False), sh_mul1, topk=2, mcg=True)
