@@ -618,6 +618,11 @@ int hx_moe_layer(void* y, float* y_routed, const void* x, const void* scores, co
         for (int i = 0; i < 3; ++i)
             if (!shared[i].trellis || !shared[i].suh || !shared[i].svh || shared_bits[i] < 1 || shared_bits[i] > 8)
                 return fail(HX_ERR_INVALID, "hx_moe_layer: bad shared expert");
+        // the shared expert is decoded with the routed experts' codebook (mcg / mul1)
+        for (int i = 0; i < 3; ++i)
+            if ((shared[i].mul1 != 0) != (mul1 != 0))
+                return fail(HX_ERR_INVALID, "hx_moe_layer: the shared expert's codebook (mul1) differs from the "
+                                            "routed experts'");
         if (act_limit <= 0.0f) return fail(HX_ERR_INVALID, "hx_moe_layer: the shared-expert swiglu needs act_limit > 0");
     }
     hx::MoeWs L;

@@ -257,7 +257,8 @@ int hx_moe_grouped(const void* x, float* y, const int64_t* expert_count, const i
 
 /* A whole MoE FFN layer without host synchronisation: sigmoid top-k over scores (fp16
  * [tokens][E], optional bias), deterministic permutation, routed experts, shared expert (three
- * hx_group_words gate/up/down with bit widths shared_bits[3], or NULL), ordered reduction and
+ * hx_group_words gate/up/down with bit widths shared_bits[3], decoded with the layer's codebook, so
+ * their mul1 must agree with it (HX_ERR_INVALID otherwise), or NULL), ordered reduction and
  * y = fp16(routed + shared) [tokens][hidden_dim]; y_routed (fp32, optional) receives the routed
  * sum.  Replaces the single-GPU part of helios Runner::moe_ffn (src/engine/runner.cpp:711-959:
  * shared expert :723-738, router :759-762, permute :764, moe_grouped + reduce :918-922,

@@ -43,6 +43,13 @@ def test_host_side_validation_without_gpu():
     r = _lib.lib.hx_routing_ds3_nogroup(1, None, 1, 1, 1, 288, 8, 2.5, 1, 2, None)
     assert r == _lib.HX_ERR_UNSUPPORTED
     assert _lib.lib.hx_exl3_gemm_workspace_size(1, 2048, 4096) > 0
+    # a shared expert whose codebook differs from the layer's (mul1 layer, mul1 = 0 shared words)
+    tabs = _lib.ExpertTablesC(*([1] * 9), None, None, None, 0)
+    sh = (_lib.GroupWordsC * 3)(*[_lib.GroupWordsC(1, 1, 1, 0) for _ in range(3)])
+    shb = (ctypes.c_int * 3)(2, 2, 2)
+    r = _lib.lib.hx_moe_layer(1, None, 1, 1, None, ctypes.byref(tabs), sh, shb, 1, 4096, 2048, 288, 8, 2, 2, 2,
+                              2.5, 10.0, 0, 1, None, 0, None)
+    assert r == _lib.HX_ERR_INVALID and b"codebook" in _lib.lib.hx_last_error()
 
 
 def test_cpp_compat_header_compiles_and_links(tmp_path):
