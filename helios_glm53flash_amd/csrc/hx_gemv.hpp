@@ -200,13 +200,25 @@ HX_INLINE void quarter_mul1(const uint32_t* r, uint32_t* x)
     }
 }
 
+// Window of local position P of a quarter: it ends at local bit E = (P+1)*BITS + 32 (MSB first);
+// M[j] = the 32 bits ending at local bit 32j + 16, for windows across words j-1 and j.
+template <int BITS, int P>
+HX_INLINE uint32_t quarter_window(const uint32_t* r, const uint32_t* M)
+{
+    constexpr int E = (P + 1) * BITS + 32;
+    constexpr int j = E >> 5, rr = E & 31;
+    if constexpr (rr == 0) return __builtin_amdgcn_ubfe(r[j - 1], 0, 16);
+    else if constexpr (rr >= 16) return __builtin_amdgcn_ubfe(r[j], 32 - rr, 16);
+    else return __builtin_amdgcn_ubfe(M[j], 16 - rr, 16);
+}
+
+// Codebooks 0 and 1: each pair from its two windows (one v_bfe_u32 each, as in the affine decode).
 template <int BITS, int CB, int P = 0>
-HX_INLINE void quarter_decode_generic(const uint32_t* r, uint32_t* out)
+HX_INLINE void quarter_decode_generic(const uint32_t* r, const uint32_t* M, uint32_t* out)
 {
     if constexpr (P < 32) {
-        out[qpos(P / 2)] = h2_as_u32(hx_decode2<CB>(quarter_reg<(P + 1) * BITS + 32>(r) & 0xffffu,
-                                              quarter_reg<(P + 2) * BITS + 32>(r) & 0xffffu));
-        quarter_decode_generic<BITS, CB, P + 2>(r, out);
+        out[qpos(P / 2)] = h2_as_u32(hx_decode2<CB>(quarter_window<BITS, P>(r, M), quarter_window<BITS, P + 1>(r, M)));
+        quarter_decode_generic<BITS, CB, P + 2>(r, M, out);
     }
 }
 
@@ -242,7 +254,10 @@ HX_INLINE void quarter_decode(const uint32_t* r, uint32_t* out)
             mul1_dec4(xs, out[4 * o], out[4 * o + 1], out[4 * o + 2], out[4 * o + 3]);
         }
     } else {
-        quarter_decode_generic<BITS, CB>(r, out);
+        uint32_t M[BITS + 1];
+#pragma unroll
+        for (int j = 1; j <= BITS; ++j) M[j] = __builtin_amdgcn_alignbit(r[j - 1], r[j], 16);
+        quarter_decode_generic<BITS, CB>(r, M, out);
     }
 }
 
@@ -257,18 +272,6 @@ HX_INLINE void quarter_decode(const uint32_t* r, uint32_t* out)
 // and a pair of products one v_sad_u8 + one v_sad_hi_u8, which leave h as packed fp16 directly.
 constexpr float CB2_SCALE = 0.00676727294921875f;  // fp16 0x1eee
 constexpr float CB2_BIAS = -10.3828125f;           // fp16 0xc931
-
-// Window of local position P of a quarter: it ends at local bit E = (P+1)*BITS + 32 (MSB first);
-// M[j] = the 32 bits ending at local bit 32j + 16, for windows across words j-1 and j.
-template <int BITS, int P>
-HX_INLINE uint32_t quarter_window(const uint32_t* r, const uint32_t* M)
-{
-    constexpr int E = (P + 1) * BITS + 32;
-    constexpr int j = E >> 5, rr = E & 31;
-    if constexpr (rr == 0) return __builtin_amdgcn_ubfe(r[j - 1], 0, 16);
-    else if constexpr (rr >= 16) return __builtin_amdgcn_ubfe(r[j], 32 - rr, 16);
-    else return __builtin_amdgcn_ubfe(M[j], 16 - rr, 16);
-}
 
 template <int BITS, int P = 0>
 HX_INLINE void quarter_affine_pairs(const uint32_t* r, const uint32_t* M, uint32_t* out)
